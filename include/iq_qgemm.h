@@ -1,0 +1,138 @@
+/*
+ * iq_qgemm.h -- C ABI of the MI355X (gfx950) quantised-matmul library.
+ *
+ * This is the drop-in boundary for inferq's quantised-matmul hot path.  A
+ * thin FFI crate binds these symbols so that the reference's matrix-level
+ * entry points run on the GPU instead of the AVX2 kernels.  Each entry point
+ * cites the reference interface it replaces (paths relative to the
+ * reference root).
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  Matrices are GGUF blocks in their
+ *     native on-disk layout, row-major, rows * (cols / block_elems) blocks.
+ *   - "device" pointers are HBM addresses on the current device; "host"
+ *     pointers are ordinary process memory.
+ *   - Every function returns IQ_OK (0) or a negative IQ_ERR_* code;
+ *     iq_last_error() returns this thread's message for the last failure.
+ *   - Results are deterministic and bit-identical to the reference's CPU
+ *     kernels for the same inputs, whatever the row count.
+ *   - stream is a hipStream_t (NULL = the default stream).
+ */
+#ifndef IQ_QGEMM_H
+#define IQ_QGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids as carried by GGUF (the reference's GgmlDType). */
+enum iq_dtype { IQ_Q8_0 = 8, IQ_Q4_K = 12, IQ_Q6_K = 14 };
+
+enum iq_status {
+    IQ_OK = 0,
+    IQ_ERR_INVALID = -1, /* null handle / pointer, bad argument */
+    IQ_ERR_SHAPE = -2,   /* width not a whole number of blocks, wrong input width, size mismatch */
+    IQ_ERR_DTYPE = -3,   /* dtype outside {Q8_0, Q4_K, Q6_K}, or mismatched dtypes */
+    IQ_ERR_OOM = -4,     /* device allocation failed */
+    IQ_ERR_HIP = -5,     /* HIP runtime error (launch, copy, no device) */
+    IQ_ERR_RANGE = -6    /* index out of range (expert, rows) */
+};
+
+typedef struct iq_weight *iq_weight_t;
+typedef struct iq_moe *iq_moe_t;
+typedef void *iq_stream_t;
+
+/* Library version string. */
+const char *iq_version(void);
+
+/* Thread-local message of the last failing call on this thread. */
+const char *iq_last_error(void);
+
+/* Select `device` for this thread and check it is a gfx950 GPU.
+ * Replaces: threading::init / require_exact_kernels, the reference's
+ * start-up capability gate (src/gguf.rs:1043-1053, src/threading.rs:35-55). */
+int iq_init(int device);
+
+/* ---- Weights resident in HBM, native GGUF block layout ---------------- */
+
+/* Copy `nbytes` of host GGUF block bytes for a [rows x cols] matrix to HBM.
+ * Replaces: GgufCheckpoint::load_matrix / QuantizedMatrix::new
+ * (src/gguf.rs:1234, :297-320) -- the storage an executable matrix owns. */
+int iq_weights_upload(const void *host_bytes, size_t nbytes, int dtype, int64_t rows, int64_t cols,
+                      iq_weight_t *out);
+
+/* Wrap block bytes already in HBM (not copied, not freed by the library);
+ * `device_bytes` must be 16-byte aligned.  Used for slices of resident
+ * expert tensors [experts, rows, cols].
+ * Replaces: GgufExpertTensor::load (src/gguf.rs:1276-1319, :1404-1458). */
+int iq_weights_view(const void *device_bytes, size_t nbytes, int dtype, int64_t rows, int64_t cols,
+                    iq_weight_t *out);
+
+/* Release a handle (and the HBM it owns, for uploads and derived matrices). */
+int iq_weights_free(iq_weight_t w);
+
+/* dtype, shape, storage bytes and HBM address of a matrix.
+ * Replaces: QuantizedMatrix::{dtype, shape, storage_bytes} (src/gguf.rs:322-332). */
+int iq_weights_info(iq_weight_t w, int *dtype, int64_t *rows, int64_t *cols, size_t *nbytes,
+                    const void **device_bytes);
+
+/* Row concatenation: a's rows then b's rows, byte-identical.
+ * Replaces: QuantizedMatrix::concatenate_rows (src/gguf.rs:379-404). */
+int iq_weights_concat_rows(iq_weight_t a, iq_weight_t b, iq_weight_t *out);
+
+/* The first `rows` output rows as a new matrix (a contiguous byte prefix).
+ * Replaces: QuantizedMatrix::leading_rows (src/gguf.rs:352-377). */
+int iq_weights_leading_rows(iq_weight_t a, int64_t rows, iq_weight_t *out);
+
+/* ---- Products ---------------------------------------------------------- */
+
+/* y[m x rows] = x[m x cols] . W^T for device f32 x and y (row-major).  The
+ * input rows are quantised on the GPU exactly as the reference's
+ * from_float does (Q8K for K-quants, Q8_0 for Q8_0) and the product follows
+ * the reference's per-lane f32 order, for any m >= 1.  Uses a library
+ * workspace on the device: calls on one device must not overlap (use
+ * iq_matmul_ws with distinct workspaces for concurrent streams).
+ * Replaces: QuantizedMatrix::forward / forward_spread / forward_rows /
+ * multi_row_forward / fused_forward (src/gguf.rs:406-456, :558-690) and the
+ * per-row kernels q4k_q8k_row / q6k_q8k_row / q80_q80_row they call
+ * (src/qgemm.rs:447-468). */
+int iq_matmul(iq_weight_t w, const float *x, int64_t m, float *y, iq_stream_t stream);
+
+/* Device workspace bytes iq_matmul_ws needs for m input rows of W. */
+size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m);
+
+/* iq_matmul with a caller-provided device workspace (>= the size above). */
+int iq_matmul_ws(iq_weight_t w, const float *x, int64_t m, float *y, void *workspace, size_t workspace_bytes,
+                 iq_stream_t stream);
+
+/* iq_matmul for host x and y (copies in, computes, copies out, synchronises).
+ * Replaces: the same entries, for a caller holding host slices
+ * (QuantizedMatrix::forward_rows, src/gguf.rs:433-456). */
+int iq_matmul_host(iq_weight_t w, const float *x_host, int64_t m, float *y_host);
+
+/* ---- Parity hooks ------------------------------------------------------- */
+
+/* Quantise device x[m x k] into the reference block layouts on the device:
+ * Q8K blocks (292 B: f32 d, 256 i8, 16 i16 bsums) or Q8_0 blocks (34 B).
+ * Replaces: candle BlockQ8K::from_float / BlockQ8_0::from_float as called
+ * at src/gguf.rs:648-654. */
+int iq_quantize_q8k(const float *x, int64_t m, int64_t k, void *blocks_out, iq_stream_t stream);
+int iq_quantize_q80(const float *x, int64_t m, int64_t k, void *blocks_out, iq_stream_t stream);
+
+/* Per-block lane integers of y = x . W^T (device buffers): isum is
+ * [m][rows][blocks][8] (the eight i32 lanes of the reference's `sumi` per
+ * block; for Q8_0 the `dot` lanes), msum is [m][rows][blocks][4] (the Q4_K
+ * mins `prod` lanes; ignored otherwise, may be NULL).  y receives the
+ * product as iq_matmul.
+ * Replaces: the intermediate integers of q4k_tile / q6k_tile / q80_tile
+ * (src/qgemm.rs:204-237, :266-330, :384-390). */
+int iq_block_sums(iq_weight_t w, const float *x, int64_t m, float *y, int32_t *isum, int32_t *msum,
+                  iq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,86 @@
+"""ctypes binding of libiq_qgemm.so (the C ABI in include/iq_qgemm.h).
+
+There is no fallback: if the library is missing or fails to load, every
+entry point raises.  Build it with `python -m inferq_amd._build`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libiq_qgemm.so")
+
+IQ_Q8_0, IQ_Q4_K, IQ_Q6_K = 8, 12, 14
+IQ_OK = 0
+IQ_ERR_INVALID, IQ_ERR_SHAPE, IQ_ERR_DTYPE, IQ_ERR_OOM, IQ_ERR_HIP, IQ_ERR_RANGE = -1, -2, -3, -4, -5, -6
+STATUS_NAMES = {
+    IQ_ERR_INVALID: "IQ_ERR_INVALID", IQ_ERR_SHAPE: "IQ_ERR_SHAPE", IQ_ERR_DTYPE: "IQ_ERR_DTYPE",
+    IQ_ERR_OOM: "IQ_ERR_OOM", IQ_ERR_HIP: "IQ_ERR_HIP", IQ_ERR_RANGE: "IQ_ERR_RANGE",
+}
+
+
+class QgemmError(RuntimeError):
+    """A C-ABI call returned an error status; `status` holds the code."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{message} [{STATUS_NAMES.get(status, status)}]")
+        self.status = status
+
+
+_lib = None
+
+P, I64, SZ, INT = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t, ctypes.c_int
+_SIGNATURES = {
+    "iq_version": ([], ctypes.c_char_p),
+    "iq_last_error": ([], ctypes.c_char_p),
+    "iq_init": ([INT], INT),
+    "iq_weights_upload": ([P, SZ, INT, I64, I64, ctypes.POINTER(P)], INT),
+    "iq_weights_view": ([P, SZ, INT, I64, I64, ctypes.POINTER(P)], INT),
+    "iq_weights_free": ([P], INT),
+    "iq_weights_info": ([P, ctypes.POINTER(INT), ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(SZ),
+                         ctypes.POINTER(P)], INT),
+    "iq_weights_concat_rows": ([P, P, ctypes.POINTER(P)], INT),
+    "iq_weights_leading_rows": ([P, I64, ctypes.POINTER(P)], INT),
+    "iq_matmul": ([P, P, I64, P, P], INT),
+    "iq_matmul_workspace_size": ([P, I64], SZ),
+    "iq_matmul_ws": ([P, P, I64, P, P, SZ, P], INT),
+    "iq_matmul_host": ([P, P, I64, P], INT),
+    "iq_quantize_q8k": ([P, I64, I64, P, P], INT),
+    "iq_quantize_q80": ([P, I64, I64, P, P], INT),
+    "iq_block_sums": ([P, P, I64, P, P, P, P], INT),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library (raises OSError when it is missing)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} is missing: build it with `python -m inferq_amd._build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(L, name, None)
+            if fn is None:
+                continue
+            fn.argtypes, fn.restype = args, res
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != IQ_OK:
+        raise QgemmError(status, lib().iq_last_error().decode(errors="replace"))
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/*.h (the exported C ABI)."""
+    import glob
+    import re
+
+    names = []
+    for header in sorted(glob.glob(os.path.join(os.path.dirname(PKG), "include", "*.h"))):
+        text = open(header).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(iq_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))

@@ -1,0 +1,367 @@
+// iq_api.cpp -- the C ABI (include/iq_qgemm.h): handles, validation that
+// mirrors the reference's load- and call-time checks, workspaces and
+// dispatch to the kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/iq_qgemm.h"
+#include "iq_api_internal.h"
+#include "iq_internal.h"
+
+#define IQ_API extern "C" __attribute__((visibility("default")))
+
+namespace iq {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(IQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+const char* dtype_name(int dtype) {
+    switch (dtype) {
+    case kQ4_K: return "Q4K";
+    case kQ6_K: return "Q6K";
+    case kQ8_0: return "Q8_0";
+    default: return "unknown";
+    }
+}
+
+int64_t block_elems(int dtype) { return dtype == kQ8_0 ? 32 : 256; }
+int64_t block_bytes(int dtype) { return dtype == kQ4_K ? 144 : dtype == kQ6_K ? 210 : 34; }
+bool dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ6_K || dtype == kQ8_0; }
+
+namespace {
+
+std::mutex g_ws_mu;
+struct Workspace {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+std::vector<Workspace> g_ws;
+
+int current_device(int* dev) {
+    hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    return IQ_OK;
+}
+
+}  // namespace
+
+// Library-owned growable workspace of the current device.
+int workspace(size_t bytes, void** out) {
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
+    Workspace& w = g_ws[dev];
+    if (w.bytes < bytes) {
+        if (w.p) {
+            hipError_t e = hipDeviceSynchronize();  // the old buffer may still be in use
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+            (void)hipFree(w.p);
+            w.p = nullptr;
+            w.bytes = 0;
+        }
+        size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+        hipError_t e = hipMalloc(&w.p, want);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(IQ_ERR_OOM, "workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+        }
+        w.bytes = want;
+    }
+    *out = w.p;
+    return IQ_OK;
+}
+
+int check_weight(const iq_weight* w) {
+    if (!w || !w->dev) return fail(IQ_ERR_INVALID, "null quantized matrix handle");
+    return IQ_OK;
+}
+
+WeightView view_of(const iq_weight* w) {
+    WeightView v;
+    v.w = w->dev;
+    v.dtype = w->dtype;
+    v.rows = w->rows;
+    v.cols = w->cols;
+    v.row_bytes = w->row_bytes;
+    return v;
+}
+
+// Validated shape and size of a GGUF matrix (mirrors QuantizedMatrix::new,
+// src/gguf.rs:297-320, and the block-count checks of fused_forward,
+// src/gguf.rs:627-646).
+int check_matrix(int dtype, int64_t rows, int64_t cols, size_t nbytes, int64_t* row_bytes) {
+    if (!dtype_ok(dtype))
+        return fail(IQ_ERR_DTYPE, "unsupported executable GGUF matrix dtype %d; expected Q4_K, Q6_K or Q8_0", dtype);
+    if (rows <= 0 || cols <= 0) return fail(IQ_ERR_SHAPE, "invalid matrix shape [%lld, %lld]", (long long)rows,
+                                             (long long)cols);
+    if (cols % block_elems(dtype))
+        return fail(IQ_ERR_SHAPE, "GGUF matrix width %lld is not divisible by %s block size %lld", (long long)cols,
+                    dtype_name(dtype), (long long)block_elems(dtype));
+    const int64_t rb = cols / block_elems(dtype) * block_bytes(dtype);
+    if ((size_t)(rows * rb) != nbytes)
+        return fail(IQ_ERR_SHAPE, "quantized matrix has %zu bytes, expected %lld for [%lld, %lld] %s", nbytes,
+                    (long long)(rows * rb), (long long)rows, (long long)cols, dtype_name(dtype));
+    *row_bytes = rb;
+    return IQ_OK;
+}
+
+int alloc_weight(int dtype, int64_t rows, int64_t cols, int64_t row_bytes, iq_weight** out) {
+    // 256 zeroed padding bytes keep every vector load of the last block
+    // inside the allocation.
+    const size_t bytes = (size_t)(rows * row_bytes);
+    uint8_t* dev = nullptr;
+    hipError_t e = hipMalloc(&dev, bytes + 256);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(IQ_ERR_OOM, "allocation of %zu bytes for a [%lld, %lld] %s matrix failed: %s", bytes,
+                    (long long)rows, (long long)cols, dtype_name(dtype), hipGetErrorString(e));
+    }
+    e = hipMemset(dev + bytes, 0, 256);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e, "hipMemset");
+    }
+    iq_weight* w = new iq_weight;
+    w->dtype = dtype;
+    w->rows = rows;
+    w->cols = cols;
+    w->row_bytes = row_bytes;
+    w->nbytes = bytes;
+    w->dev = dev;
+    w->owned = true;
+    (void)hipGetDevice(&w->device);
+    *out = w;
+    return IQ_OK;
+}
+
+// Quantise m rows of device x for W's activation format into `a`.
+int quantize_for(const iq_weight* w, const float* x, int64_t m, const ActView& a, uint8_t* ref, hipStream_t s) {
+    hipError_t e = w->dtype == kQ8_0 ? launch_quant_q80(x, w->cols, m, w->cols, a, ref, s)
+                                     : launch_quant_q8k(x, w->cols, m, w->cols, a, ref, s);
+    if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
+    return IQ_OK;
+}
+
+int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* ws, size_t ws_bytes, int32_t* isum,
+                int32_t* msum, hipStream_t s) {
+    if (int rc = check_weight(w)) return rc;
+    if (m < 0) return fail(IQ_ERR_SHAPE, "negative input row count %lld", (long long)m);
+    if (m == 0) return IQ_OK;
+    if (!x || !y) return fail(IQ_ERR_INVALID, "null input or output pointer");
+    const size_t need = act_bytes(m, w->cols);
+    if (!ws) {
+        if (int rc = workspace(need, &ws)) return rc;
+    } else if (ws_bytes < need) {
+        return fail(IQ_ERR_SHAPE, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+    }
+    ActView a = act_carve(ws, m, w->cols);
+    if (int rc = quantize_for(w, x, m, a, nullptr, s)) return rc;
+    hipError_t e = launch_matmul_lanes(view_of(w), a, y, w->rows, isum, msum, s);
+    if (e != hipSuccess) return hip_fail(e, "matmul launch");
+    return IQ_OK;
+}
+
+}  // namespace iq
+
+using namespace iq;
+
+IQ_API const char* iq_version(void) { return "inferq-amd 0.1 (gfx950)"; }
+
+IQ_API const char* iq_last_error(void) { return g_err.c_str(); }
+
+IQ_API int iq_init(int device) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= n) return fail(IQ_ERR_RANGE, "device %d out of range (%d devices)", device, n);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(IQ_ERR_HIP, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+    return IQ_OK;
+}
+
+IQ_API int iq_weights_upload(const void* host_bytes, size_t nbytes, int dtype, int64_t rows, int64_t cols,
+                             iq_weight_t* out) {
+    if (!host_bytes || !out) return fail(IQ_ERR_INVALID, "null pointer");
+    int64_t rb;
+    if (int rc = check_matrix(dtype, rows, cols, nbytes, &rb)) return rc;
+    iq_weight* w;
+    if (int rc = alloc_weight(dtype, rows, cols, rb, &w)) return rc;
+    hipError_t e = hipMemcpy(w->dev, host_bytes, nbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(w->dev);
+        delete w;
+        return hip_fail(e, "hipMemcpy (weights upload)");
+    }
+    *out = w;
+    return IQ_OK;
+}
+
+IQ_API int iq_weights_view(const void* device_bytes, size_t nbytes, int dtype, int64_t rows, int64_t cols,
+                           iq_weight_t* out) {
+    if (!device_bytes || !out) return fail(IQ_ERR_INVALID, "null pointer");
+    if ((uintptr_t)device_bytes & 15u)
+        return fail(IQ_ERR_INVALID, "device matrix bytes must be 16-byte aligned");
+    int64_t rb;
+    if (int rc = check_matrix(dtype, rows, cols, nbytes, &rb)) return rc;
+    iq_weight* w = new iq_weight;
+    w->dtype = dtype;
+    w->rows = rows;
+    w->cols = cols;
+    w->row_bytes = rb;
+    w->nbytes = nbytes;
+    w->dev = (uint8_t*)device_bytes;
+    w->owned = false;
+    (void)hipGetDevice(&w->device);
+    *out = w;
+    return IQ_OK;
+}
+
+IQ_API int iq_weights_free(iq_weight_t w) {
+    if (!w) return IQ_OK;
+    if (w->owned && w->dev) (void)hipFree(w->dev);
+    delete w;
+    return IQ_OK;
+}
+
+IQ_API int iq_weights_info(iq_weight_t w, int* dtype, int64_t* rows, int64_t* cols, size_t* nbytes,
+                           const void** device_bytes) {
+    if (int rc = check_weight(w)) return rc;
+    if (dtype) *dtype = w->dtype;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (nbytes) *nbytes = w->nbytes;
+    if (device_bytes) *device_bytes = w->dev;
+    return IQ_OK;
+}
+
+IQ_API int iq_weights_concat_rows(iq_weight_t a, iq_weight_t b, iq_weight_t* out) {
+    if (int rc = check_weight(a)) return rc;
+    if (int rc = check_weight(b)) return rc;
+    if (!out) return fail(IQ_ERR_INVALID, "null output handle");
+    if (a->dtype != b->dtype)
+        return fail(IQ_ERR_DTYPE, "cannot concatenate quantized matrices with dtypes %s and %s", dtype_name(a->dtype),
+                    dtype_name(b->dtype));
+    if (a->cols != b->cols)
+        return fail(IQ_ERR_SHAPE, "cannot concatenate quantized matrices with %lld and %lld columns",
+                    (long long)a->cols, (long long)b->cols);
+    iq_weight* w;
+    if (int rc = alloc_weight(a->dtype, a->rows + b->rows, a->cols, a->row_bytes, &w)) return rc;
+    hipError_t e = hipMemcpy(w->dev, a->dev, a->nbytes, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess) e = hipMemcpy(w->dev + a->nbytes, b->dev, b->nbytes, hipMemcpyDeviceToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(w->dev);
+        delete w;
+        return hip_fail(e, "hipMemcpy (concatenate_rows)");
+    }
+    *out = w;
+    return IQ_OK;
+}
+
+IQ_API int iq_weights_leading_rows(iq_weight_t a, int64_t rows, iq_weight_t* out) {
+    if (int rc = check_weight(a)) return rc;
+    if (!out) return fail(IQ_ERR_INVALID, "null output handle");
+    if (rows <= 0 || rows > a->rows)
+        return fail(IQ_ERR_RANGE, "cannot take %lld leading rows of a %lld-row matrix", (long long)rows,
+                    (long long)a->rows);
+    iq_weight* w;
+    if (int rc = alloc_weight(a->dtype, rows, a->cols, a->row_bytes, &w)) return rc;
+    hipError_t e = hipMemcpy(w->dev, a->dev, (size_t)(rows * a->row_bytes), hipMemcpyDeviceToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(w->dev);
+        delete w;
+        return hip_fail(e, "hipMemcpy (leading_rows)");
+    }
+    *out = w;
+    return IQ_OK;
+}
+
+IQ_API int iq_matmul(iq_weight_t w, const float* x, int64_t m, float* y, iq_stream_t stream) {
+    return matmul_impl(w, x, m, y, nullptr, 0, nullptr, nullptr, (hipStream_t)stream);
+}
+
+IQ_API size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m) {
+    if (!w || m <= 0) return 0;
+    return act_bytes(m, w->cols);
+}
+
+IQ_API int iq_matmul_ws(iq_weight_t w, const float* x, int64_t m, float* y, void* workspace_ptr,
+                        size_t workspace_bytes, iq_stream_t stream) {
+    if (!workspace_ptr) return fail(IQ_ERR_INVALID, "null workspace");
+    return matmul_impl(w, x, m, y, workspace_ptr, workspace_bytes, nullptr, nullptr, (hipStream_t)stream);
+}
+
+IQ_API int iq_matmul_host(iq_weight_t w, const float* x_host, int64_t m, float* y_host) {
+    if (int rc = check_weight(w)) return rc;
+    if (m <= 0) return m == 0 ? IQ_OK : fail(IQ_ERR_SHAPE, "negative input row count");
+    if (!x_host || !y_host) return fail(IQ_ERR_INVALID, "null input or output pointer");
+    const size_t xb = (size_t)(m * w->cols) * 4, yb = (size_t)(m * w->rows) * 4;
+    const size_t xo = 0, yo = (xb + 255) & ~(size_t)255, ao = yo + ((yb + 255) & ~(size_t)255);
+    const size_t need = ao + act_bytes(m, w->cols);
+    void* ws;
+    if (int rc = workspace(need, &ws)) return rc;
+    uint8_t* base = (uint8_t*)ws;
+    hipError_t e = hipMemcpy(base + xo, x_host, xb, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy (input)");
+    if (int rc = matmul_impl(w, (const float*)(base + xo), m, (float*)(base + yo), base + ao, need - ao, nullptr,
+                             nullptr, nullptr))
+        return rc;
+    e = hipMemcpy(y_host, base + yo, yb, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy (output)");
+    return IQ_OK;
+}
+
+static int quantize_entry(int dtype, const float* x, int64_t m, int64_t k, void* blocks_out, hipStream_t s) {
+    if (!x || !blocks_out) return fail(IQ_ERR_INVALID, "null pointer");
+    const int64_t be = dtype == kQ8_0 ? 32 : 256;
+    if (m < 0 || k <= 0 || k % be)
+        return fail(IQ_ERR_SHAPE, "quantize_row_%s: %lld is not divisible by %lld", dtype == kQ8_0 ? "q8_0" : "q8k",
+                    (long long)k, (long long)be);
+    if (m == 0) return IQ_OK;
+    void* ws;
+    if (int rc = workspace(act_bytes(m, k), &ws)) return rc;
+    ActView a = act_carve(ws, m, k);
+    hipError_t e = dtype == kQ8_0 ? launch_quant_q80(x, k, m, k, a, (uint8_t*)blocks_out, s)
+                                  : launch_quant_q8k(x, k, m, k, a, (uint8_t*)blocks_out, s);
+    if (e != hipSuccess) return hip_fail(e, "quantisation launch");
+    return IQ_OK;
+}
+
+IQ_API int iq_quantize_q8k(const float* x, int64_t m, int64_t k, void* blocks_out, iq_stream_t stream) {
+    return quantize_entry(kQ4_K, x, m, k, blocks_out, (hipStream_t)stream);
+}
+
+IQ_API int iq_quantize_q80(const float* x, int64_t m, int64_t k, void* blocks_out, iq_stream_t stream) {
+    return quantize_entry(kQ8_0, x, m, k, blocks_out, (hipStream_t)stream);
+}
+
+IQ_API int iq_block_sums(iq_weight_t w, const float* x, int64_t m, float* y, int32_t* isum, int32_t* msum,
+                         iq_stream_t stream) {
+    if (!isum) return fail(IQ_ERR_INVALID, "null isum buffer");
+    if (w && w->dtype == kQ4_K && !msum) return fail(IQ_ERR_INVALID, "Q4_K needs an msum buffer");
+    return matmul_impl(w, x, m, y, nullptr, 0, isum, msum, (hipStream_t)stream);
+}

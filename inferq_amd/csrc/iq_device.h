@@ -1,0 +1,95 @@
+// iq_device.h -- device helpers shared by the gfx950 kernels.
+//
+// Numerics contract: every kernel here reproduces the reference CPU kernels'
+// f32 arithmetic exactly (src/qgemm.rs:175-397): exact integer lane sums,
+// one correctly rounded FMA per block per lane, and the fixed hsum trees.
+// The library is compiled with -ffp-contract=off so that no a*b+c is fused
+// unless written as __builtin_fmaf.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "iq_internal.h"
+
+namespace iq {
+
+// Internal activation layout.  Activations for K-quant weights are Q8K
+// (256 values per block); for Q8_0 weights they are Q8_0 (32 per block).
+// Either way the int8 values of each 256-value group are stored with their
+// dwords transposed 8x8: dword (chunk c, lane k), which holds values
+// 32c+4k .. 32c+4k+3, is stored at dword index 8k+c.  Lane k of an output
+// row then reads its eight dwords (one per 32-value chunk) as 32 contiguous
+// bytes.
+__host__ __device__ constexpr int perm_dword(int c, int k) { return 8 * k + c; }
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4a16 __attribute__((ext_vector_type(4), aligned(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4), aligned(16)));
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffffu));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
+__device__ __forceinline__ uint32_t ld16(const uint8_t* p) { return *(const uint16_t*)p; }
+
+// Four bytes at a 2-byte aligned address, never reading outside [p, p+4).
+__device__ __forceinline__ uint32_t ld32_a2(const uint8_t* p) {
+    if (((uintptr_t)p & 3u) == 0) return ld32(p);
+    return ld16(p) | (ld16(p + 2) << 16);
+}
+
+// Four bytes at p == 2 (mod 4) when the two bytes before p are readable:
+// one aligned 8-byte load and a byte funnel shift.
+__device__ __forceinline__ uint32_t ld32_m2(const uint8_t* p) {
+    u32x2 v = *(const u32x2*)(p - 2);
+    return __builtin_amdgcn_alignbyte(v.y, v.x, 2);
+}
+
+// Lane exchange inside groups of 8 lanes (lane ^ mask), mask in {1, 2, 4}.
+template <int MASK>
+__device__ __forceinline__ float xor_lane(float v) {
+    int i = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (MASK == 1) {
+        r = __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (MASK == 2) {
+        r = __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else {
+        r = __builtin_amdgcn_ds_swizzle(i, 0x101F);  // bitmode: and 0x1f, xor 4
+    }
+    return __builtin_bit_cast(float, r);
+}
+
+// hsum_f32_8 over the 8 lanes of a group: ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)).
+// Every lane of the group ends with the same value.
+__device__ __forceinline__ float hsum8(float v) {
+    v = v + xor_lane<4>(v);
+    v = v + xor_lane<2>(v);
+    v = v + xor_lane<1>(v);
+    return v;
+}
+
+// hsum_f32_4 over lanes 0..3 of a group: (l0+l2) + (l1+l3), valid in lane 0.
+__device__ __forceinline__ float hsum4(float v) {
+    v = v + xor_lane<2>(v);
+    v = v + xor_lane<1>(v);
+    return v;
+}
+
+// Correctly rounded exp for f32 arguments: exp is evaluated in double and
+// rounded once.  glibc's expf (what the reference's f32::exp calls) agrees
+// with it except where glibc itself misrounds a near-midpoint case.
+__device__ __forceinline__ float exp_f32(float x) { return (float)::exp((double)x); }
+
+}  // namespace iq

@@ -1,0 +1,52 @@
+// iq_internal.h -- host-side declarations shared by the library's sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace iq {
+
+// GGML type ids (GGUF dtype codes).
+constexpr int kQ8_0 = 8;
+constexpr int kQ4_K = 12;
+constexpr int kQ6_K = 14;
+
+// Quantised activations in the internal (lane-transposed) layout.
+struct ActView {
+    int8_t* q = nullptr;     // [m][ldq] int8, 256-value groups lane-transposed
+    float* d = nullptr;      // [m][ldd] scale per block (Q8K: per 256; Q8_0: per 32)
+    int16_t* s8 = nullptr;   // [m][ng][8] Q8K 32-value sub-block sums (K-quants only)
+    int64_t ldq = 0, ldd = 0;
+    int ng = 0;              // 256-value groups per row
+    int m = 0;
+};
+
+// Bytes of workspace an ActView of m rows and width k needs (all parts,
+// each 256-byte aligned).
+size_t act_bytes(int64_t m, int64_t k);
+// Carve an ActView out of `base` (which holds at least act_bytes(m, k)).
+ActView act_carve(void* base, int64_t m, int64_t k);
+
+// Activation quantisers.  x is f32 [m][ldx]; `ref`, when not null, also
+// receives the reference block layout (292-byte Q8K or 34-byte Q8_0 blocks,
+// [m][k/256] or [m][k/32]).
+hipError_t launch_quant_q8k(const float* x, int64_t ldx, int64_t m, int64_t k, const ActView& a, uint8_t* ref,
+                            hipStream_t s);
+hipError_t launch_quant_q80(const float* x, int64_t ldx, int64_t m, int64_t k, const ActView& a, uint8_t* ref,
+                            hipStream_t s);
+
+// Weight matrix in native GGUF block layout.
+struct WeightView {
+    const uint8_t* w = nullptr;
+    int dtype = 0;
+    int64_t rows = 0, cols = 0, row_bytes = 0;
+};
+
+// y[m][ldy] = act . W^T with the reference's exact f32 order.  When isum is
+// not null, the per-block lane integers are also written:
+// isum [m][rows][blocks][8], msum [m][rows][blocks][4] (Q4_K only).
+hipError_t launch_matmul_lanes(const WeightView& w, const ActView& a, float* y, int64_t ldy, int32_t* isum,
+                               int32_t* msum, hipStream_t s);
+
+}  // namespace iq

@@ -1,0 +1,213 @@
+"""Host-side mirror of the reference's executable quantised matrix.
+
+`QuantizedMatrix` keeps the interface of inferq's QuantizedMatrix
+(src/gguf.rs:163-690): the same method names, argument meaning and error
+behaviour, with the packed GGUF blocks resident in HBM and every product run
+by the gfx950 kernels through the C ABI (include/iq_qgemm.h).  PyTorch is
+used only for device memory and the current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import IQ_Q4_K, IQ_Q6_K, IQ_Q8_0, QgemmError, check, lib
+
+DTYPE_NAMES = {IQ_Q4_K: "Q4K", IQ_Q6_K: "Q6K", IQ_Q8_0: "Q8_0"}
+BLOCK_ELEMS = {IQ_Q4_K: 256, IQ_Q6_K: 256, IQ_Q8_0: 32}
+BLOCK_BYTES = {IQ_Q4_K: 144, IQ_Q6_K: 210, IQ_Q8_0: 34}
+
+_initialised = set()
+
+
+def init(device: int = 0) -> None:
+    """Bind the calling thread to `device` (a gfx950 GPU)."""
+    import torch
+
+    torch.cuda.set_device(device)
+    check(lib().iq_init(device))
+    _initialised.add(device)
+
+
+def _ensure_init():
+    import torch
+
+    dev = torch.cuda.current_device()
+    if dev not in _initialised:
+        init(dev)
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class QuantizedMatrix:
+    """A [rows x cols] GGUF matrix (Q4_K, Q6_K or Q8_0) resident in HBM."""
+
+    def __init__(self, handle: ctypes.c_void_p, keepalive=None):
+        self._h = handle
+        self._keepalive = keepalive  # device buffer a view borrows
+        dt, r, c, nb = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_size_t()
+        check(lib().iq_weights_info(self._h, ctypes.byref(dt), ctypes.byref(r), ctypes.byref(c), ctypes.byref(nb),
+                                    None))
+        self._dtype, self._rows, self._cols, self._bytes = dt.value, r.value, c.value, nb.value
+
+    # ---- construction --------------------------------------------------
+    @classmethod
+    def upload(cls, data, dtype: int, rows: int, cols: int) -> "QuantizedMatrix":
+        """Copy host GGUF block bytes (bytes / numpy uint8) to HBM."""
+        _ensure_init()
+        arr = np.ascontiguousarray(np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray))
+                                   else np.asarray(data).view(np.uint8).reshape(-1))
+        h = ctypes.c_void_p()
+        check(lib().iq_weights_upload(arr.ctypes.data, arr.nbytes, dtype, rows, cols, ctypes.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def view(cls, device_tensor, dtype: int, rows: int, cols: int, offset: int = 0,
+             nbytes: int | None = None) -> "QuantizedMatrix":
+        """Wrap bytes already in HBM (a CUDA uint8 tensor) without copying."""
+        _ensure_init()
+        if nbytes is None:
+            nbytes = rows * (cols // BLOCK_ELEMS.get(dtype, 1)) * BLOCK_BYTES.get(dtype, 0)
+        h = ctypes.c_void_p()
+        check(lib().iq_weights_view(device_tensor.data_ptr() + offset, nbytes, dtype, rows, cols, ctypes.byref(h)))
+        return cls(h, keepalive=device_tensor)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and _lib._lib is not None:
+            _lib._lib.iq_weights_free(h)
+            self._h = None
+
+    # ---- reference accessors (src/gguf.rs:322-332) --------------------
+    def dtype(self) -> str:
+        return DTYPE_NAMES[self._dtype]
+
+    @property
+    def ggml_dtype(self) -> int:
+        return self._dtype
+
+    def shape(self) -> list[int]:
+        return [self._rows, self._cols]
+
+    def storage_bytes(self) -> int:
+        return self._bytes
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def device_ptr(self) -> int:
+        p = ctypes.c_void_p()
+        check(lib().iq_weights_info(self._h, None, None, None, None, ctypes.byref(p)))
+        return p.value
+
+    # ---- derived matrices ----------------------------------------------
+    def concatenate_rows(self, other: "QuantizedMatrix") -> "QuantizedMatrix":
+        """src/gguf.rs:379-404: this matrix's rows, then `other`'s."""
+        h = ctypes.c_void_p()
+        check(lib().iq_weights_concat_rows(self._h, other._h, ctypes.byref(h)))
+        return QuantizedMatrix(h)
+
+    def leading_rows(self, rows: int) -> "QuantizedMatrix":
+        """src/gguf.rs:352-377: the first `rows` output rows."""
+        h = ctypes.c_void_p()
+        check(lib().iq_weights_leading_rows(self._h, rows, ctypes.byref(h)))
+        return QuantizedMatrix(h)
+
+    # ---- products --------------------------------------------------------
+    def _validated_input(self, xs):
+        """src/gguf.rs:692-708: rank >= 2, last dim == cols, converted to f32."""
+        import torch
+
+        if xs.dim() < 2:
+            raise QgemmError(_lib.IQ_ERR_SHAPE, "quantized matrix input must have rank at least two")
+        if xs.shape[-1] != self._cols:
+            raise QgemmError(_lib.IQ_ERR_SHAPE, f"quantized matrix input has final dimension {xs.shape[-1]}, "
+                                                f"expected {self._cols}")
+        if not xs.is_cuda:
+            raise QgemmError(_lib.IQ_ERR_INVALID, "quantized matrix input must be a device (HBM) tensor")
+        return xs.to(torch.float32).contiguous()
+
+    def forward(self, xs):
+        """src/gguf.rs:406: y[..., rows] = xs[..., cols] . W^T."""
+        import torch
+
+        xs = self._validated_input(xs)
+        m = xs.numel() // self._cols
+        y = torch.empty(*xs.shape[:-1], self._rows, dtype=torch.float32, device=xs.device)
+        check(lib().iq_matmul(self._h, xs.data_ptr(), m, y.data_ptr(), _stream()))
+        return y
+
+    # Where the output rows are computed never changes the result
+    # (RowSpread, src/gguf.rs:64-80); on the GPU there is one spread.
+    def forward_spread(self, xs, spread=None):
+        return self.forward(xs)
+
+    def forward_rows(self, values, input_rows: int):
+        """src/gguf.rs:433-456: `input_rows` contiguous rows of a flat f32
+        device tensor, result flat row-major [input_rows x rows]."""
+        import torch
+
+        if values.numel() != input_rows * self._cols:
+            raise QgemmError(_lib.IQ_ERR_SHAPE, f"expected {input_rows * self._cols} input values for {input_rows} "
+                                                f"rows of {self._cols} columns, got {values.numel()}")
+        x = values.reshape(input_rows, self._cols)
+        return self.forward(x).reshape(-1) if input_rows else torch.empty(0, device=values.device)
+
+    def forward_host(self, x: np.ndarray) -> np.ndarray:
+        """Host f32 [m x cols] in, host f32 [m x rows] out (iq_matmul_host)."""
+        _ensure_init()
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim < 2 or x.shape[-1] != self._cols:
+            raise QgemmError(_lib.IQ_ERR_SHAPE, f"quantized matrix input has final dimension {x.shape[-1]}, "
+                                                f"expected {self._cols}")
+        m = x.size // self._cols
+        y = np.empty((*x.shape[:-1], self._rows), np.float32)
+        check(lib().iq_matmul_host(self._h, x.ctypes.data, m, y.ctypes.data))
+        return y
+
+    def block_sums(self, xs):
+        """Per-block lane integers of xs . W^T (see iq_block_sums)."""
+        import torch
+
+        xs = self._validated_input(xs)
+        m = xs.numel() // self._cols
+        nb = self._cols // BLOCK_ELEMS[self._dtype]
+        y = torch.empty(m, self._rows, dtype=torch.float32, device=xs.device)
+        isum = torch.empty(m, self._rows, nb, 8, dtype=torch.int32, device=xs.device)
+        msum = torch.empty(m, self._rows, nb, 4, dtype=torch.int32, device=xs.device)
+        check(lib().iq_block_sums(self._h, xs.data_ptr(), m, y.data_ptr(), isum.data_ptr(), msum.data_ptr(),
+                                  _stream()))
+        return y, isum, (msum if self._dtype == IQ_Q4_K else None)
+
+
+def quantize_q8k(xs):
+    """Q8K blocks (292 B each) of device f32 rows xs[m x k], k % 256 == 0."""
+    import torch
+
+    _ensure_init()
+    xs = xs.to(torch.float32).contiguous()
+    k = xs.shape[-1]
+    m = xs.numel() // k
+    out = torch.empty(m * (k // 256) * 292, dtype=torch.uint8, device=xs.device)
+    check(lib().iq_quantize_q8k(xs.data_ptr(), m, k, out.data_ptr(), _stream()))
+    return out
+
+
+def quantize_q80(xs):
+    """Q8_0 blocks (34 B each) of device f32 rows xs[m x k], k % 32 == 0."""
+    import torch
+
+    _ensure_init()
+    xs = xs.to(torch.float32).contiguous()
+    k = xs.shape[-1]
+    m = xs.numel() // k
+    out = torch.empty(m * (k // 32) * 34, dtype=torch.uint8, device=xs.device)
+    check(lib().iq_quantize_q80(xs.data_ptr(), m, k, out.data_ptr(), _stream()))
+    return out

@@ -1,0 +1,62 @@
+"""Seeded synthetic GGUF block data and activations.
+
+Weights are random bytes in the native GGUF block layouts, drawn so that
+every block is a valid, finite block:
+  * Q4_K (144 B): fp16 d and dmin ~ U[0, 2^-6); 12 scale bytes and 128 quant
+    bytes uniform u8.
+  * Q6_K (210 B): ql, qh uniform u8; 16 scales uniform i8; fp16 d ~ U[0, 2^-6).
+  * Q8_0 (34 B): fp16 d = |N(0,1)| * 0.02; 32 quants uniform in [-127, 127].
+Activations and router logits are f32 ~ N(0, 1).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_0: 34}
+BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32}
+NAMES = {Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_0: "Q8_0"}
+
+
+def row_bytes(dtype: int, cols: int) -> int:
+    if cols % BLOCK_ELEMS[dtype]:
+        raise ValueError(f"{NAMES[dtype]} needs a width divisible by {BLOCK_ELEMS[dtype]}, got {cols}")
+    return cols // BLOCK_ELEMS[dtype] * BLOCK_BYTES[dtype]
+
+
+def matrix_bytes(dtype: int, rows: int, cols: int) -> int:
+    return rows * row_bytes(dtype, cols)
+
+
+def _f16_bits(values: np.ndarray) -> np.ndarray:
+    return values.astype(np.float16).view(np.uint16)
+
+
+def random_blocks(dtype: int, n_blocks: int, rng: np.random.Generator) -> np.ndarray:
+    """n_blocks random blocks as a flat uint8 array."""
+    bb = BLOCK_BYTES[dtype]
+    raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
+    if dtype == Q4_K:
+        d = _f16_bits(rng.random(n_blocks, dtype=np.float32) * np.float32(2.0 ** -6))
+        dmin = _f16_bits(rng.random(n_blocks, dtype=np.float32) * np.float32(2.0 ** -6))
+        raw[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
+        raw[:, 2:4] = dmin.view(np.uint8).reshape(n_blocks, 2)
+    elif dtype == Q6_K:
+        d = _f16_bits(rng.random(n_blocks, dtype=np.float32) * np.float32(2.0 ** -6))
+        raw[:, 208:210] = d.view(np.uint8).reshape(n_blocks, 2)
+    elif dtype == Q8_0:
+        d = _f16_bits(np.abs(rng.standard_normal(n_blocks, dtype=np.float32)) * np.float32(0.02))
+        raw[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
+        raw[:, 2:34] = rng.integers(-127, 128, size=(n_blocks, 32), dtype=np.int8).view(np.uint8)
+    else:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return raw.reshape(-1)
+
+
+def random_matrix(dtype: int, rows: int, cols: int, rng: np.random.Generator) -> np.ndarray:
+    """A [rows x cols] matrix of random GGUF blocks (flat uint8)."""
+    return random_blocks(dtype, rows * (cols // BLOCK_ELEMS[dtype]), rng)
+
+
+def normal(shape, rng: np.random.Generator) -> np.ndarray:
+    return rng.standard_normal(shape, dtype=np.float32)

@@ -1,0 +1,146 @@
+"""GPU parity of the quantised matmul through the C ABI.
+
+Tolerance: the path's stated bar is per-block integers bit-exact and f32
+outputs within a normwise relative error of 1e-4.  These kernels follow the
+reference's per-lane f32 order, so the tests assert the stronger property:
+every output is bit-identical to the oracle (the reference's fused kernel
+restated), and the per-block lane integers are identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bitexact
+from inferq_amd import qgemm as Q
+from inferq_amd import synth as S
+
+pytestmark = pytest.mark.gpu
+
+Q4, Q6, Q8 = S.Q4_K, S.Q6_K, S.Q8_0
+
+# (dtype, rows, cols): the reference test matrix shape [96 x 512] for each
+# format (src/gguf.rs:1630-1677), the BASELINE shapes, ragged row counts
+# (not a multiple of 8) and an odd number of Q6_K blocks per row.
+SHAPES = [
+    (Q4, 96, 512), (Q6, 96, 512), (Q8, 96, 512),
+    (Q4, 1024, 2048), (Q6, 2048, 512), (Q8, 4096, 2048),
+    (Q4, 2048, 4096), (Q6, 37, 768), (Q8, 45, 96), (Q4, 13, 256),
+]
+ROWS = [1, 2, 3, 4, 7, 8, 9, 15, 16, 17, 33]
+
+
+def _case(dtype, rows, cols, m, seed):
+    rng = np.random.default_rng(seed)
+    w = S.random_matrix(dtype, rows, cols, rng)
+    x = S.normal((m, cols), rng)
+    return w, x
+
+
+@pytest.mark.parametrize("dtype,rows,cols", SHAPES)
+def test_matmul_bitexact_across_row_counts(gpu, oracle, dtype, rows, cols):
+    w, _ = _case(dtype, rows, cols, 1, seed=rows * 131 + cols + dtype)
+    mat = Q.QuantizedMatrix.upload(w, dtype, rows, cols)
+    assert mat.shape() == [rows, cols] and mat.storage_bytes() == w.size
+    for m in ROWS:
+        x = S.normal((m, cols), np.random.default_rng(1000 + m))
+        expected = oracle.matmul(dtype, w, rows, cols, x, impl=0)
+        got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+        assert_bitexact(got, expected, f"{S.NAMES[dtype]} [{rows}x{cols}] m={m}")
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(Q4, 64, 512), (Q6, 40, 512), (Q8, 24, 256)])
+def test_block_lane_integers_bitexact(gpu, oracle, dtype, rows, cols):
+    w, x = _case(dtype, rows, cols, 3, seed=7)
+    mat = Q.QuantizedMatrix.upload(w, dtype, rows, cols)
+    y, isum, msum = mat.block_sums(torch.from_numpy(x).to(gpu))
+    isum = isum.cpu().numpy()
+    msum = msum.cpu().numpy() if msum is not None else None
+    nb = cols // S.BLOCK_ELEMS[dtype]
+    wb = w.view(oracle.BLOCK[dtype]).reshape(rows, nb)
+    for r in range(x.shape[0]):
+        q = oracle.quantize_q80(x[r]) if dtype == Q8 else oracle.quantize_q8k(x[r])
+        for n in range(rows):
+            for b in range(nb):
+                ei, em = oracle.block_lanes(dtype, wb[n, b], q[b])
+                assert np.array_equal(isum[r, n, b], ei), (r, n, b)
+                if em is not None:
+                    assert np.array_equal(msum[r, n, b], em), (r, n, b)
+    assert_bitexact(y.cpu().numpy(), oracle.matmul(dtype, w, rows, cols, x), "block_sums output")
+
+
+def _edge_rows(k, rng):
+    rows = [
+        np.zeros(k, np.float32),                         # amax == 0: d = 0, q = 0
+        S.normal(k, rng),
+        np.where(np.arange(k) == 5, np.float32(-3.0), np.float32(0)),  # one nonzero (negative max)
+        np.tile(np.float32([1.0, -1.0]), k // 2),        # |max| tied everywhere: first index wins
+        (np.arange(k, dtype=np.float32) - k / 2) / 64,   # values on exact .5 ties after scaling
+        S.normal(k, rng) * np.float32(1e-30),            # tiny magnitudes
+        S.normal(k, rng) * np.float32(1e30),             # huge magnitudes
+    ]
+    return np.stack(rows).astype(np.float32)
+
+
+def test_quantize_q8k_bitexact(gpu, oracle):
+    rng = np.random.default_rng(3)
+    x = _edge_rows(1024, rng)
+    got = Q.quantize_q8k(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    expected = np.concatenate([oracle.quantize_q8k(r) for r in x]).view(np.uint8)
+    assert np.array_equal(got, expected.reshape(-1))
+
+
+def test_quantize_q80_bitexact(gpu, oracle):
+    rng = np.random.default_rng(4)
+    x = _edge_rows(512, rng)
+    got = Q.quantize_q80(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    expected = np.concatenate([oracle.quantize_q80(r) for r in x]).view(np.uint8)
+    assert np.array_equal(got, expected.reshape(-1))
+
+
+def test_m_invariance_bitwise(gpu):
+    """One row alone equals the same row inside 4-, 8- and 16-row passes
+    (tests/speculative_policy.rs:373-450 in the reference)."""
+    rng = np.random.default_rng(11)
+    for dtype, rows, cols in [(Q4, 512, 2048), (Q6, 512, 2048), (Q8, 512, 2048)]:
+        w = S.random_matrix(dtype, rows, cols, rng)
+        mat = Q.QuantizedMatrix.upload(w, dtype, rows, cols)
+        x = torch.from_numpy(S.normal((16, cols), rng)).to(gpu)
+        singles = torch.cat([mat.forward(x[i:i + 1]) for i in range(16)]).cpu().numpy()
+        for m in (4, 8, 16):
+            multi = mat.forward(x[:m]).cpu().numpy()
+            assert_bitexact(multi, singles[:m], f"{S.NAMES[dtype]} m={m}")
+
+
+def test_concatenated_rows_match_separate_matrices(gpu):
+    rng = np.random.default_rng(5)
+    for dtype in (Q4, Q6, Q8):
+        a = Q.QuantizedMatrix.upload(S.random_matrix(dtype, 16, 512, rng), dtype, 16, 512)
+        b = Q.QuantizedMatrix.upload(S.random_matrix(dtype, 24, 512, rng), dtype, 24, 512)
+        c = a.concatenate_rows(b)
+        assert c.shape() == [40, 512]
+        x = torch.from_numpy(S.normal((3, 512), rng)).to(gpu)
+        expected = torch.cat([a.forward(x), b.forward(x)], dim=1).cpu().numpy()
+        assert_bitexact(c.forward(x).cpu().numpy(), expected, "concatenate_rows")
+        lead = c.leading_rows(16)
+        assert_bitexact(lead.forward(x).cpu().numpy(), a.forward(x).cpu().numpy(), "leading_rows")
+
+
+def test_host_entry_matches_device_entry(gpu, oracle):
+    rng = np.random.default_rng(6)
+    w = S.random_matrix(Q4, 128, 1024, rng)
+    mat = Q.QuantizedMatrix.upload(w, Q4, 128, 1024)
+    x = S.normal((5, 1024), rng)
+    assert_bitexact(mat.forward_host(x), oracle.matmul(Q4, w, 128, 1024, x), "host entry")
+
+
+def test_call_time_errors(gpu):
+    mat = Q.QuantizedMatrix.upload(np.zeros(144, np.uint8), Q4, 1, 256)
+    with pytest.raises(Q.QgemmError, match="final dimension 128, expected 256"):
+        mat.forward(torch.zeros(1, 128, device=gpu))
+    with pytest.raises(Q.QgemmError, match="rank at least two"):
+        mat.forward(torch.zeros(256, device=gpu))
+    with pytest.raises(Q.QgemmError, match="cannot take 2 leading rows of a 1-row matrix"):
+        mat.leading_rows(2)
+    other = Q.QuantizedMatrix.upload(np.zeros(34 * 8, np.uint8), Q8, 1, 256)
+    with pytest.raises(Q.QgemmError, match="cannot concatenate quantized matrices with dtypes"):
+        mat.concatenate_rows(other)
