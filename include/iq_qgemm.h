@@ -132,6 +132,42 @@ int iq_quantize_q80(const float *x, int64_t m, int64_t k, void *blocks_out, iq_s
 int iq_block_sums(iq_weight_t w, const float *x, int64_t m, float *y, int32_t *isum, int32_t *msum,
                   iq_stream_t stream);
 
+/* ---- MoE sublayer ---------------------------------------------------------- */
+
+/* One quantised MoE sublayer: routed experts resident in HBM as the GGUF
+ * expert tensors (not copied), plus an optional shared expert.  Shapes:
+ *   gate, up     [n_experts, inter, hidden]   (blk.N.ffn_{gate,up}_exps)
+ *   down         [n_experts, hidden, inter]   (blk.N.ffn_down_exps)
+ *   shared_gate, shared_up [inter, hidden]; shared_down [hidden, inter]
+ *   selector     f32 [hidden]                 (blk.N.ffn_gate_inp_shexp)
+ * Replaces: QuantizedMoeLayer::load (src/qwen/quantized_moe.rs:141-225) over
+ * a fully resident expert cache (src/residency.rs:39-131). */
+typedef struct {
+    int64_t hidden, inter, n_experts, top_k;
+    int normalize; /* renormalise the top-k weights to sum to one */
+    int gate_dtype, down_dtype;
+    const void *gate, *up, *down; /* device, 16-byte aligned */
+    size_t gate_bytes, up_bytes, down_bytes;
+    int shared_gate_dtype, shared_down_dtype;
+    const void *shared_gate, *shared_up, *shared_down; /* device or all NULL */
+    const float *selector;                              /* device; required with a shared expert */
+} iq_moe_desc;
+
+int iq_moe_create(const iq_moe_desc *desc, iq_moe_t *out);
+int iq_moe_destroy(iq_moe_t moe);
+
+/* out[m x hidden] = MoE(x[m x hidden]) for device x, router logits
+ * [m x n_experts] and out.  Routing is softmax, top-k by probability,
+ * renormalised (src/qwen/moe.rs:21-54); routed experts run grouped by
+ * expert (src/qwen/quantized_moe.rs:336-406), SwiGLU between gate/up and
+ * down, ordered combine, then routed + shared * sigmoid(x . selector)
+ * (:266-273).  experts_out [m x top_k] i32 and weights_out [m x top_k] f32
+ * (device, may be NULL) receive the routes.  m * top_k <= 4096.
+ * Replaces: QuantizedMoeLayer::forward (src/qwen/quantized_moe.rs:227-281)
+ * minus the router matmul, whose logits are the input here. */
+int iq_moe_forward(iq_moe_t moe, const float *x, const float *router_logits, int64_t m, float *out,
+                   int32_t *experts_out, float *weights_out, iq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

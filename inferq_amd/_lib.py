@@ -49,7 +49,25 @@ _SIGNATURES = {
     "iq_quantize_q8k": ([P, I64, I64, P, P], INT),
     "iq_quantize_q80": ([P, I64, I64, P, P], INT),
     "iq_block_sums": ([P, P, I64, P, P, P, P], INT),
+    "iq_moe_create": ([P, ctypes.POINTER(P)], INT),
+    "iq_moe_destroy": ([P], INT),
+    "iq_moe_forward": ([P, P, P, I64, P, P, P, P], INT),
 }
+
+
+class MoeDesc(ctypes.Structure):
+    """iq_moe_desc (include/iq_qgemm.h)."""
+
+    _fields_ = [
+        ("hidden", ctypes.c_int64), ("inter", ctypes.c_int64), ("n_experts", ctypes.c_int64),
+        ("top_k", ctypes.c_int64), ("normalize", ctypes.c_int),
+        ("gate_dtype", ctypes.c_int), ("down_dtype", ctypes.c_int),
+        ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+        ("gate_bytes", ctypes.c_size_t), ("up_bytes", ctypes.c_size_t), ("down_bytes", ctypes.c_size_t),
+        ("shared_gate_dtype", ctypes.c_int), ("shared_down_dtype", ctypes.c_int),
+        ("shared_gate", ctypes.c_void_p), ("shared_up", ctypes.c_void_p), ("shared_down", ctypes.c_void_p),
+        ("selector", ctypes.c_void_p),
+    ]
 
 
 def lib() -> ctypes.CDLL:

@@ -1,0 +1,50 @@
+// iq_moe.h -- parameters of the MoE launches (host and device).
+#pragma once
+
+#include "iq_internal.h"
+
+namespace iq {
+
+constexpr int kMoeMaxExperts = 512;   // routed experts per layer
+constexpr int kMoeMaxTopK = 16;       // experts per token
+constexpr int kMoeMaxAssign = 4096;   // tokens * top_k per call
+
+struct MoeParams {
+    // layer (device pointers, GGUF native layout)
+    int64_t H = 0, I = 0, E = 0, K = 0;
+    int normalize = 1;
+    const uint8_t* gate = nullptr;  // [E][I][H]
+    const uint8_t* up = nullptr;    // [E][I][H]
+    const uint8_t* down = nullptr;  // [E][H][I]
+    const uint8_t* sgate_w = nullptr;  // shared expert [I][H], or null
+    const uint8_t* sup_w = nullptr;    // [I][H]
+    const uint8_t* sdown_w = nullptr;  // [H][I]
+    const float* selector = nullptr;   // [H]
+    int64_t g_row_bytes = 0, d_row_bytes = 0, g_exp_bytes = 0, d_exp_bytes = 0;
+    int g_nbw = 0, d_nbw = 0;  // weight blocks per row of gate/up and of down
+    // call
+    const float* x = nullptr;       // [M][H]
+    const float* logits = nullptr;  // [M][E]
+    int M = 0;
+    float* out = nullptr;  // [M][H]
+    // workspace
+    int32_t* experts = nullptr;  // [M][K]
+    float* weights = nullptr;    // [M][K]
+    float* sgate = nullptr;      // [M] sigmoid(x . selector)
+    int32_t* meta = nullptr;     // [0] number of groups
+    int32_t* group_expert = nullptr;
+    int32_t* group_start = nullptr;
+    int32_t* group_count = nullptr;
+    int32_t* assign_row = nullptr;  // [P] token of each grouped position
+    int32_t* slot_pos = nullptr;    // [M][K] grouped position of (token, route)
+    int32_t* counters = nullptr;    // [M*K+1][ceil(I/256)], zero between calls
+    ActView xq;                     // x quantised, M rows of width H
+    float* act = nullptr;           // [P][I] SwiGLU output
+    ActView aq;                     // act quantised, P rows of width I
+    float* vals = nullptr;          // [P][H] expert outputs before the combine
+};
+
+// Launch prep, gate_up and down for one layer call.
+hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s);
+
+}  // namespace iq

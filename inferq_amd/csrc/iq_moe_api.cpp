@@ -1,0 +1,194 @@
+// iq_moe_api.cpp -- C ABI of the MoE sublayer (include/iq_qgemm.h).
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+#include "../../include/iq_qgemm.h"
+#include "iq_api_internal.h"
+#include "iq_moe.h"
+
+#define IQ_API extern "C" __attribute__((visibility("default")))
+
+struct iq_moe {
+    iq::MoeParams layer;
+    int gfmt = 0, dfmt = 0;
+    std::mutex mu;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    int ws_m = 0;
+};
+
+namespace {
+
+using namespace iq;
+
+constexpr size_t a256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+int64_t row_bytes_of(int dtype, int64_t cols) { return cols / block_elems(dtype) * block_bytes(dtype); }
+
+// Carve the per-call workspace for m tokens; returns its size when base is null.
+size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
+    const int64_t K = L->layer.K, H = L->layer.H, I = L->layer.I;
+    const int64_t na = m * K, gmax = na + 1, P = na + m;
+    const int64_t ngI = (I + 255) / 256;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t* ptr = base ? base + off : nullptr;
+        off += a256(bytes);
+        return ptr;
+    };
+    uint8_t* experts = take(na * 4);
+    uint8_t* weights = take(na * 4);
+    uint8_t* sgate = take(m * 4);
+    uint8_t* meta = take(16);
+    uint8_t* gexp = take(gmax * 4);
+    uint8_t* gstart = take(gmax * 4);
+    uint8_t* gcount = take(gmax * 4);
+    uint8_t* arow = take(P * 4);
+    uint8_t* spos = take(na * 4);
+    uint8_t* ctr = take(gmax * ngI * 4);
+    uint8_t* xq = take(act_bytes(m, H));
+    uint8_t* act = take(P * I * 4);
+    uint8_t* aq = take(act_bytes(P, I));
+    uint8_t* vals = take(P * H * 4);
+    if (p) {
+        p->experts = (int32_t*)experts;
+        p->weights = (float*)weights;
+        p->sgate = (float*)sgate;
+        p->meta = (int32_t*)meta;
+        p->group_expert = (int32_t*)gexp;
+        p->group_start = (int32_t*)gstart;
+        p->group_count = (int32_t*)gcount;
+        p->assign_row = (int32_t*)arow;
+        p->slot_pos = (int32_t*)spos;
+        p->counters = (int32_t*)ctr;
+        p->xq = act_carve(xq, m, H);
+        p->act = (float*)act;
+        p->aq = act_carve(aq, P, I);
+        p->vals = (float*)vals;
+    }
+    (void)ctr;
+    return off;
+}
+
+}  // namespace
+
+IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
+    if (!d || !out) return fail(IQ_ERR_INVALID, "null pointer");
+    const int64_t E = d->n_experts, K = d->top_k, H = d->hidden, I = d->inter;
+    if (!(K > 0 && K <= E)) return fail(IQ_ERR_SHAPE, "invalid top-k %lld for %lld experts", (long long)K, (long long)E);
+    if (E > kMoeMaxExperts || K > kMoeMaxTopK)
+        return fail(IQ_ERR_RANGE, "this build supports at most %d experts and top-%d (got %lld, %lld)", kMoeMaxExperts,
+                    kMoeMaxTopK, (long long)E, (long long)K);
+    if (!dtype_ok(d->gate_dtype) || !dtype_ok(d->down_dtype))
+        return fail(IQ_ERR_DTYPE, "unsupported expert dtypes %d / %d; expected Q4_K, Q6_K or Q8_0", d->gate_dtype,
+                    d->down_dtype);
+    if (H <= 0 || I <= 0 || H % block_elems(d->gate_dtype) || I % block_elems(d->down_dtype) || I % 32)
+        return fail(IQ_ERR_SHAPE, "hidden %lld / intermediate %lld do not fit %s gate and %s down blocks",
+                    (long long)H, (long long)I, dtype_name(d->gate_dtype), dtype_name(d->down_dtype));
+    const int64_t grb = row_bytes_of(d->gate_dtype, H), drb = row_bytes_of(d->down_dtype, I);
+    if (!d->gate || !d->up || !d->down) return fail(IQ_ERR_INVALID, "null expert tensor");
+    if (d->gate_bytes != (size_t)(E * I * grb))
+        return fail(IQ_ERR_SHAPE, "invalid gate expert shape: %zu bytes for [%lld, %lld, %lld] %s", d->gate_bytes,
+                    (long long)E, (long long)I, (long long)H, dtype_name(d->gate_dtype));
+    if (d->up_bytes != d->gate_bytes)
+        return fail(IQ_ERR_SHAPE, "up expert shape (%zu bytes) does not match gate shape (%zu bytes)", d->up_bytes,
+                    d->gate_bytes);
+    if (d->down_bytes != (size_t)(E * H * drb))
+        return fail(IQ_ERR_SHAPE, "invalid down expert shape: %zu bytes for [%lld, %lld, %lld] %s", d->down_bytes,
+                    (long long)E, (long long)H, (long long)I, dtype_name(d->down_dtype));
+    for (const void* ptr : {d->gate, d->up, d->down, (const void*)d->shared_gate, (const void*)d->shared_up,
+                            (const void*)d->shared_down, (const void*)d->selector})
+        if ((uintptr_t)ptr & 15u) return fail(IQ_ERR_INVALID, "device tensors must be 16-byte aligned");
+    const int nshared = (d->shared_gate != nullptr) + (d->shared_up != nullptr) + (d->shared_down != nullptr);
+    if (nshared != 0 && nshared != 3) return fail(IQ_ERR_INVALID, "shared expert needs gate, up and down matrices");
+    if (nshared == 3) {
+        if (!d->selector) return fail(IQ_ERR_INVALID, "shared expert needs its f32 selector vector");
+        if (d->shared_gate_dtype != d->gate_dtype || d->shared_down_dtype != d->down_dtype)
+            return fail(IQ_ERR_DTYPE, "shared expert dtypes %s / %s differ from the routed experts' %s / %s",
+                        dtype_name(d->shared_gate_dtype), dtype_name(d->shared_down_dtype),
+                        dtype_name(d->gate_dtype), dtype_name(d->down_dtype));
+    }
+    iq_moe* L = new iq_moe;
+    MoeParams& p = L->layer;
+    p.H = H;
+    p.I = I;
+    p.E = E;
+    p.K = K;
+    p.normalize = d->normalize ? 1 : 0;
+    p.gate = (const uint8_t*)d->gate;
+    p.up = (const uint8_t*)d->up;
+    p.down = (const uint8_t*)d->down;
+    if (nshared == 3) {
+        p.sgate_w = (const uint8_t*)d->shared_gate;
+        p.sup_w = (const uint8_t*)d->shared_up;
+        p.sdown_w = (const uint8_t*)d->shared_down;
+        p.selector = d->selector;
+    }
+    p.g_row_bytes = grb;
+    p.d_row_bytes = drb;
+    p.g_exp_bytes = I * grb;
+    p.d_exp_bytes = H * drb;
+    p.g_nbw = (int)(H / block_elems(d->gate_dtype));
+    p.d_nbw = (int)(I / block_elems(d->down_dtype));
+    L->gfmt = d->gate_dtype;
+    L->dfmt = d->down_dtype;
+    *out = L;
+    return IQ_OK;
+}
+
+IQ_API int iq_moe_destroy(iq_moe_t L) {
+    if (!L) return IQ_OK;
+    if (L->ws) (void)hipFree(L->ws);
+    delete L;
+    return IQ_OK;
+}
+
+IQ_API int iq_moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
+                          int32_t* experts_out, float* weights_out, iq_stream_t stream) {
+    if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
+    if (m < 0) return fail(IQ_ERR_SHAPE, "negative token count");
+    if (m == 0) return IQ_OK;
+    if (!x || !logits || !out) return fail(IQ_ERR_INVALID, "null input or output pointer");
+    if (m * L->layer.K > kMoeMaxAssign)
+        return fail(IQ_ERR_RANGE, "%lld tokens x top-%lld exceeds %d assignments per call", (long long)m,
+                    (long long)L->layer.K, kMoeMaxAssign);
+    hipStream_t s = (hipStream_t)stream;
+    std::lock_guard<std::mutex> lock(L->mu);
+    if (L->ws_m < m) {
+        const size_t bytes = carve(L, (int)m, nullptr, nullptr);
+        if (L->ws) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+            (void)hipFree(L->ws);
+            L->ws = nullptr;
+            L->ws_m = 0;
+        }
+        hipError_t e = hipMalloc(&L->ws, bytes);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            L->ws = nullptr;
+            return fail(IQ_ERR_OOM, "MoE workspace of %zu bytes: %s", bytes, hipGetErrorString(e));
+        }
+        e = hipMemset(L->ws, 0, bytes);  // the completion counters start at zero
+        if (e != hipSuccess) return hip_fail(e, "hipMemset");
+        L->ws_bytes = bytes;
+        L->ws_m = (int)m;
+    }
+    MoeParams p = L->layer;
+    carve(L, L->ws_m, (uint8_t*)L->ws, &p);
+    // carve() sized the views for ws_m tokens; the call uses m
+    p.xq.m = (int)m;
+    p.x = x;
+    p.logits = logits;
+    p.M = (int)m;
+    p.out = out;
+    hipError_t e = launch_moe(p, L->gfmt, L->dfmt, s);
+    if (e != hipSuccess) return hip_fail(e, "MoE launch");
+    const size_t rb = (size_t)(m * L->layer.K) * 4;
+    if (experts_out && (e = hipMemcpyAsync(experts_out, p.experts, rb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_fail(e, "hipMemcpyAsync (experts)");
+    if (weights_out && (e = hipMemcpyAsync(weights_out, p.weights, rb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_fail(e, "hipMemcpyAsync (weights)");
+    return IQ_OK;
+}

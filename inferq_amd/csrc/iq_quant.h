@@ -1,0 +1,123 @@
+// iq_quant.h -- wave-level activation quantisers, bit-exact to candle
+// 0.11's BlockQ8K::from_float and BlockQ8_0::from_float (called by the
+// reference at src/gguf.rs:648-654).
+//
+// One wave quantises one 256-value group of one row.  Lane l holds values
+// 4l..4l+3, i.e. chunk c = l/8 and lane-in-chunk k = l%8, and writes its
+// packed dword to the lane-transposed position 8k+c of the internal layout.
+#pragma once
+
+#include "iq_device.h"
+
+namespace iq {
+
+__device__ __forceinline__ f32x4 load4(const float* p) {
+    if (((uintptr_t)p & 15u) == 0) return *(const f32x4*)p;
+    return f32x4{p[0], p[1], p[2], p[3]};
+}
+
+__device__ __forceinline__ int sat_i8(float v) {  // Rust `f32 as i8`
+    if (v != v) return 0;
+    v = v < -128.f ? -128.f : v;
+    v = v > 127.f ? 127.f : v;
+    return (int)v;
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// Q8K: xs points at the 256 values of group g of activation row `row`.
+// `ref`, when not null, receives the reference 292-byte block.
+__device__ __forceinline__ void quant_q8k_wave(const float* xs, int64_t row, int g, const ActView& a, uint8_t* ref) {
+    const int lane = threadIdx.x & 63;
+    const f32x4 v = load4(xs + 4 * lane);
+    // amax and the first index reaching it (the reference updates only on a
+    // strictly larger |x| while scanning upwards)
+    float am = 0.f;
+    int idx = 1 << 20;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float ax = fabsf(v[e]);
+        if (am < ax) {
+            am = ax;
+            idx = 4 * lane + e;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float am2 = __shfl_xor(am, off);
+        const int idx2 = __shfl_xor(idx, off);
+        if (am2 > am || (am2 == am && idx2 < idx)) {
+            am = am2;
+            idx = idx2;
+        }
+    }
+    int q[4] = {0, 0, 0, 0};
+    float dval = 0.f;
+    if (am != 0.f) {  // uniform
+        const int e = idx & 3;
+        const float mine = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
+        const float maxv = __shfl(mine, idx >> 2);
+        const float iscale = __fdiv_rn(-128.f, maxv);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float t = roundf(iscale * v[j]);
+            q[j] = sat_i8(t < 127.f ? t : 127.f);
+        }
+        dval = __fdiv_rn(1.f, iscale);
+    }
+    const uint32_t packed = pack4(q[0], q[1], q[2], q[3]);
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    const int bsum16 = s;   // lanes 4j..4j+3: bsums[j]
+    s += __shfl_xor(s, 4);  // lanes 8c..8c+7: sum of 32-value sub-block c
+
+    const int c = lane >> 3, k = lane & 7;
+    uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
+    qrow[perm_dword(c, k)] = packed;
+    if (k == 0) a.s8[(row * a.ng + g) * 8 + c] = (int16_t)s;
+    if (lane == 0) a.d[row * a.ldd + g] = dval;
+    if (ref) {
+        if (lane == 0) *(float*)ref = dval;
+        *(uint32_t*)(ref + 4 + 4 * lane) = packed;
+        if ((lane & 3) == 0) *(int16_t*)(ref + 260 + 2 * (lane >> 2)) = (int16_t)bsum16;
+    }
+}
+
+// Q8_0: the 8 blocks of group g of a row of width k (xrow = row start).
+// `ref_row`, when not null, receives the row's reference 34-byte blocks.
+__device__ __forceinline__ void quant_q80_wave(const float* xrow, int64_t k, int64_t row, int g, const ActView& a,
+                                               uint8_t* ref_row) {
+    const int lane = threadIdx.x & 63;
+    const int c = lane >> 3, kk = lane & 7;
+    const int64_t nb32 = k / 32;
+    const int64_t b = (int64_t)g * 8 + c;  // this lane's Q8_0 block
+    const bool valid = b < nb32;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (valid) v = load4(xrow + b * 32 + 4 * kk);
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = fmaxf(am, __shfl_xor(am, 1));
+    am = fmaxf(am, __shfl_xor(am, 2));
+    am = fmaxf(am, __shfl_xor(am, 4));
+    const float d = __fdiv_rn(am, 127.f);
+    const float id = d != 0.f ? __fdiv_rn(1.f, d) : 0.f;
+    int q[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) q[j] = sat_i8(roundf(v[j] * id));
+    const uint32_t packed = pack4(q[0], q[1], q[2], q[3]);
+    const uint16_t dh = f32_to_f16_rne(d);
+    uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
+    qrow[perm_dword(c, kk)] = packed;  // padding lanes store zeros
+    if (valid && kk == 0) a.d[row * a.ldd + b] = f16_to_f32(dh);
+    if (valid && ref_row) {
+        uint8_t* blk = ref_row + b * 34;
+        if (kk == 0) *(uint16_t*)blk = dh;
+        *(uint16_t*)(blk + 2 + 4 * kk) = (uint16_t)(packed & 0xffffu);
+        *(uint16_t*)(blk + 4 + 4 * kk) = (uint16_t)(packed >> 16);
+    }
+}
+
+}  // namespace iq

@@ -1,0 +1,94 @@
+"""Host-side mirror of the reference's quantised MoE sublayer.
+
+`QuantizedMoeLayer` keeps the interface of inferq's QuantizedMoeLayer
+(src/qwen/quantized_moe.rs:105-460) with the routed experts resident in HBM
+as the GGUF expert tensors and the whole layer (routing, grouped experts,
+SwiGLU, ordered combine, shared expert) run by the gfx950 kernels through
+the C ABI.  The router's logits are an input: the router matmul is not part
+of this path.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+from . import _lib
+from ._lib import MoeDesc, QgemmError, check, lib
+from .qgemm import BLOCK_BYTES, BLOCK_ELEMS, _ensure_init, _stream
+
+
+@dataclass
+class Route:
+    """src/qwen/moe.rs:14-19 (without the logits echo)."""
+
+    experts: list
+    weights: list
+
+
+@dataclass
+class QuantizedMoeOutput:
+    hidden: object  # torch.Tensor [..., hidden]
+    routes: list
+
+
+def _rows_bytes(dtype: int, rows: int, cols: int) -> int:
+    return rows * (cols // BLOCK_ELEMS[dtype]) * BLOCK_BYTES[dtype]
+
+
+class QuantizedMoeLayer:
+    """One MoE sublayer over device tensors (uint8 GGUF bytes, f32 selector)."""
+
+    def __init__(self, hidden: int, inter: int, n_experts: int, top_k: int, gate_dtype: int, down_dtype: int,
+                 gate, up, down, shared_gate=None, shared_up=None, shared_down=None, selector=None,
+                 normalize: bool = True, shared_gate_dtype: int | None = None,
+                 shared_down_dtype: int | None = None):
+        _ensure_init()
+        self.hidden, self.inter, self.n_experts, self.top_k = hidden, inter, n_experts, top_k
+        self._keep = [t for t in (gate, up, down, shared_gate, shared_up, shared_down, selector) if t is not None]
+
+        def ptr(t):
+            return None if t is None else t.data_ptr()
+
+        def nbytes(t):
+            return 0 if t is None else t.numel() * t.element_size()
+
+        desc = MoeDesc(
+            hidden, inter, n_experts, top_k, int(normalize), gate_dtype, down_dtype,
+            ptr(gate), ptr(up), ptr(down), nbytes(gate), nbytes(up), nbytes(down),
+            shared_gate_dtype if shared_gate_dtype is not None else gate_dtype,
+            shared_down_dtype if shared_down_dtype is not None else down_dtype,
+            ptr(shared_gate), ptr(shared_up), ptr(shared_down), ptr(selector),
+        )
+        h = ctypes.c_void_p()
+        check(lib().iq_moe_create(ctypes.byref(desc), ctypes.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and _lib._lib is not None:
+            _lib._lib.iq_moe_destroy(h)
+            self._h = None
+
+    def forward_into(self, xs, router_logits, out, experts=None, weights=None) -> None:
+        """Raw call: device f32 xs [m, hidden], logits [m, n_experts], out [m, hidden]."""
+        m = xs.numel() // self.hidden
+        check(lib().iq_moe_forward(self._h, xs.data_ptr(), router_logits.data_ptr(), m, out.data_ptr(),
+                                   None if experts is None else experts.data_ptr(),
+                                   None if weights is None else weights.data_ptr(), _stream()))
+
+    def forward(self, xs, router_logits) -> QuantizedMoeOutput:
+        """src/qwen/quantized_moe.rs:227: the layer output and the routes."""
+        import torch
+
+        if xs.numel() % self.hidden:
+            raise QgemmError(_lib.IQ_ERR_SHAPE,
+                             f"MoE input element count is not divisible by hidden size {self.hidden}")
+        flat = xs.to(torch.float32).reshape(-1, self.hidden).contiguous()
+        m = flat.shape[0]
+        logits = router_logits.to(torch.float32).reshape(m, self.n_experts).contiguous()
+        out = torch.empty_like(flat)
+        experts = torch.empty(m, self.top_k, dtype=torch.int32, device=flat.device)
+        weights = torch.empty(m, self.top_k, dtype=torch.float32, device=flat.device)
+        self.forward_into(flat, logits, out, experts, weights)
+        e, w = experts.cpu().tolist(), weights.cpu().tolist()
+        return QuantizedMoeOutput(out.reshape(xs.shape), [Route(a, b) for a, b in zip(e, w)])

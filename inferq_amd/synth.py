@@ -60,3 +60,27 @@ def random_matrix(dtype: int, rows: int, cols: int, rng: np.random.Generator) ->
 
 def normal(shape, rng: np.random.Generator) -> np.ndarray:
     return rng.standard_normal(shape, dtype=np.float32)
+
+
+def random_moe_layer(hidden: int, inter: int, n_experts: int, gate_dtype: int, down_dtype: int,
+                     rng: np.random.Generator, shared: bool = True) -> dict:
+    """Byte arrays of one MoE sublayer in GGUF expert-tensor layout:
+    gate/up [E, inter, hidden], down [E, hidden, inter], the shared expert
+    (gate/up [inter, hidden], down [hidden, inter]) and the f32 selector
+    ~ N(0,1)/sqrt(hidden)."""
+    layer = {
+        "hidden": hidden, "inter": inter, "n_experts": n_experts,
+        "gate_dtype": gate_dtype, "down_dtype": down_dtype,
+        "gate": random_matrix(gate_dtype, n_experts * inter, hidden, rng),
+        "up": random_matrix(gate_dtype, n_experts * inter, hidden, rng),
+        "down": random_matrix(down_dtype, n_experts * hidden, inter, rng),
+    }
+    if shared:
+        layer.update({
+            "shared_gate_dtype": gate_dtype, "shared_down_dtype": down_dtype,
+            "shared_gate": random_matrix(gate_dtype, inter, hidden, rng),
+            "shared_up": random_matrix(gate_dtype, inter, hidden, rng),
+            "shared_down": random_matrix(down_dtype, hidden, inter, rng),
+            "selector": (rng.standard_normal(hidden, dtype=np.float32) / np.float32(np.sqrt(hidden))),
+        })
+    return layer
