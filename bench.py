@@ -1,0 +1,424 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantised-matmul hot path on one MI355X.
+
+Headline: one Qwen3.6-35B-A3B-shaped MoE
+sublayer at M=1 -- hidden 2048, 256 experts of [512 x 2048] Q4_K gate/up and
+[2048 x 512] Q6_K down, top-8 routing plus one shared expert.  A step is one
+layer call (routing, grouped gate/up + SwiGLU, down + ordered combine +
+shared expert).  Steps rotate over 40 resident layers (~21 GB of experts, as
+the real model's residency) with fresh N(0,1) inputs and router logits, so
+weights come from HBM, not from the 256 MB Infinity Cache.
+
+Printed JSON line: value = algorithmic HBM bytes per layer / wall time per
+layer (GB/s); roofline = the dominant kernel's algorithmic bytes / its own
+average duration (HIP events on the launch stream); cpu_baseline = the
+oracle's AVX2 restatement of the reference's CPU kernels on this host's
+cores, on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0   # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+H, I, E, TOPK = 2048, 512, 256, 8
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Hip:
+    """hipEvent_t helpers over libamdhip64 (events on the launch stream)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        L = self.lib
+        L.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        L.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        L.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        L.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def events(self, n):
+        out = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            assert self.lib.hipEventCreate(ctypes.byref(e)) == 0
+            out.append(e.value)
+        return out
+
+    def record(self, ev, stream):
+        assert self.lib.hipEventRecord(ev, stream) == 0
+
+    def ms(self, a, b):
+        t = ctypes.c_float()
+        assert self.lib.hipEventElapsedTime(ctypes.byref(t), a, b) == 0
+        return t.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.lib.hipEventDestroy(e)
+
+
+def make_layers(n_layers, device, seed):
+    """Resident expert tensors of n_layers MoE layers (native GGUF layout)."""
+    import torch
+
+    from inferq_amd import moe, synth
+
+    layers = []
+    for li in range(n_layers):
+        s = seed + 1000 * li
+        t = {
+            "gate": synth.random_matrix_device(synth.Q4_K, E * I, H, device, s + 1),
+            "up": synth.random_matrix_device(synth.Q4_K, E * I, H, device, s + 2),
+            "down": synth.random_matrix_device(synth.Q6_K, E * H, I, device, s + 3),
+            "shared_gate": synth.random_matrix_device(synth.Q4_K, I, H, device, s + 4),
+            "shared_up": synth.random_matrix_device(synth.Q4_K, I, H, device, s + 5),
+            "shared_down": synth.random_matrix_device(synth.Q6_K, H, I, device, s + 6),
+        }
+        g = torch.Generator(device=device)
+        g.manual_seed(s + 7)
+        t["selector"] = torch.randn(H, device=device, generator=g) / float(np.sqrt(H))
+        m = moe.QuantizedMoeLayer(H, I, E, TOPK, synth.Q4_K, synth.Q6_K, t["gate"], t["up"], t["down"],
+                                  t["shared_gate"], t["shared_up"], t["shared_down"], t["selector"])
+        layers.append((m, t))
+    return layers
+
+
+def expert_bytes():
+    from inferq_amd import synth
+
+    gu = 2 * synth.matrix_bytes(synth.Q4_K, I, H)
+    dn = synth.matrix_bytes(synth.Q6_K, H, I)
+    return gu, dn
+
+
+def moe_kernel_bytes(m, unique):
+    """Algorithmic HBM bytes per launch of the three MoE kernels for m tokens
+    routed to `unique` distinct experts (plus the shared expert)."""
+    gu, dn = expert_bytes()
+    g = unique + 1
+    rows = m * TOPK + m                       # grouped activation rows
+    xq = m * (H + H // 256 * (4 + 16))        # quantised x: int8 + scale + sub-block sums
+    aq = rows * (I + I // 256 * (4 + 16))     # quantised SwiGLU output
+    prep = m * E * 4 + m * H * 4 + xq
+    gate_up = g * gu + xq + rows * I * 4 + aq
+    down = g * dn + aq + rows * H * 4 + m * H * 4
+    return {"prep": prep, "gate_up": gate_up, "down": down}
+
+
+def time_moe(layers, xs, logits, out, steps, warmup, hip, stream):
+    """Warm up, then time `steps` layer calls (rotating layers); returns wall
+    ms per call and the per-kernel durations of every timed call."""
+    import torch
+
+    n = len(layers)
+    for i in range(warmup):
+        layers[i % n][0].forward_into(xs[i], logits[i], out)
+    torch.cuda.synchronize()
+    evs = hip.events(4 * steps)
+    t0, t1 = hip.events(2)
+    torch.cuda.synchronize()
+    hip.record(t0, stream)
+    for s in range(steps):
+        i = warmup + s
+        layers[i % n][0].forward_timed(xs[i], logits[i], out, evs[4 * s:4 * s + 4])
+    hip.record(t1, stream)
+    torch.cuda.synchronize()
+    wall = hip.ms(t0, t1) / steps
+    per = {"prep": [], "gate_up": [], "down": []}
+    for s in range(steps):
+        e = evs[4 * s:4 * s + 4]
+        per["prep"].append(hip.ms(e[0], e[1]))
+        per["gate_up"].append(hip.ms(e[1], e[2]))
+        per["down"].append(hip.ms(e[2], e[3]))
+    hip.destroy(evs + [t0, t1])
+    return wall, per
+
+
+def time_moe_graph(layers, xs, logits, out, steps, warmup, hip):
+    """The same `steps` layer calls captured once in a HIP graph and
+    replayed: wall ms per layer call without host submission gaps; then,
+    for each of the two kernels, a graph of `steps` launches of that kernel
+    alone (each layer re-running its last call's stage), giving its average
+    duration per launch (graph node gaps included)."""
+    import torch
+
+    n = len(layers)
+    cap = torch.cuda.Stream()
+    t0, t1 = hip.events(2)
+
+    def replay(capture):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            capture()
+        graph.replay()  # warm
+        torch.cuda.synchronize()
+        hip.record(t0, cap.cuda_stream)
+        graph.replay()
+        hip.record(t1, cap.cuda_stream)
+        torch.cuda.synchronize()
+        return hip.ms(t0, t1) / steps
+
+    with torch.cuda.stream(cap):
+        for i in range(warmup):
+            layers[i % n][0].forward_into(xs[i], logits[i], out)
+        torch.cuda.synchronize()
+
+        def full():
+            for s_ in range(steps):
+                i = warmup + s_
+                layers[i % n][0].forward_into(xs[i], logits[i], out)
+
+        wall = replay(full)
+        per = {}
+        for stage, name in ((1, "gate_up"), (2, "down")):
+            per[name] = replay(lambda st=stage: [layers[(warmup + s_) % n][0].forward_stage(st) for s_ in range(steps)])
+    hip.destroy([t0, t1])
+    return wall, per
+
+
+def time_calls(fn, iters, hip, stream, warmup=3):
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0, t1 = hip.events(2)
+    hip.record(t0, stream)
+    for i in range(iters):
+        fn(warmup + i)
+    hip.record(t1, stream)
+    torch.cuda.synchronize()
+    ms = hip.ms(t0, t1) / iters
+    hip.destroy([t0, t1])
+    return ms
+
+
+def host_layer(t):
+    d = {k: v.cpu().numpy() for k, v in t.items()}
+    from inferq_amd import synth
+
+    d.update(hidden=H, inter=I, n_experts=E, top_k=TOPK, normalize=True, gate_dtype=synth.Q4_K,
+             down_dtype=synth.Q6_K, shared_gate_dtype=synth.Q4_K, shared_down_dtype=synth.Q6_K)
+    return d
+
+
+def cpu_threads():
+    n = os.cpu_count() or 1
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n)), 16))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def secondary(args, hip, stream, device, layers):
+    """Other BASELINE configs, reported beside the headline (not the value)."""
+    import torch
+
+    from inferq_amd import qgemm, synth
+
+    extra = {}
+    # config 1: Q8_0 [4096 x 2048] matvec, rotated over copies beyond the MALL
+    copies = 64
+    mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q8_0, 4096, 2048, device, 50 + c),
+                                       synth.Q8_0, 4096, 2048) for c in range(copies)]
+    x = torch.randn(2048, 2048, device=device).reshape(-1, 1, 2048)
+    y = torch.empty(1, 4096, device=device)
+    ms = time_calls(lambda i: mats[i % copies].forward_into(x[i % 2048], y), args.steps, hip, stream)
+    b = mats[0].storage_bytes() + 2048 * 4 + 4096 * 4
+    extra["q8_0_matvec_4096x2048"] = {"us": round(ms * 1e3, 3), "GB_s": round(b / ms / 1e6, 1),
+                                      "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    del mats
+    # LM head [248320 x 2048] Q6_K, M=1 (417 MB: larger than the MALL)
+    lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 60),
+                                    synth.Q6_K, 248320, 2048)
+    yl = torch.empty(1, 248320, device=device)
+    ms = time_calls(lambda i: lm.forward_into(x[i % 2048], yl), max(10, args.steps // 10), hip, stream)
+    b = lm.storage_bytes() + 2048 * 4 + 248320 * 4
+    extra["lm_head_q6k_248320x2048_m1"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1),
+                                           "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    x8 = torch.randn(8, 2048, device=device)
+    y8 = torch.empty(8, 248320, device=device)
+    ms = time_calls(lambda i: lm.forward_into(x8, y8), 10, hip, stream, warmup=2)
+    extra["lm_head_q6k_m8"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1)}
+    del lm
+    # config 3: verify pass MoE at M = 4 and 8 (independent routing per row)
+    n = len(layers)
+    g = torch.Generator(device=device)
+    g.manual_seed(77)
+    for m in (4, 8):
+        xs = torch.randn(64, m, H, device=device, generator=g)
+        lg = torch.randn(64, m, E, device=device, generator=g)
+        out = torch.empty(m, H, device=device)
+        ms = time_calls(lambda i: layers[i % n][0].forward_into(xs[i % 64], lg[i % 64], out), 40, hip, stream)
+        uniq = float(np.mean([len(torch.unique(torch.topk(lg[j], TOPK, dim=1).indices)) for j in range(64)]))
+        kb = moe_kernel_bytes(m, uniq)
+        tot = kb["gate_up"] + kb["down"] + kb["prep"]
+        extra[f"moe_layer_m{m}"] = {"us": round(ms * 1e3, 2), "unique_experts": round(uniq, 1),
+                                    "GB_s": round(tot / ms / 1e6, 1), "frac_hbm": round(tot / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    return extra
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=40, help="resident MoE layers rotated over (40 = the model)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
+    ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="run one device copy of this many MiB first (PMC byte-counter calibration)")
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        log(f"bench.py: --gpus {args.gpus} is not supported: this build measures the hot path on one GPU "
+            "(the multi-GPU split is a design in DESIGN.md, not implemented).")
+        sys.exit(2)
+
+    import torch
+
+    from inferq_amd import qgemm
+
+    device = torch.device("cuda", 0)
+    qgemm.init(0)
+    hip = Hip()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    if args.copy_probe_mb:
+        n = args.copy_probe_mb * (1 << 20)
+        src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    t = time.time()
+    layers = make_layers(args.layers, device, args.seed)
+    torch.cuda.synchronize()
+    log(f"built {args.layers} resident MoE layers in {time.time() - t:.1f}s")
+
+    total = args.warmup + args.steps
+    g = torch.Generator(device=device)
+    g.manual_seed(args.seed)
+    xs = torch.randn(total, 1, H, device=device, generator=g)
+    logits = torch.randn(total, 1, E, device=device, generator=g)
+    out = torch.empty(1, H, device=device)
+
+    eager_ms, eager_per = time_moe(layers, xs, logits, out, args.steps, args.warmup, hip, stream)
+    wall_ms, per = time_moe_graph(layers, xs, logits, out, args.steps, args.warmup, hip)
+    kb = moe_kernel_bytes(1, TOPK)
+    gu, dn = expert_bytes()
+    layer_bytes = 9 * (gu + dn) + H * 4 + E * 4 + H * 4
+    value = layer_bytes / (wall_ms * 1e-3) / 1e9
+    avg = {k: float(v) for k, v in per.items()}
+    dom = max(avg, key=avg.get)
+    achieved = kb[dom] / (avg[dom] * 1e-3) / 1e9
+    log(f"MoE layer M=1: {wall_ms * 1e3:.2f} us/layer (graph replay), {value:.0f} GB/s; "
+        f"eager {eager_ms * 1e3:.2f} us/layer; kernels alone (us per launch in a graph): "
+        + ", ".join(f"{k} {v * 1e3:.2f}" for k, v in avg.items()))
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get(f"moe_{dom}")
+
+    result = {
+        "metric": "Q4_K MoE-layer us & HBM GB/s (%peak) at M=1; int8 TOPS at prefill width 256",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot (Q4_K/Q6_K x Q8K), f32 accumulate",
+        "data": "synthetic: random GGUF blocks, N(0,1) activations and router logits",
+        "config": {"workload": "configs[1]: Qwen3.6-35B-A3B-shaped MoE layer at M=1 (256 experts, top-8 + 1 shared, "
+                               "hidden 2048, moe_intermediate 512, Q4_K gate/up, Q6_K down)",
+                   "layers_rotated": args.layers,
+                   "resident_expert_bytes": args.layers * E * (gu + dn),
+                   "algorithmic_bytes_per_layer": layer_bytes},
+        "us_per_layer": round(wall_ms * 1e3, 3),
+        "timing": "HIP graph of the timed steps replayed once, HIP events on the launch stream; per-kernel: graph of "
+                  "the timed steps' launches of that kernel alone",
+        "eager_us_per_layer": round(eager_ms * 1e3, 3),
+        "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "kernel_us": {k: round(v * 1e3, 3) for k, v in avg.items()},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": kb[dom], "avg_us": round(avg[dom] * 1e3, 3)},
+    }
+
+    if not args.no_parity:
+        from oracle import oracle as O
+
+        li = (args.warmup + args.steps - 1) % args.layers
+        hl = host_layer(layers[li][1])
+        xi, li_ = xs[-1].cpu().numpy(), logits[-1].cpu().numpy()
+        got = layers[li][0].forward(xs[-1], logits[-1])
+        ref, re, _ = O.moe_forward(hl, xi, li_, mode=0, impl=1 if O.have_avx2() else 0, nthreads=cpu_threads())
+        h = got.hidden.cpu().numpy()
+        err = float(np.abs(h.astype(np.float64) - ref).max() / np.abs(ref).max())
+        result["parity"] = {"routes_equal": [r.experts for r in got.routes] == re.tolist(),
+                            "normwise_rel_err": err, "bitexact_fraction":
+                                float((h.view(np.uint32) == ref.view(np.uint32)).mean()), "tolerance": 1e-4}
+        log(f"parity vs oracle: {result['parity']}")
+        if args.cpu_seconds > 0:
+            nt = cpu_threads()
+            rng = np.random.default_rng(5)
+            xh = rng.standard_normal((64, 1, H), dtype=np.float32)
+            lh = rng.standard_normal((64, 1, E), dtype=np.float32)
+            impl = 1 if O.have_avx2() else 0
+            O.moe_forward(hl, xh[0], lh[0], mode=0, impl=impl, nthreads=nt)
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < args.cpu_seconds:
+                O.moe_forward(hl, xh[n % 64], lh[n % 64], mode=0, impl=impl, nthreads=nt)
+                n += 1
+            dt = (time.perf_counter() - t0) / n
+            result["cpu_baseline"] = {
+                "value": round(layer_bytes / dt / 1e9, 2), "unit": "GB/s", "cores": nt,
+                "kind": "port", "us_per_layer": round(dt * 1e6, 1),
+                "sample": f"{n} MoE-layer calls (M=1, token-major, {'AVX2' if impl else 'scalar'} restatement of "
+                          f"the reference kernels) on one resident layer, {nt} threads, {cpu_model()}",
+            }
+            log(f"cpu baseline: {result['cpu_baseline']}")
+
+    if not args.no_secondary:
+        result["extra"] = secondary(args, hip, stream, device, layers)
+        result["extra"]["prefill_int8_tops"] = None
+        log(f"secondary: {result['extra']}")
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -168,6 +168,24 @@ int iq_moe_destroy(iq_moe_t moe);
 int iq_moe_forward(iq_moe_t moe, const float *x, const float *router_logits, int64_t m, float *out,
                    int32_t *experts_out, float *weights_out, iq_stream_t stream);
 
+/* iq_moe_forward, also recording events[0..3] (hipEvent_t handles created by
+ * the caller) on `stream`: before the routing launch, then after the
+ * routing, gate/up and down launches.  Consecutive event pairs time the
+ * three kernels.
+ * Replaces: the per-stage QuantizedMoeTimings the reference collects
+ * (src/qwen/quantized_moe.rs:67-96, :252-275). */
+int iq_moe_forward_timed(iq_moe_t moe, const float *x, const float *router_logits, int64_t m, float *out,
+                         int32_t *experts_out, float *weights_out, void *const events[4], iq_stream_t stream);
+
+/* Launch one stage of the last iq_moe_forward call on this handle again,
+ * with the same inputs: stage 1 = the gate/up launch, stage 2 = the down
+ * launch (the M = 1 path; stage 0 = the routing launch of the grouped
+ * path).  The outputs are identical to that call's.  For timing a single
+ * kernel in isolation.
+ * Replaces: the per-stage timers of QuantizedMoeTimings
+ * (src/qwen/quantized_moe.rs:67-96). */
+int iq_moe_forward_stage(iq_moe_t moe, int stage, iq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,8 @@ _SIGNATURES = {
     "iq_moe_create": ([P, ctypes.POINTER(P)], INT),
     "iq_moe_destroy": ([P], INT),
     "iq_moe_forward": ([P, P, P, I64, P, P, P, P], INT),
+    "iq_moe_forward_timed": ([P, P, P, I64, P, P, P, ctypes.POINTER(P), P], INT),
+    "iq_moe_forward_stage": ([P, INT, P], INT),
 }
 
 

@@ -39,12 +39,17 @@ struct Q4W {
     u32x4a16 hdr;   // d, dmin, scales[12]
     uint32_t q[4];  // qs dwords 32j + 4k
 };
+// Q6_K lane data.  A block at 2 (mod 4) is loaded as aligned dword pairs
+// whose byte funnel shift (by `sh` bytes) is applied at use, so that a burst
+// of loads is never interrupted by waits for earlier ones.
 struct Q6W {
-    uint32_t ql[4];  // ql windows 32i + 4k
-    uint32_t qh[2];  // qh windows 32j + 4k
-    uint32_t sc[4];  // scales[16]
+    u32x2 ql[4];  // ql windows 32i + 4k
+    u32x2 qh[2];  // qh windows 32j + 4k
+    u32x2 sc[4];  // scales[16]
     uint32_t d;
+    uint32_t sh;
 };
+__device__ __forceinline__ uint32_t q6win(u32x2 v, uint32_t sh) { return __builtin_amdgcn_alignbyte(v.y, v.x, sh); }
 struct Q8W {
     uint32_t q[8];  // qs window 2 + 4k of the 8 blocks of a group
     uint32_t d[8];
@@ -74,26 +79,38 @@ __device__ __forceinline__ void load_q4(const uint8_t* blk, int k, Q4W& w) {
     for (int j = 0; j < 4; j++) w.q[j] = ld32(blk + 16 + 32 * j + 4 * k);
 }
 
-__device__ __forceinline__ void load_q6(const uint8_t* blk, int k, Q6W& w) {
-    if (((uintptr_t)blk & 3u) == 0) {
+// Q6_K block known to start at 0 (mod 4): exact dword loads.
+__device__ __forceinline__ void load_q6_a0(const uint8_t* blk, int k, Q6W& w) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) w.ql[i] = ld32(blk + 32 * i + 4 * k);
+    for (int i = 0; i < 4; i++) w.ql[i] = u32x2{ld32(blk + 32 * i + 4 * k), 0u};
 #pragma unroll
-        for (int j = 0; j < 2; j++) w.qh[j] = ld32(blk + 128 + 32 * j + 4 * k);
-#pragma unroll
-        for (int t = 0; t < 4; t++) w.sc[t] = ld32(blk + 192 + 4 * t);
-    } else {
-        // A block at 2 (mod 4) always follows another block of the same
-        // 4-byte aligned matrix, so the two bytes before it are readable,
-        // and every window here ends at least 2 bytes before the block end.
-#pragma unroll
-        for (int i = 0; i < 4; i++) w.ql[i] = ld32_m2(blk + 32 * i + 4 * k);
-#pragma unroll
-        for (int j = 0; j < 2; j++) w.qh[j] = ld32_m2(blk + 128 + 32 * j + 4 * k);
-#pragma unroll
-        for (int t = 0; t < 4; t++) w.sc[t] = ld32_m2(blk + 192 + 4 * t);
-    }
+    for (int j = 0; j < 2; j++) w.qh[j] = u32x2{ld32(blk + 128 + 32 * j + 4 * k), 0u};
+    const u32x4 sc = *(const u32x4*)(blk + 192);
+    w.sc[0] = u32x2{sc.x, 0u};
+    w.sc[1] = u32x2{sc.y, 0u};
+    w.sc[2] = u32x2{sc.z, 0u};
+    w.sc[3] = u32x2{sc.w, 0u};
     w.d = ld16(blk + 208);
+    w.sh = 0;
+}
+// Q6_K block known to start at 2 (mod 4): each window is the aligned dword
+// pair around it.  The two bytes before the block belong to the previous
+// block of the same row, and every window ends at least 2 bytes before the
+// block's end, so nothing outside the matrix is read.
+__device__ __forceinline__ void load_q6_a2(const uint8_t* blk, int k, Q6W& w) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) w.ql[i] = *(const u32x2*)(blk + 32 * i + 4 * k - 2);
+#pragma unroll
+    for (int j = 0; j < 2; j++) w.qh[j] = *(const u32x2*)(blk + 128 + 32 * j + 4 * k - 2);
+#pragma unroll
+    for (int t = 0; t < 4; t++) w.sc[t] = *(const u32x2*)(blk + 192 + 4 * t - 2);
+    w.d = ld16(blk + 208);
+    w.sh = 2;
+}
+
+__device__ __forceinline__ void load_q6(const uint8_t* blk, int k, Q6W& w) {
+    if (((uintptr_t)blk & 3u) == 0) load_q6_a0(blk, k, w);
+    else load_q6_a2(blk, k, w);
 }
 
 __device__ __forceinline__ void load_q8(const uint8_t* row, int64_t b0, int nbw, int k, Q8W& w) {
@@ -118,6 +135,78 @@ __device__ __forceinline__ void load_act(const ActView& a, int64_t r, int g, int
     av[4] = a1.x; av[5] = a1.y; av[6] = a1.z; av[7] = a1.w;
 }
 
+// ---- one block of one row for lane k, split into a per-row decode (shared
+// by every input row) and a per-input dot.  Term values are exactly the
+// reference's: isum/msum the i32 lanes, d = y.d * xd, dmin = -y.d * xdmin.
+struct Q4Dec {
+    uint32_t lo[4], hi[4];
+    int sc[8];
+    int mA, mB;
+    float xd, xdmin;
+};
+__device__ __forceinline__ Q4Dec q4_decode(const Q4W& wb, int k) {
+    Q4Dec r;
+    const Q4Scales s = q4_scales(wb.hdr.y, wb.hdr.z, wb.hdr.w);
+    r.xd = f16_to_f32(wb.hdr.x);
+    r.xdmin = f16_to_f32(wb.hdr.x >> 16);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        r.sc[t] = byte_of(s.sc_lo, t);
+        r.sc[t + 4] = byte_of(s.sc_hi, t);
+    }
+    // mins 2k and 2k+1 for lanes k < 4 (lanes 4..7 hold an unused copy)
+    const uint32_t mw = (k & 2) ? s.mn_hi : s.mn_lo;
+    r.mA = byte_of(mw, 2 * (k & 1));
+    r.mB = byte_of(mw, 2 * (k & 1) + 1);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        r.lo[j] = wb.q[j] & 0x0f0f0f0fu;
+        r.hi[j] = (wb.q[j] >> 4) & 0x0f0f0f0fu;
+    }
+    return r;
+}
+__device__ __forceinline__ void q4_dot(const Q4Dec& r, const uint32_t (&av)[8], float yd, uint32_t q8s, int32_t& isum,
+                                       int32_t& msum, float& d, float& dmin) {
+    isum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) isum += r.sc[2 * j] * sdot4(r.lo[j], av[2 * j], 0) + r.sc[2 * j + 1] * sdot4(r.hi[j], av[2 * j + 1], 0);
+    msum = r.mA * (int32_t)(int16_t)(q8s & 0xffffu) + r.mB * (int32_t)(int16_t)(q8s >> 16);
+    d = yd * r.xd;
+    dmin = -yd * r.xdmin;
+}
+
+struct Q6Dec {
+    uint32_t v[8];
+    int sc[8];
+    float xd;
+};
+__device__ __forceinline__ Q6Dec q6_decode(const Q6W& wb, int k) {
+    Q6Dec r;
+    r.xd = f16_to_f32(wb.d);
+    const int hk = k >= 4;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t l = q6win(wb.ql[2 * j + (i & 1)], wb.sh);
+            const uint32_t lo = i < 2 ? (l & 0x0f0f0f0fu) : ((l >> 4) & 0x0f0f0f0fu);
+            const uint32_t hi = ((q6win(wb.qh[j], wb.sh) >> (2 * i)) & 0x03030303u) << 4;
+            // bytes q6 - 32: q6 + 0x60 never carries out of a byte, and xor
+            // 0x80 maps it to two's complement
+            r.v[4 * j + i] = ((lo | hi) + 0x60606060u) ^ 0x80808080u;
+            const int t = 8 * j + 2 * i + hk;  // this lane's scale
+            r.sc[4 * j + i] = (int)(int8_t)(uint8_t)(q6win(wb.sc[t >> 2], wb.sh) >> (8 * (t & 3)));
+        }
+    }
+    return r;
+}
+__device__ __forceinline__ void q6_dot(const Q6Dec& r, const uint32_t (&av)[8], float yd, int32_t& isum, float& d) {
+    isum = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++) isum += r.sc[c] * sdot4(r.v[c], av[c], 0);
+    d = yd * r.xd;
+}
+
 // Optional per-block lane integers (parity hook).
 struct DbgOut {
     int32_t* isum = nullptr;
@@ -125,6 +214,158 @@ struct DbgOut {
     int64_t n = 0, row = 0;
     int nbw = 0;
 };
+
+// Issue the weight loads of blocks [g0, g0+BC) of R rows (nullptr rows and
+// blocks past ng load nothing and decode as zero).
+template <int FMT, int R, int BC>
+__device__ __forceinline__ void lanes_load(const uint8_t* const (&wrow)[R], int g0, int ng, int nbw, int k,
+                                           typename WT<FMT>::T (&w)[R][BC]) {
+    using W = typename WT<FMT>::T;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int bi = 0; bi < BC; bi++) {
+            const int g = g0 + bi;
+            if (g < ng && wrow[r] != nullptr) {
+                if constexpr (FMT == kQ4_K) load_q4(wrow[r] + (int64_t)g * 144, k, w[r][bi]);
+                else if constexpr (FMT == kQ6_K) load_q6(wrow[r] + (int64_t)g * 210, k, w[r][bi]);
+                else load_q8(wrow[r], (int64_t)g * 8, nbw, k, w[r][bi]);
+            } else {
+                w[r][bi] = W{};
+            }
+        }
+    }
+}
+
+// lanes_load for exactly NG blocks per row with no control flow at all, so
+// the whole burst issues back to back: every wrow[r] must be a readable row
+// (callers point unused jobs at a used row and discard the results).
+template <int FMT, int R, int NG>
+__device__ __forceinline__ void lanes_load_exact(const uint8_t* const (&wrow)[R], int k,
+                                                 typename WT<FMT>::T (&w)[R][NG]) {
+    static_assert(FMT != kQ8_0, "lanes_load_exact covers the K-quants");
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            if constexpr (FMT == kQ4_K) {
+                load_q4(wrow[r] + (int64_t)g * 144, k, w[r][g]);
+            } else if constexpr (NG % 2 == 0) {
+                // rows of an even number of 210-byte blocks are 4-byte
+                // aligned, so block g starts at 2g (mod 4)
+                if (g % 2 == 0) load_q6_a0(wrow[r] + (int64_t)g * 210, k, w[r][g]);
+                else load_q6_a2(wrow[r] + (int64_t)g * 210, k, w[r][g]);
+            } else {
+                load_q6(wrow[r] + (int64_t)g * 210, k, w[r][g]);
+            }
+        }
+    }
+    // keep every consumer of the loaded data below the whole burst, so no
+    // register of the burst is recycled (and waited for) mid-burst
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Advance the lane accumulators over blocks [g0, g0+BC) (see lanes_dot).
+template <int FMT, int MT, int R, int BC, bool DBG = false>
+__device__ __forceinline__ void lanes_accumulate(const typename WT<FMT>::T (&w)[R][BC], const uint8_t* const (&wrow)[R],
+                                                 int g0, int ng, int nbw, const ActView& a,
+                                                 const int64_t (&arow)[R][MT], const int (&mc)[R], int k,
+                                                 float (&acc)[R][MT], float (&accm)[R][MT],
+                                                 const DbgOut& dbg = DbgOut{}) {
+    using W = typename WT<FMT>::T;
+#pragma unroll
+    for (int bi = 0; bi < BC; bi++) {
+        const int g = g0 + bi;
+        if (g >= ng) break;  // uniform
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (mc[r] <= 0) continue;  // uniform: a job with no rows reads nothing
+            const W& wb = w[r][bi];
+            if constexpr (FMT == kQ4_K) {
+                const Q4Dec dec = q4_decode(wb, k);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    if (mi < mc[r]) {
+                        const int64_t ar = arow[r][mi];
+                        uint32_t av[8];
+                        load_act(a, ar, g, k, av);
+                        const float yd = a.d[ar * a.ldd + g];
+                        const uint32_t q8s = *(const uint32_t*)(a.s8 + (ar * a.ng + g) * 8 + 2 * (k & 3));
+                        int32_t isum, msum;
+                        float d, dmin;
+                        q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
+                        acc[r][mi] = __builtin_fmaf(d, (float)isum, acc[r][mi]);
+                        accm[r][mi] = __builtin_fmaf(dmin, (float)msum, accm[r][mi]);
+                        if constexpr (DBG) {
+                            if (wrow[r]) {
+                                const int64_t base = ((ar * dbg.n + dbg.row) * dbg.nbw + g);
+                                dbg.isum[base * 8 + k] = isum;
+                                if (k < 4) dbg.msum[base * 4 + k] = msum;
+                            }
+                        }
+                    }
+                }
+            } else if constexpr (FMT == kQ6_K) {
+                const Q6Dec dec = q6_decode(wb, k);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    if (mi < mc[r]) {
+                        const int64_t ar = arow[r][mi];
+                        uint32_t av[8];
+                        load_act(a, ar, g, k, av);
+                        const float yd = a.d[ar * a.ldd + g];
+                        int32_t isum;
+                        float d;
+                        q6_dot(dec, av, yd, isum, d);
+                        acc[r][mi] = __builtin_fmaf(d, (float)isum, acc[r][mi]);
+                        if constexpr (DBG) {
+                            if (wrow[r]) dbg.isum[((ar * dbg.n + dbg.row) * dbg.nbw + g) * 8 + k] = isum;
+                        }
+                    }
+                }
+            } else {  // Q8_0: a group is 8 consecutive 32-value blocks
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    if (mi < mc[r]) {
+                        const int64_t ar = arow[r][mi];
+                        uint32_t av[8];
+                        load_act(a, ar, g, k, av);
+                        const float* dp = a.d + ar * a.ldd + (int64_t)g * 8;
+                        const f32x4 d0 = *(const f32x4*)dp, d1 = *(const f32x4*)(dp + 4);
+                        const float yd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                        for (int c = 0; c < 8; c++) {
+                            if ((int64_t)g * 8 + c < nbw) {  // uniform
+                                const int32_t dot = sdot4(wb.q[c], av[c], 0);
+                                acc[r][mi] = __builtin_fmaf(f16_to_f32(wb.d[c]) * yd[c], (float)dot, acc[r][mi]);
+                                if constexpr (DBG) {
+                                    if (wrow[r])
+                                        dbg.isum[((ar * dbg.n + dbg.row) * dbg.nbw + (int64_t)g * 8 + c) * 8 + k] = dot;
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// The 8 lanes of each row combine: hsum_f32_8 (+ hsum_f32_4 of the Q4_K
+// mins).  out[r][i] is valid in lane k == 0 of each group.
+template <int FMT, int MT, int R>
+__device__ __forceinline__ void lanes_finish(const float (&acc)[R][MT], const float (&accm)[R][MT],
+                                             float (&out)[R][MT]) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int mi = 0; mi < MT; mi++) {
+            float v = hsum8(acc[r][mi]);
+            if constexpr (FMT == kQ4_K) v = v + hsum4(accm[r][mi]);
+            out[r][mi] = v;
+        }
+    }
+}
 
 // R jobs of one lane: weight row base (nullptr when the row is outside the
 // matrix), activation rows arow[r][0..mc[r]) with mc[r] wave-uniform.
@@ -140,148 +381,12 @@ __device__ __forceinline__ void lanes_dot(const uint8_t* const (&wrow)[R], int n
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[r][i] = accm[r][i] = 0.f;
-
     for (int g0 = 0; g0 < ng; g0 += BC) {
         W w[R][BC];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int bi = 0; bi < BC; bi++) {
-                const int g = g0 + bi;
-                if (g < ng && wrow[r] != nullptr) {
-                    if constexpr (FMT == kQ4_K) load_q4(wrow[r] + (int64_t)g * 144, k, w[r][bi]);
-                    else if constexpr (FMT == kQ6_K) load_q6(wrow[r] + (int64_t)g * 210, k, w[r][bi]);
-                    else load_q8(wrow[r], (int64_t)g * 8, nbw, k, w[r][bi]);
-                } else {
-                    w[r][bi] = W{};
-                }
-            }
-        }
-#pragma unroll
-        for (int bi = 0; bi < BC; bi++) {
-            const int g = g0 + bi;
-            if (g >= ng) break;  // uniform
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const W& wb = w[r][bi];
-                if constexpr (FMT == kQ4_K) {
-                    const Q4Scales s = q4_scales(wb.hdr.y, wb.hdr.z, wb.hdr.w);
-                    const float xd = f16_to_f32(wb.hdr.x), xdmin = f16_to_f32(wb.hdr.x >> 16);
-                    int sc[8];
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        sc[t] = byte_of(s.sc_lo, t);
-                        sc[t + 4] = byte_of(s.sc_hi, t);
-                    }
-                    // mins 2k and 2k+1 for lanes k < 4 (lanes 4..7 hold an
-                    // unused copy)
-                    const uint32_t mw = (k & 2) ? s.mn_hi : s.mn_lo;
-                    const int mA = byte_of(mw, 2 * (k & 1)), mB = byte_of(mw, 2 * (k & 1) + 1);
-                    uint32_t lo[4], hi[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        lo[j] = wb.q[j] & 0x0f0f0f0fu;
-                        hi[j] = (wb.q[j] >> 4) & 0x0f0f0f0fu;
-                    }
-#pragma unroll
-                    for (int mi = 0; mi < MT; mi++) {
-                        if (mi < mc[r]) {
-                            const int64_t ar = arow[r][mi];
-                            uint32_t av[8];
-                            load_act(a, ar, g, k, av);
-                            const float yd = a.d[ar * a.ldd + g];
-                            const uint32_t q8s = *(const uint32_t*)(a.s8 + (ar * ng + g) * 8 + 2 * (k & 3));
-                            int32_t isum = 0;
-#pragma unroll
-                            for (int j = 0; j < 4; j++)
-                                isum += sc[2 * j] * sdot4(lo[j], av[2 * j], 0) +
-                                        sc[2 * j + 1] * sdot4(hi[j], av[2 * j + 1], 0);
-                            const int32_t msum =
-                                mA * (int32_t)(int16_t)(q8s & 0xffffu) + mB * (int32_t)(int16_t)(q8s >> 16);
-                            acc[r][mi] = __builtin_fmaf(yd * xd, (float)isum, acc[r][mi]);
-                            accm[r][mi] = __builtin_fmaf(-yd * xdmin, (float)msum, accm[r][mi]);
-                            if constexpr (DBG) {
-                                if (wrow[r]) {
-                                    const int64_t base = ((ar * dbg.n + dbg.row) * dbg.nbw + g);
-                                    dbg.isum[base * 8 + k] = isum;
-                                    if (k < 4) dbg.msum[base * 4 + k] = msum;
-                                }
-                            }
-                        }
-                    }
-                } else if constexpr (FMT == kQ6_K) {
-                    const float xd = f16_to_f32(wb.d);
-                    const int hk = k >= 4;
-                    uint32_t v[8];
-                    int sc[8];
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const uint32_t l = wb.ql[2 * j + (i & 1)];
-                            const uint32_t lo = i < 2 ? (l & 0x0f0f0f0fu) : ((l >> 4) & 0x0f0f0f0fu);
-                            const uint32_t hi = ((wb.qh[j] >> (2 * i)) & 0x03030303u) << 4;
-                            // bytes q6 - 32: q6 + 0x60 never carries out of a
-                            // byte, and xor 0x80 maps it to two's complement
-                            v[4 * j + i] = ((lo | hi) + 0x60606060u) ^ 0x80808080u;
-                            const int t = 8 * j + 2 * i + hk;  // this lane's scale
-                            sc[4 * j + i] = (int)(int8_t)(uint8_t)(wb.sc[t >> 2] >> (8 * (t & 3)));
-                        }
-                    }
-#pragma unroll
-                    for (int mi = 0; mi < MT; mi++) {
-                        if (mi < mc[r]) {
-                            const int64_t ar = arow[r][mi];
-                            uint32_t av[8];
-                            load_act(a, ar, g, k, av);
-                            const float yd = a.d[ar * a.ldd + g];
-                            int32_t isum = 0;
-#pragma unroll
-                            for (int c = 0; c < 8; c++) isum += sc[c] * sdot4(v[c], av[c], 0);
-                            acc[r][mi] = __builtin_fmaf(yd * xd, (float)isum, acc[r][mi]);
-                            if constexpr (DBG) {
-                                if (wrow[r]) dbg.isum[((ar * dbg.n + dbg.row) * dbg.nbw + g) * 8 + k] = isum;
-                            }
-                        }
-                    }
-                } else {  // Q8_0: a group is 8 consecutive 32-value blocks
-#pragma unroll
-                    for (int mi = 0; mi < MT; mi++) {
-                        if (mi < mc[r]) {
-                            const int64_t ar = arow[r][mi];
-                            uint32_t av[8];
-                            load_act(a, ar, g, k, av);
-                            const float* dp = a.d + ar * a.ldd + (int64_t)g * 8;
-                            const f32x4 d0 = *(const f32x4*)dp, d1 = *(const f32x4*)(dp + 4);
-                            const float yd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-#pragma unroll
-                            for (int c = 0; c < 8; c++) {
-                                if ((int64_t)g * 8 + c < nbw) {  // uniform
-                                    const int32_t dot = sdot4(wb.q[c], av[c], 0);
-                                    acc[r][mi] = __builtin_fmaf(f16_to_f32(wb.d[c]) * yd[c], (float)dot, acc[r][mi]);
-                                    if constexpr (DBG) {
-                                        if (wrow[r])
-                                            dbg.isum[((ar * dbg.n + dbg.row) * dbg.nbw + (int64_t)g * 8 + c) * 8 + k] =
-                                                dot;
-                                    }
-                                }
-                            }
-                        }
-                    }
-                }
-            }
-        }
+        lanes_load<FMT, R, BC>(wrow, g0, ng, nbw, k, w);
+        lanes_accumulate<FMT, MT, R, BC, DBG>(w, wrow, g0, ng, nbw, a, arow, mc, k, acc, accm, dbg);
     }
-
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-#pragma unroll
-        for (int mi = 0; mi < MT; mi++) {
-            float v = hsum8(acc[r][mi]);
-            if constexpr (FMT == kQ4_K) v = v + hsum4(accm[r][mi]);
-            out[r][mi] = v;
-        }
-    }
+    lanes_finish<FMT, MT, R>(acc, accm, out);
 }
 
 }  // namespace iq

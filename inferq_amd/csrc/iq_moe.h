@@ -45,6 +45,11 @@ struct MoeParams {
 };
 
 // Launch prep, gate_up and down for one layer call.
-hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s);
+// events (may be null): 4 hipEvent_t recorded before and between the launches.
+hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
+                      hipEvent_t const* events = nullptr);
+// One launch of a call already made with these parameters (stage 0 routing
+// of the grouped path, 1 gate/up, 2 down).
+hipError_t launch_moe_stage(const MoeParams& p, int gate_dtype, int down_dtype, int stage, hipStream_t s);
 
 }  // namespace iq

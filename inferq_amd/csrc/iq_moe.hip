@@ -21,6 +21,7 @@
 #include "iq_lanes.h"
 #include "iq_moe.h"
 #include "iq_quant.h"
+#include "iq_route.h"
 
 namespace iq {
 
@@ -30,7 +31,7 @@ constexpr int kMaxAssign = kMoeMaxAssign;
 
 // ---------------------------------------------------------------- routing
 __device__ void route_and_group(const MoeParams& p) {
-    __shared__ float s_ev[4][kMoeMaxExperts];
+    __shared__ __align__(16) float s_ev[4][kMoeMaxExperts];
     __shared__ int s_exp[kMaxAssign];
     __shared__ int s_cnt[kMoeMaxExperts];
     __shared__ int s_sg[256], s_sc[256];
@@ -38,87 +39,22 @@ __device__ void route_and_group(const MoeParams& p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = (int)p.E, K = (int)p.K, M = p.M;
-    constexpr int PER = kMoeMaxExperts / 64;
 
     for (int t = wave; t < M; t += 4) {
-        const float* lg = p.logits + (int64_t)t * E;
-        float ev[PER];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int i = lane + 64 * j;
-            ev[j] = i < E ? lg[i] : -INFINITY;
-            mx = fmaxf(mx, ev[j]);
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int i = lane + 64 * j;
-            ev[j] = i < E ? exp_f32(ev[j] - mx) : 0.f;
-            if (i < E) s_ev[wave][i] = ev[j];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // The softmax denominator is a sequential f32 sum in index order.
-        float den = 0.f;
-        for (int i = 0; i < E; i++) den = den + s_ev[wave][i];
-        float pr[PER];
-#pragma unroll
-        for (int j = 0; j < PER; j++) pr[j] = __fdiv_rn(ev[j], den);
-
-        // top-k by probability, descending; equal probabilities keep index order
-        uint32_t taken = 0;
-        int sel_e[kMoeMaxTopK];
-        float sel_p[kMoeMaxTopK];
-        for (int s = 0; s < K; s++) {
-            float bp = -1.f;
-            int bi = 0x7fffffff;
-#pragma unroll
-            for (int j = 0; j < PER; j++) {
-                const int i = lane + 64 * j;
-                // a NaN probability ranks below every number (the reference's
-                // partial_cmp treats it as equal to everything)
-                const float pv = pr[j] == pr[j] ? pr[j] : -0.5f;
-                if (i < E && !((taken >> j) & 1u) && pv > bp) {
-                    bp = pv;
-                    bi = i;
-                }
-            }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float op = __shfl_xor(bp, off);
-                const int oi = __shfl_xor(bi, off);
-                if (op > bp || (op == bp && oi < bi)) {
-                    bp = op;
-                    bi = oi;
-                }
-            }
-            if (bi != 0x7fffffff && (bi & 63) == lane) taken |= 1u << (bi >> 6);
-            sel_e[s] = bi;
-            sel_p[s] = bp;
-        }
-        if (p.normalize) {
-            float sum = 0.f;
-            for (int s = 0; s < K; s++) sum = sum + sel_p[s];
-            for (int s = 0; s < K; s++) sel_p[s] = __fdiv_rn(sel_p[s], sum);
-        }
+        int sel[kMoeMaxTopK];
+        float lv[kRoutePer], w[kMoeMaxTopK];
+        route_topk<kMoeMaxTopK>(p.logits + (int64_t)t * E, E, K, sel, lv);
+        route_weights<kMoeMaxTopK>(lv, E, K, sel, p.normalize, s_ev[wave], w);
         if (lane == 0) {
             for (int s = 0; s < K; s++) {
-                p.experts[t * K + s] = sel_e[s];
-                p.weights[t * K + s] = sel_p[s];
-                s_exp[t * K + s] = sel_e[s];
+                p.experts[t * K + s] = sel[s];
+                p.weights[t * K + s] = w[s];
+                s_exp[t * K + s] = sel[s];
             }
         }
         if (p.selector) {
-            // x . selector (candle's f32 gemm order is not visible; a tree
-            // reduction is used), then sigmoid = 1 / (exp(-v) + 1)
-            float part = 0.f;
-            for (int64_t h = lane; h < p.H; h += 64) part = part + p.x[t * p.H + h] * p.selector[h];
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
-            if (lane == 0) p.sgate[t] = __fdiv_rn(1.f, exp_f32(-part) + 1.f);
+            const float gate = selector_gate(p.x + (int64_t)t * p.H, p.selector, p.H);
+            if (lane == 0) p.sgate[t] = gate;
         }
     }
     __syncthreads();
@@ -329,9 +265,242 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeParams p) {
     }
 }
 
+// ------------------------------------------------ M = 1 (decode) kernels
+// One token: no grouping is needed, so the routing is recomputed where it
+// is used and each launch has a single dependent memory round trip before
+// its weight loads (logits -> weights).
+
+constexpr int kMoe1MaxSlots = 12;  // top-k routes plus the shared expert
+
+// Routing workgroup of the M = 1 gate/up launch: wave 0 routes the token
+// (top-k, exact softmax weights), wave 1 computes the shared-expert gate.
+// Both run beside the matmul workgroups, off their critical path.
+__device__ void moe1_route(const MoeParams& p, int wave) {
+    const int K = (int)p.K, E = (int)p.E, lane = threadIdx.x & 63;
+    __shared__ __align__(16) float s_scratch[kMoeMaxExperts];
+    if (wave == 0) {
+        float lv[kRoutePer], wt[kMoe1MaxSlots];
+        int sel[kMoe1MaxSlots];
+        route_load(p.logits, E, lv);
+        route_topk_any<kMoe1MaxSlots>(lv, E, K, sel);
+        route_weights<kMoe1MaxSlots>(lv, E, K, sel, p.normalize, s_scratch, wt);
+        if (lane == 0) {
+            for (int s = 0; s < K; s++) {
+                p.experts[s] = sel[s];
+                p.weights[s] = wt[s];
+            }
+        }
+    } else if (wave == 1 && p.sdown_w) {
+        const float gate = selector_gate(p.x, p.selector, p.H);
+        if (lane == 0) p.sgate[0] = gate;
+    }
+}
+
+// Grid (I/8, slots + 1).  Workgroup (x, s < slots): 8 intermediate rows of
+// gate and up of the expert at route rank s (or the shared expert), 4 waves
+// each taking a quarter of the NG blocks along hidden.  Each wave forms its
+// blocks' exact lane integers and f32 scales; wave 0 then advances the
+// accumulators through all NG blocks in order (the reference's chain),
+// reduces them with the hsum trees, applies SwiGLU and stores act[s][i].
+// Row slots + 1 holds the routing workgroup (x == 0).
+template <int GFMT, int NG>
+__global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
+    constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
+    static_assert(NG % NW == 0 && (VPL == 8 || VPL == 16 || VPL == 32), "shape");
+    __shared__ __align__(16) int8_t s_q[NG * 256];
+    __shared__ __align__(16) float s_d[NG * 8];
+    __shared__ __align__(16) int16_t s_s8[NG * 8];
+    __shared__ int s_isum[2][8][8][NG];  // [gate/up][row][lane k][block]
+    __shared__ int s_msum[2][8][4][NG];
+    __shared__ float s_dd[2][8][NG], s_dm[2][8][NG];
+    const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int K = (int)p.K;
+    const int nslots = K + (p.sdown_w ? 1 : 0);
+    const int sidx = blockIdx.y;
+    if (sidx == nslots) {
+        if (blockIdx.x == 0) moe1_route(p, wave);
+        return;
+    }
+    // small inputs first: logits, and this wave's x blocks
+    constexpr int LPB = 256 / VPL;
+    const int g0 = wave * NB;
+    const int gx = g0 + lane / LPB;  // x block this lane quantises
+    float lv[kRoutePer], xv[VPL];
+    route_load(p.logits, (int)p.E, lv);
+    q8k_vpl_load<VPL>(p.x + (int64_t)gx * 256, xv);
+    int e = (int)p.E;
+    if (sidx < K) {
+        int sel[kMoe1MaxSlots];
+        route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
+        e = sel[sidx];
+    }
+    const bool shared = sidx >= K;
+    const uint8_t* gb = shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes;
+    const uint8_t* ub = shared ? p.sup_w : p.up + (int64_t)e * p.g_exp_bytes;
+    const int64_t i = (int64_t)blockIdx.x * 8 + slot;
+    const bool ok = i < p.I;
+    const int64_t ic = ok ? i : p.I - 1;
+    const uint8_t* wrow[2] = {gb + ic * p.g_row_bytes + (int64_t)g0 * WT<GFMT>::kBlockBytes,
+                              ub + ic * p.g_row_bytes + (int64_t)g0 * WT<GFMT>::kBlockBytes};
+    typename WT<GFMT>::T w[2][NB];
+    lanes_load_exact<GFMT, 2, NB>(wrow, k, w);
+    ActView a;
+    a.ng = NG;
+    a.ldq = NG * 256;
+    a.ldd = NG * 8;
+    a.m = 1;
+    a.q = s_q;
+    a.d = s_d;
+    a.s8 = s_s8;
+    quant_q8k_vpl<VPL>(xv, true, 0, gx, a);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int g = g0 + b;
+            uint32_t av[8];
+            load_act(a, 0, g, k, av);
+            const float yd = a.d[g];
+            if constexpr (GFMT == kQ4_K) {
+                const Q4Dec dec = q4_decode(w[r][b], k);
+                const uint32_t q8s = *(const uint32_t*)(a.s8 + g * 8 + 2 * (k & 3));
+                int32_t isum, msum;
+                float d, dmin;
+                q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
+                s_isum[r][slot][k][g] = isum;
+                if (k < 4) s_msum[r][slot][k][g] = msum;
+                if (k == 0) {
+                    s_dd[r][slot][g] = d;
+                    s_dm[r][slot][g] = dmin;
+                }
+            } else {
+                const Q6Dec dec = q6_decode(w[r][b], k);
+                int32_t isum;
+                float d;
+                q6_dot(dec, av, yd, isum, d);
+                s_isum[r][slot][k][g] = isum;
+                if (k == 0) s_dd[r][slot][g] = d;
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float o[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        float acc = 0.f, accm = 0.f;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            acc = __builtin_fmaf(s_dd[r][slot][g], (float)s_isum[r][slot][k][g], acc);
+            if constexpr (GFMT == kQ4_K) accm = __builtin_fmaf(s_dm[r][slot][g], (float)s_msum[r][slot][k & 3][g], accm);
+        }
+        float v = hsum8(acc);
+        if constexpr (GFMT == kQ4_K) v = v + hsum4(accm);
+        o[r] = v;
+    }
+    // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
+    if (k == 0 && ok) p.act[(int64_t)sidx * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
+}
+
+// Grid H/8; one wave per route slot (blockDim 64 * slots), all on the same
+// 8 hidden rows.  Each wave loads its slot's expert id and SwiGLU row, issues
+// its down-row burst, quantises the SwiGLU row into LDS while the weights
+// fly, and forms the row products; the 8 rows are then combined in route
+// order (multiply, then add) plus shared * gate.
+template <int DFMT, int NG>
+__global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
+    constexpr int VPL = NG * 4;  // SwiGLU values per lane (I = NG * 256)
+    static_assert(VPL == 8 || VPL == 16 || VPL == 32, "shape");
+    __shared__ __align__(16) int8_t s_q[kMoe1MaxSlots * NG * 256];
+    __shared__ __align__(16) float s_d[kMoe1MaxSlots * NG * 8];
+    __shared__ __align__(16) int16_t s_s8[kMoe1MaxSlots * NG * 8];
+    __shared__ float s_vals[kMoe1MaxSlots][8];
+    const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = route slot
+    const int K = (int)p.K;
+    const bool has_shared = p.sdown_w != nullptr;
+    const int nslots = K + (has_shared ? 1 : 0);
+    constexpr int LPB = 256 / VPL;
+    const int gq = lane / LPB;
+    float av[VPL];
+    q8k_vpl_load<VPL>(p.act + (int64_t)wave * p.I + (int64_t)gq * 256, av);
+    const int e = wave < K ? __builtin_amdgcn_readfirstlane(p.experts[wave]) : 0;
+    const int64_t n = (int64_t)blockIdx.x * 8 + slot;
+    const bool ok = n < p.H;
+    const int64_t nc = ok ? n : p.H - 1;
+    const uint8_t* base = wave < K ? p.down + (int64_t)e * p.d_exp_bytes : p.sdown_w;
+    const uint8_t* wrow[1] = {base + nc * p.d_row_bytes};
+    typename WT<DFMT>::T w[1][NG];
+    lanes_load_exact<DFMT, 1, NG>(wrow, k, w);
+    ActView a;
+    a.ng = NG;
+    a.ldq = NG * 256;
+    a.ldd = NG * 8;
+    a.m = nslots;
+    a.q = s_q;
+    a.d = s_d;
+    a.s8 = s_s8;
+    quant_q8k_vpl<VPL>(av, true, wave, gq, a);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float acc[1][1] = {{0.f}}, accm[1][1] = {{0.f}};
+    const int64_t arow[1][1] = {{wave}};
+    const int mc[1] = {1};
+    lanes_accumulate<DFMT, 1, 1, NG>(w, wrow, 0, NG, p.d_nbw, a, arow, mc, k, acc, accm);
+    float o[1][1];
+    lanes_finish<DFMT, 1, 1>(acc, accm, o);
+    if (k == 0) s_vals[wave][slot] = o[0][0];
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        const int64_t nn = (int64_t)blockIdx.x * 8 + threadIdx.x;
+        if (nn < p.H) {
+            float v = 0.f;
+            for (int j = 0; j < K; j++) v = v + s_vals[j][threadIdx.x] * p.weights[j];
+            if (has_shared) v = v + s_vals[K][threadIdx.x] * p.sgate[0];
+            p.out[nn] = v;
+        }
+    }
+}
+
+// The M = 1 kernels cover K-quant experts with hidden 2048 and
+// intermediate 512 (Qwen3.6-35B-A3B and Qwen3-Next); other shapes take the
+// grouped path.
+bool moe1_supported(const MoeParams& p, int gfmt, int dfmt) {
+    const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
+    return p.M == 1 && gfmt != kQ8_0 && dfmt != kQ8_0 && p.H == 2048 && p.I == 512 && nslots <= kMoe1MaxSlots &&
+           p.E <= kMoeMaxExperts;
+}
+
+template <int GFMT, int DFMT>
+hipError_t launch_moe1(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
+    const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
+    if (ev) (void)hipEventRecord(ev[1], s);
+    hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1), dim3(256), 0, s, p);
+    if (hipError_t e = hipGetLastError()) return e;
+    if (ev) (void)hipEventRecord(ev[2], s);
+    hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8)), dim3(64 * nslots), 0, s, p);
+    if (hipError_t e = hipGetLastError()) return e;
+    if (ev) (void)hipEventRecord(ev[3], s);
+    return hipSuccess;
+}
+
+template <int GFMT>
+hipError_t launch_moe1_g(const MoeParams& p, int dfmt, hipStream_t s, hipEvent_t const* ev) {
+    switch (dfmt) {
+    case kQ4_K: return launch_moe1<GFMT, kQ4_K>(p, s, ev);
+    case kQ6_K: return launch_moe1<GFMT, kQ6_K>(p, s, ev);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 // ------------------------------------------------------------- launchers
 template <int GFMT, int DFMT>
-hipError_t launch_gd(const MoeParams& p, hipStream_t s) {
+hipError_t launch_gd(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
     constexpr int GAF = GFMT == kQ8_0 ? kQ8_0 : kQ4_K;  // activation format of x
     constexpr int DAF = DFMT == kQ8_0 ? kQ8_0 : kQ4_K;  // activation format of act
     const int gmax = p.M * (int)p.K + 1;
@@ -340,40 +509,81 @@ hipError_t launch_gd(const MoeParams& p, hipStream_t s) {
     if (p.M == 1) {
         hipLaunchKernelGGL((k_moe_gate_up<GFMT, DAF, 1, GFMT == kQ8_0 ? 4 : 8>), dim3(tilesI, gmax), dim3(256), 0, s, p);
         if (hipError_t e = hipGetLastError()) return e;
+        if (ev) (void)hipEventRecord(ev[2], s);
         hipLaunchKernelGGL((k_moe_down<DFMT, 1, 3, 2>), dim3(groupsH), dim3(256), 0, s, p);
     } else {
         hipLaunchKernelGGL((k_moe_gate_up<GFMT, DAF, 8, GFMT == kQ8_0 ? 2 : 4>), dim3(tilesI, gmax), dim3(256), 0, s, p);
         if (hipError_t e = hipGetLastError()) return e;
+        if (ev) (void)hipEventRecord(ev[2], s);
         hipLaunchKernelGGL((k_moe_down<DFMT, 8, 2, 2>), dim3(groupsH), dim3(256), 0, s, p);
     }
     (void)GAF;
-    return hipGetLastError();
+    if (hipError_t e = hipGetLastError()) return e;
+    if (ev) (void)hipEventRecord(ev[3], s);
+    return hipSuccess;
 }
 
 template <int GFMT>
-hipError_t launch_g(const MoeParams& p, int dfmt, hipStream_t s) {
+hipError_t launch_g(const MoeParams& p, int dfmt, hipStream_t s, hipEvent_t const* ev) {
     switch (dfmt) {
-    case kQ4_K: return launch_gd<GFMT, kQ4_K>(p, s);
-    case kQ6_K: return launch_gd<GFMT, kQ6_K>(p, s);
-    case kQ8_0: return launch_gd<GFMT, kQ8_0>(p, s);
+    case kQ4_K: return launch_gd<GFMT, kQ4_K>(p, s, ev);
+    case kQ6_K: return launch_gd<GFMT, kQ6_K>(p, s, ev);
+    case kQ8_0: return launch_gd<GFMT, kQ8_0>(p, s, ev);
     default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
-hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s) {
+hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hipEvent_t const* ev) {
+    if (moe1_supported(p, gfmt, dfmt)) {
+        if (ev) (void)hipEventRecord(ev[0], s);
+        switch (gfmt) {
+        case kQ4_K: return launch_moe1_g<kQ4_K>(p, dfmt, s, ev);
+        case kQ6_K: return launch_moe1_g<kQ6_K>(p, dfmt, s, ev);
+        default: return hipErrorInvalidValue;
+        }
+    }
     const int64_t qwaves = (int64_t)p.M * p.xq.ng;
     const unsigned prep_blocks = 1 + (unsigned)((qwaves + 3) / 4);
+    if (ev) (void)hipEventRecord(ev[0], s);
     if (gfmt == kQ8_0) hipLaunchKernelGGL((k_moe_prep<kQ8_0>), dim3(prep_blocks), dim3(256), 0, s, p);
     else hipLaunchKernelGGL((k_moe_prep<kQ4_K>), dim3(prep_blocks), dim3(256), 0, s, p);
     if (hipError_t e = hipGetLastError()) return e;
+    if (ev) (void)hipEventRecord(ev[1], s);
     switch (gfmt) {
-    case kQ4_K: return launch_g<kQ4_K>(p, dfmt, s);
-    case kQ6_K: return launch_g<kQ6_K>(p, dfmt, s);
-    case kQ8_0: return launch_g<kQ8_0>(p, dfmt, s);
+    case kQ4_K: return launch_g<kQ4_K>(p, dfmt, s, ev);
+    case kQ6_K: return launch_g<kQ6_K>(p, dfmt, s, ev);
+    case kQ8_0: return launch_g<kQ8_0>(p, dfmt, s, ev);
     default: return hipErrorInvalidValue;
     }
+}
+
+}  // namespace iq
+
+namespace iq {
+
+namespace {
+template <int GFMT, int DFMT>
+hipError_t stage_moe1(const MoeParams& p, int stage, hipStream_t s) {
+    const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
+    if (stage == 1)
+        hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1), dim3(256), 0, s, p);
+    else if (stage == 2)
+        hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8)), dim3(64 * nslots), 0, s, p);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_moe_stage(const MoeParams& p, int gfmt, int dfmt, int stage, hipStream_t s) {
+    if (!moe1_supported(p, gfmt, dfmt)) return hipErrorNotSupported;
+    if (gfmt == kQ4_K && dfmt == kQ6_K) return stage_moe1<kQ4_K, kQ6_K>(p, stage, s);
+    if (gfmt == kQ4_K && dfmt == kQ4_K) return stage_moe1<kQ4_K, kQ4_K>(p, stage, s);
+    if (gfmt == kQ6_K && dfmt == kQ6_K) return stage_moe1<kQ6_K, kQ6_K>(p, stage, s);
+    if (gfmt == kQ6_K && dfmt == kQ4_K) return stage_moe1<kQ6_K, kQ4_K>(p, stage, s);
+    return hipErrorNotSupported;
 }
 
 }  // namespace iq

@@ -11,6 +11,8 @@
 
 struct iq_moe {
     iq::MoeParams layer;
+    iq::MoeParams last;  // parameters of the last forward call
+    bool has_last = false;
     int gfmt = 0, dfmt = 0;
     std::mutex mu;
     void* ws = nullptr;
@@ -144,8 +146,8 @@ IQ_API int iq_moe_destroy(iq_moe_t L) {
     return IQ_OK;
 }
 
-IQ_API int iq_moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
-                          int32_t* experts_out, float* weights_out, iq_stream_t stream) {
+static int moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
+                       int32_t* experts_out, float* weights_out, void* const* events, iq_stream_t stream) {
     if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
     if (m < 0) return fail(IQ_ERR_SHAPE, "negative token count");
     if (m == 0) return IQ_OK;
@@ -183,12 +185,38 @@ IQ_API int iq_moe_forward(iq_moe_t L, const float* x, const float* logits, int64
     p.logits = logits;
     p.M = (int)m;
     p.out = out;
-    hipError_t e = launch_moe(p, L->gfmt, L->dfmt, s);
+    hipError_t e = launch_moe(p, L->gfmt, L->dfmt, s, (hipEvent_t const*)events);
     if (e != hipSuccess) return hip_fail(e, "MoE launch");
+    L->last = p;
+    L->has_last = true;
     const size_t rb = (size_t)(m * L->layer.K) * 4;
     if (experts_out && (e = hipMemcpyAsync(experts_out, p.experts, rb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
         return hip_fail(e, "hipMemcpyAsync (experts)");
     if (weights_out && (e = hipMemcpyAsync(weights_out, p.weights, rb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
         return hip_fail(e, "hipMemcpyAsync (weights)");
+    return IQ_OK;
+}
+
+IQ_API int iq_moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
+                          int32_t* experts_out, float* weights_out, iq_stream_t stream) {
+    return moe_forward(L, x, logits, m, out, experts_out, weights_out, nullptr, stream);
+}
+
+IQ_API int iq_moe_forward_timed(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
+                                int32_t* experts_out, float* weights_out, void* const events[4],
+                                iq_stream_t stream) {
+    if (!events || !events[0] || !events[1] || !events[2] || !events[3])
+        return fail(IQ_ERR_INVALID, "iq_moe_forward_timed needs four events");
+    return moe_forward(L, x, logits, m, out, experts_out, weights_out, events, stream);
+}
+
+IQ_API int iq_moe_forward_stage(iq_moe_t L, int stage, iq_stream_t stream) {
+    if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
+    std::lock_guard<std::mutex> lock(L->mu);
+    if (!L->has_last) return fail(IQ_ERR_INVALID, "iq_moe_forward_stage needs a previous iq_moe_forward call");
+    hipError_t e = launch_moe_stage(L->last, L->gfmt, L->dfmt, stage, (hipStream_t)stream);
+    if (e == hipErrorNotSupported)
+        return fail(IQ_ERR_RANGE, "stage launches cover the single-token path of this layer shape only");
+    if (e != hipSuccess) return hip_fail(e, "MoE stage launch");
     return IQ_OK;
 }

@@ -121,3 +121,229 @@ __device__ __forceinline__ void quant_q80_wave(const float* xrow, int64_t k, int
 }
 
 }  // namespace iq
+
+namespace iq {
+
+// 64-lane DPP helpers for 8-lane groups (xor 1, xor 2 within a quad; xor 4
+// by swizzle) on 32-bit payloads.
+__device__ __forceinline__ int xor_lane_i(int v, int mask) {
+    if (mask == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    if (mask == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    return __builtin_amdgcn_ds_swizzle(v, 0x101F);
+}
+
+// Load this lane's 32 values for quant8_q8k_vals (chunk l % 8 of the
+// 256-value block at `src`; zeros when src is null).  Issued separately so
+// callers can put these loads ahead of others in the memory queue.
+__device__ __forceinline__ void q8k_chunk_load(const float* src, float (&v)[32]) {
+    const int c = threadIdx.x & 7;
+    if (src) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const f32x4 t = load4(src + 32 * c + 4 * j);
+            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) v[j] = 0.f;
+    }
+}
+
+// One pass over up to 8 Q8K blocks: lane l quantises chunk c = l % 8 (32
+// values, from q8k_chunk_load) of block l / 8 into row `row`, group `g` of
+// `a` (live == false: an idle 8-lane group).  All 64 lanes must call it.
+// Same arithmetic as quant_q8k_wave.
+__device__ __forceinline__ void quant8_q8k_vals(const float (&v)[32], bool live, int64_t row, int g,
+                                                const ActView& a) {
+    const int c = threadIdx.x & 7;
+    // first index of the largest |x| in this chunk, then across the 8 chunks
+    float am = 0.f, mv = 0.f;
+    int idx = 1 << 20;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const float ax = fabsf(v[j]);
+        if (am < ax) {
+            am = ax;
+            mv = v[j];
+            idx = 32 * c + j;
+        }
+    }
+#pragma unroll
+    for (int mask = 1; mask <= 4; mask <<= 1) {
+        const float am2 = __builtin_bit_cast(float, xor_lane_i(__builtin_bit_cast(int, am), mask));
+        const float mv2 = __builtin_bit_cast(float, xor_lane_i(__builtin_bit_cast(int, mv), mask));
+        const int idx2 = xor_lane_i(idx, mask);
+        if (am2 > am || (am2 == am && idx2 < idx)) {
+            am = am2;
+            mv = mv2;
+            idx = idx2;
+        }
+    }
+    if (!live) return;
+    int q[32];
+    float dval = 0.f;
+    if (am != 0.f) {  // uniform per 8-lane group
+        const float iscale = __fdiv_rn(-128.f, mv);
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const float t = roundf(iscale * v[j]);
+            q[j] = sat_i8(t < 127.f ? t : 127.f);
+        }
+        dval = __fdiv_rn(1.f, iscale);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) q[j] = 0;
+    }
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 32; j++) s += q[j];
+    uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++)
+        qrow[perm_dword(c, kk)] = pack4(q[4 * kk], q[4 * kk + 1], q[4 * kk + 2], q[4 * kk + 3]);
+    a.s8[(row * a.ng + g) * 8 + c] = (int16_t)s;
+    if (c == 0) a.d[row * a.ldd + g] = dval;
+}
+
+__device__ __forceinline__ void quant8_q8k(const float* src, int64_t row, int g, const ActView& a) {
+    float v[32];
+    q8k_chunk_load(src, v);
+    quant8_q8k_vals(v, src != nullptr, row, g, a);
+}
+
+// Load the 32 values of one Q8_0 block (zeros when src is null).
+__device__ __forceinline__ void q80_block_load(const float* src, float (&v)[32]) {
+    if (src) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const f32x4 t = load4(src + 4 * j);
+            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) v[j] = 0.f;
+    }
+}
+
+// One pass over up to 64 Q8_0 blocks: lane l quantises one 32-value block
+// (from q80_block_load) into block b of row `row` of `a`.  Same arithmetic
+// as quant_q80_wave.
+__device__ __forceinline__ void quant64_q80_vals(const float (&v)[32], bool live, int64_t row, int64_t b,
+                                                 const ActView& a) {
+    if (!live) return;
+    float am = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) am = fmaxf(am, fabsf(v[j]));
+    const float d = __fdiv_rn(am, 127.f);
+    const float id = d != 0.f ? __fdiv_rn(1.f, d) : 0.f;
+    const int g = (int)(b / 8), c = (int)(b % 8);
+    uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++)
+        qrow[perm_dword(c, kk)] = pack4(sat_i8(roundf(v[4 * kk] * id)), sat_i8(roundf(v[4 * kk + 1] * id)),
+                                        sat_i8(roundf(v[4 * kk + 2] * id)), sat_i8(roundf(v[4 * kk + 3] * id)));
+    a.d[row * a.ldd + b] = f16_to_f32(f32_to_f16_rne(d));
+}
+
+__device__ __forceinline__ void quant64_q80(const float* src, int64_t row, int64_t b, const ActView& a) {
+    float v[32];
+    q80_block_load(src, v);
+    quant64_q80_vals(v, src != nullptr, row, b, a);
+}
+
+}  // namespace iq
+
+namespace iq {
+
+// xor-exchange across lanes for any mask < 32 (DPP for 1 and 2, swizzle
+// otherwise), 32-bit payload.
+__device__ __forceinline__ int xor_lane_any(int v, int mask) {
+    switch (mask) {
+    case 1: return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    case 2: return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    case 4: return __builtin_amdgcn_ds_swizzle(v, 0x101F);
+    case 8: return __builtin_amdgcn_ds_swizzle(v, 0x201F);
+    default: return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+    }
+}
+
+// Q8K with VPL values per lane (8, 16 or 32): a block spans LPB = 256/VPL
+// lanes and a wave covers 64/LPB blocks; lane l holds values
+// VPL*(l % LPB) .. +VPL of its block.  q8k_vpl_load fetches them (zeros when
+// src, the block start, is null); quant_q8k_vpl quantises the block into
+// row `row`, group `g` of `a` (live == false: skip the stores).  Same
+// arithmetic as quant_q8k_wave.
+template <int VPL>
+__device__ __forceinline__ void q8k_vpl_load(const float* src, float (&v)[VPL]) {
+    constexpr int LPB = 256 / VPL;
+    const int pl = (threadIdx.x & 63) % LPB;
+    if (src) {
+#pragma unroll
+        for (int j = 0; j < VPL / 4; j++) {
+            const f32x4 t = load4(src + VPL * pl + 4 * j);
+            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < VPL; j++) v[j] = 0.f;
+    }
+}
+
+template <int VPL>
+__device__ __forceinline__ void quant_q8k_vpl(const float (&v)[VPL], bool live, int64_t row, int g,
+                                              const ActView& a) {
+    constexpr int LPB = 256 / VPL, LPC = 32 / VPL > 0 ? 32 / VPL : 1;
+    static_assert(VPL == 8 || VPL == 16 || VPL == 32, "VPL");
+    const int pl = (threadIdx.x & 63) % LPB;
+    float am = 0.f, mv = 0.f;
+    int idx = 1 << 20;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) {
+        const float ax = fabsf(v[j]);
+        if (am < ax) {
+            am = ax;
+            mv = v[j];
+            idx = VPL * pl + j;
+        }
+    }
+#pragma unroll
+    for (int mask = 1; mask < LPB; mask <<= 1) {
+        const float am2 = __builtin_bit_cast(float, xor_lane_any(__builtin_bit_cast(int, am), mask));
+        const float mv2 = __builtin_bit_cast(float, xor_lane_any(__builtin_bit_cast(int, mv), mask));
+        const int idx2 = xor_lane_any(idx, mask);
+        if (am2 > am || (am2 == am && idx2 < idx)) {
+            am = am2;
+            mv = mv2;
+            idx = idx2;
+        }
+    }
+    int q[VPL];
+    float dval = 0.f;
+    if (am != 0.f) {
+        const float iscale = __fdiv_rn(-128.f, mv);
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            const float t = roundf(iscale * v[j]);
+            q[j] = sat_i8(t < 127.f ? t : 127.f);
+        }
+        dval = __fdiv_rn(1.f, iscale);
+    } else {
+#pragma unroll
+        for (int j = 0; j < VPL; j++) q[j] = 0;
+    }
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) s += q[j];
+#pragma unroll
+    for (int mask = 1; mask < LPC; mask <<= 1) s += xor_lane_any(s, mask);
+    if (!live) return;
+    const int c = (VPL * pl) / 32, kk0 = ((VPL * pl) % 32) / 4;
+    uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
+#pragma unroll
+    for (int t = 0; t < VPL / 4; t++)
+        qrow[perm_dword(c, kk0 + t)] = pack4(q[4 * t], q[4 * t + 1], q[4 * t + 2], q[4 * t + 3]);
+    if (pl % LPC == 0) a.s8[(row * a.ng + g) * 8 + c] = (int16_t)s;
+    if (pl == 0) a.d[row * a.ldd + g] = dval;
+}
+
+}  // namespace iq

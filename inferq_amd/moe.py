@@ -76,6 +76,18 @@ class QuantizedMoeLayer:
                                    None if experts is None else experts.data_ptr(),
                                    None if weights is None else weights.data_ptr(), _stream()))
 
+    def forward_timed(self, xs, router_logits, out, events) -> None:
+        """forward_into recording 4 hipEvent_t handles around the routing,
+        gate/up and down launches (iq_moe_forward_timed)."""
+        m = xs.numel() // self.hidden
+        ev = (ctypes.c_void_p * 4)(*events)
+        check(lib().iq_moe_forward_timed(self._h, xs.data_ptr(), router_logits.data_ptr(), m, out.data_ptr(),
+                                         None, None, ev, _stream()))
+
+    def forward_stage(self, stage: int) -> None:
+        """Re-launch one stage of the last call (iq_moe_forward_stage)."""
+        check(lib().iq_moe_forward_stage(self._h, stage, _stream()))
+
     def forward(self, xs, router_logits) -> QuantizedMoeOutput:
         """src/qwen/quantized_moe.rs:227: the layer output and the routes."""
         import torch

@@ -144,6 +144,11 @@ class QuantizedMatrix:
         check(lib().iq_matmul(self._h, xs.data_ptr(), m, y.data_ptr(), _stream()))
         return y
 
+    def forward_into(self, x, y) -> None:
+        """Raw call: contiguous device f32 x [m, cols] into y [m, rows]."""
+        m = x.numel() // self._cols
+        check(lib().iq_matmul(self._h, x.data_ptr(), m, y.data_ptr(), _stream()))
+
     # Where the output rows are computed never changes the result
     # (RowSpread, src/gguf.rs:64-80); on the GPU there is one spread.
     def forward_spread(self, xs, spread=None):

@@ -84,3 +84,34 @@ def random_moe_layer(hidden: int, inter: int, n_experts: int, gate_dtype: int, d
             "selector": (rng.standard_normal(hidden, dtype=np.float32) / np.float32(np.sqrt(hidden))),
         })
     return layer
+
+
+def random_blocks_device(dtype: int, n_blocks: int, device, seed: int):
+    """random_blocks drawn on the GPU (same distributions, different stream
+    of numbers): a flat CUDA uint8 tensor of n_blocks blocks."""
+    import torch
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    bb = BLOCK_BYTES[dtype]
+    raw = torch.randint(0, 256, (n_blocks, bb), dtype=torch.uint8, device=device, generator=gen)
+
+    def f16_bytes(values):
+        return values.to(torch.float16).view(torch.uint8).reshape(n_blocks, 2)
+
+    if dtype == Q4_K:
+        raw[:, 0:2] = f16_bytes(torch.rand(n_blocks, device=device, generator=gen) * 2.0 ** -6)
+        raw[:, 2:4] = f16_bytes(torch.rand(n_blocks, device=device, generator=gen) * 2.0 ** -6)
+    elif dtype == Q6_K:
+        raw[:, 208:210] = f16_bytes(torch.rand(n_blocks, device=device, generator=gen) * 2.0 ** -6)
+    elif dtype == Q8_0:
+        raw[:, 0:2] = f16_bytes(torch.randn(n_blocks, device=device, generator=gen).abs() * 0.02)
+        q = torch.randint(-127, 128, (n_blocks, 32), dtype=torch.int8, device=device, generator=gen)
+        raw[:, 2:34] = q.view(torch.uint8)
+    else:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return raw.reshape(-1)
+
+
+def random_matrix_device(dtype: int, rows: int, cols: int, device, seed: int):
+    return random_blocks_device(dtype, rows * (cols // BLOCK_ELEMS[dtype]), device, seed)

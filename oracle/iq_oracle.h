@@ -106,8 +106,9 @@ int or_matmul_tiled(int dtype, const void *w, size_t n_rows, size_t cols,
                     const float *x, size_t m, float *y, int impl, int nthreads);
 
 /* top_k_routes (src/qwen/moe.rs:21-54): softmax over each row of logits
- * [m x e], rank descending by probability (ties: lower index first -- the
- * reference's unstable sort leaves exact ties unspecified), keep k,
+ * [m x e], rank descending by probability (exactly equal probabilities,
+ * which the reference's unstable sort leaves unordered: larger logit, then
+ * lower index), keep k,
  * renormalise when `normalize`.  experts/weights are [m x k]. */
 int or_top_k_routes(const float *logits, size_t m, size_t e, size_t k, int normalize,
                     int32_t *experts, float *weights);

@@ -40,9 +40,76 @@ static void run_rows(const row_job *j) {
     }
 }
 
-static void *row_thread(void *arg) {
-    run_rows((const row_job *)arg);
+/* A persistent pool of spinning workers, like the reference's matvec pool
+ * (candle's BarrierPool, src/threading.rs:4-9): a call publishes a job
+ * generation, every thread (the caller included) takes static row chunks,
+ * and the caller spins until all chunks are done. */
+#include <stdatomic.h>
+
+#define OR_MAX_THREADS 256
+static struct {
+    int n; /* threads including the caller */
+    pthread_t tids[OR_MAX_THREADS];
+    atomic_int gen, next, done;
+    int nchunks;
+    row_job jobs[OR_MAX_THREADS];
+} pool;
+static pthread_mutex_t pool_mu = PTHREAD_MUTEX_INITIALIZER;
+
+static void pool_work(void) {
+    for (;;) {
+        int c = atomic_fetch_add(&pool.next, 1);
+        if (c >= pool.nchunks) break;
+        run_rows(&pool.jobs[c]);
+        atomic_fetch_add(&pool.done, 1);
+    }
+}
+
+/* Idle workers spin briefly (a matvec call is tens of microseconds), then
+ * park on a condition variable so an idle pool costs no CPU. */
+static pthread_mutex_t sleep_mu = PTHREAD_MUTEX_INITIALIZER;
+static pthread_cond_t sleep_cv = PTHREAD_COND_INITIALIZER;
+static atomic_int sleepers;
+
+static void *pool_thread(void *arg) {
+    (void)arg;
+    int seen = 0;
+    for (;;) {
+        int g, spins = 0;
+        while ((g = atomic_load(&pool.gen)) == seen) {
+            if (++spins < 200000) continue;
+            pthread_mutex_lock(&sleep_mu);
+            atomic_fetch_add(&sleepers, 1);
+            while (atomic_load(&pool.gen) == seen) pthread_cond_wait(&sleep_cv, &sleep_mu);
+            atomic_fetch_sub(&sleepers, 1);
+            pthread_mutex_unlock(&sleep_mu);
+            spins = 0;
+        }
+        seen = g;
+        pool_work();
+    }
     return NULL;
+}
+
+static void pool_run(row_job *jobs, int nchunks, int nthreads) {
+    if (nthreads > OR_MAX_THREADS) nthreads = OR_MAX_THREADS;
+    if (pool.n < nthreads) {
+        for (int t = pool.n > 0 ? pool.n : 1; t < nthreads; t++) pthread_create(&pool.tids[t], NULL, pool_thread, NULL);
+        pool.n = nthreads;
+    }
+    memcpy(pool.jobs, jobs, (size_t)nchunks * sizeof(row_job));
+    pool.nchunks = nchunks;
+    atomic_store(&pool.done, 0);
+    atomic_store(&pool.next, 0);
+    atomic_fetch_add(&pool.gen, 1);
+    if (atomic_load(&sleepers)) {
+        pthread_mutex_lock(&sleep_mu);
+        pthread_cond_broadcast(&sleep_cv);
+        pthread_mutex_unlock(&sleep_mu);
+    }
+    pool_work();
+    while (atomic_load(&pool.done) < nchunks) {
+    }
 }
 
 int or_matmul(int dtype, const void *w, size_t n_rows, size_t cols, const float *x, size_t m, float *y, int impl,
@@ -67,22 +134,23 @@ int or_matmul(int dtype, const void *w, size_t n_rows, size_t cols, const float 
         for (size_t r = 0; r < m; r++) memcpy(packed + (b * m + r) * ib, q + (r * nb + b) * ib, ib);
 
     if (nthreads < 1) nthreads = 1;
-    if ((size_t)nthreads > n_rows) nthreads = (int)n_rows;
-    row_job jobs[256];
-    pthread_t tids[256];
-    if (nthreads > 256) nthreads = 256;
-    size_t chunk = (n_rows + (size_t)nthreads - 1) / (size_t)nthreads;
-    int launched = 0;
-    for (int t = 0; t < nthreads; t++) {
-        size_t b0 = (size_t)t * chunk, b1 = b0 + chunk < n_rows ? b0 + chunk : n_rows;
-        if (b0 >= b1) break;
-        jobs[t] = (row_job){dtype, impl, w, nb, m, packed, cm, b0, b1};
-        if (t == 0) continue;
-        pthread_create(&tids[t], NULL, row_thread, &jobs[t]);
-        launched = t;
+    if (nthreads > OR_MAX_THREADS) nthreads = OR_MAX_THREADS;
+    if (nthreads == 1) {
+        row_job j = {dtype, impl, w, nb, m, packed, cm, 0, n_rows};
+        run_rows(&j);
+    } else {
+        row_job jobs[OR_MAX_THREADS];
+        size_t chunk = (n_rows + (size_t)nthreads - 1) / (size_t)nthreads;
+        int nchunks = 0;
+        for (int t = 0; t < nthreads; t++) {
+            size_t b0 = (size_t)t * chunk, b1 = b0 + chunk < n_rows ? b0 + chunk : n_rows;
+            if (b0 >= b1) break;
+            jobs[nchunks++] = (row_job){dtype, impl, w, nb, m, packed, cm, b0, b1};
+        }
+        pthread_mutex_lock(&pool_mu);
+        pool_run(jobs, nchunks, nthreads);
+        pthread_mutex_unlock(&pool_mu);
     }
-    run_rows(&jobs[0]);
-    for (int t = 1; t <= launched; t++) pthread_join(tids[t], NULL);
 
     for (size_t r = 0; r < m; r++)
         for (size_t n = 0; n < n_rows; n++) y[r * n_rows + n] = cm[n * m + r];

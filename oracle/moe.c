@@ -43,9 +43,13 @@ int or_top_k_routes(const float *logits, size_t m, size_t e, size_t k, int norma
         memset(taken, 0, e);
         for (size_t s = 0; s < k; s++) {
             size_t best = e;
+            /* descending probability; the reference's unstable sort leaves
+             * exactly equal probabilities unordered -- they are ordered here
+             * by larger logit, then lower index (probability never decreases
+             * with the logit, so this is one of the reference's orders) */
             for (size_t i = 0; i < e; i++) {
                 if (taken[i]) continue;
-                if (best == e || p[i] > p[best]) best = i;
+                if (best == e || p[i] > p[best] || (p[i] == p[best] && row[i] > row[best])) best = i;
             }
             taken[best] = 1;
             experts[r * k + s] = (int32_t)best;
