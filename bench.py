@@ -111,6 +111,14 @@ def moe_kernel_bytes(m, unique):
     routed to `unique` distinct experts (plus the shared expert)."""
     gu, dn = expert_bytes()
     g = unique + 1
+    if m == 1:
+        # single-token path: routing, x quantisation and SwiGLU quantisation
+        # stay on chip; gate/up reads x, logits, the selector and 9 gate/up
+        # pairs and writes 9 SwiGLU rows; down reads them, 9 down matrices
+        # and the route weights and writes the output row
+        act = g * I * 4
+        return {"prep": 0, "gate_up": g * gu + 2 * H * 4 + E * 4 + act + 2 * TOPK * 4 + 4,
+                "down": g * dn + act + TOPK * 4 + 4 + H * 4}
     rows = m * TOPK + m                       # grouped activation rows
     xq = m * (H + H // 256 * (4 + 16))        # quantised x: int8 + scale + sub-block sums
     aq = rows * (I + I // 256 * (4 + 16))     # quantised SwiGLU output
@@ -335,7 +343,7 @@ def main():
     wall_ms, per = time_moe_graph(layers, xs, logits, out, args.steps, args.warmup, hip)
     kb = moe_kernel_bytes(1, TOPK)
     gu, dn = expert_bytes()
-    layer_bytes = 9 * (gu + dn) + H * 4 + E * 4 + H * 4
+    layer_bytes = 9 * (gu + dn) + H * 4 + H * 4 + E * 4 + H * 4  # weights + selector, x, logits, out
     value = layer_bytes / (wall_ms * 1e-3) / 1e9
     avg = {k: float(v) for k, v in per.items()}
     dom = max(avg, key=avg.get)
@@ -350,7 +358,7 @@ def main():
         traffic = json.load(open(tpath)).get(f"moe_{dom}")
 
     result = {
-        "metric": "Q4_K MoE-layer us & HBM GB/s (%peak) at M=1; int8 TOPS at prefill width 256",
+        "metric": "Q4_K MoE-layer \u00b5s & HBM GB/s (%peak) at M=1; int8 TOPS at prefill width 256",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,

@@ -129,3 +129,40 @@ def test_moe_load_time_errors(gpu):
     with pytest.raises(QgemmError, match="selector"):
         MOE.QuantizedMoeLayer(256, 256, 4, 2, Q4, Q6, t["gate"], t["up"], t["down"], t["gate"][:256 * 144],
                               t["up"][:256 * 144], t["down"][:256 * 210], None)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_graph_replays_match_eager_calls(gpu, qwen_layer, m):
+    """A layer call captured in a HIP graph and replayed several times, with
+    fresh inputs copied into its buffers and eager work between replays,
+    gives bitwise the eager call's output each time (no allocation, memset
+    or host copy is recorded into the graph)."""
+    moe, _ = _device_layer(qwen_layer, 8, gpu)
+    rng = np.random.default_rng(300 + m)
+    xs = [torch.from_numpy(S.normal((m, 2048), rng)).to(gpu) for _ in range(3)]
+    ls = [torch.from_numpy(S.normal((m, 256), rng)).to(gpu) for _ in range(3)]
+    eager = []
+    for x, lg in zip(xs, ls):
+        o = torch.empty(m, 2048, device=gpu)
+        moe.forward_into(x, lg, o)
+        eager.append(o.cpu().numpy())
+    x_buf, l_buf, o_buf = torch.zeros(m, 2048, device=gpu), torch.zeros(m, 256, device=gpu), \
+        torch.empty(m, 2048, device=gpu)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        moe.forward_into(x_buf, l_buf, o_buf)  # sizes the workspace outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        moe.forward_into(x_buf, l_buf, o_buf)
+    for rep in range(2):
+        for i in range(3):
+            x_buf.copy_(xs[i])
+            l_buf.copy_(ls[i])
+            graph.replay()
+            torch.cuda.synchronize()
+            assert_bitexact(o_buf.cpu().numpy(), eager[i], f"replay {rep}.{i} m={m}")
+            o = torch.empty(m, 2048, device=gpu)  # eager work between replays
+            moe.forward_into(xs[(i + 1) % 3], ls[(i + 1) % 3], o)
+            torch.cuda.synchronize()
+            assert_bitexact(o.cpu().numpy(), eager[(i + 1) % 3], "eager between replays")
