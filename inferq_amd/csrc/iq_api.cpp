@@ -174,9 +174,13 @@ int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* w
     } else if (ws_bytes < need) {
         return fail(IQ_ERR_SHAPE, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
     }
-    ActView a = act_carve(ws, m, w->cols);
-    if (int rc = quantize_for(w, x, m, a, nullptr, s)) return rc;
-    hipError_t e = launch_matmul_lanes(view_of(w), a, y, w->rows, isum, msum, s);
+    hipError_t e = hipErrorNotSupported;
+    if (!isum && gemv_supported(view_of(w), m)) e = launch_gemv(view_of(w), x, w->cols, m, y, w->rows, s);
+    if (e == hipErrorNotSupported) {
+        ActView a = act_carve(ws, m, w->cols);
+        if (int rc = quantize_for(w, x, m, a, nullptr, s)) return rc;
+        e = launch_matmul_lanes(view_of(w), a, y, w->rows, isum, msum, s);
+    }
     if (e != hipSuccess) return hip_fail(e, "matmul launch");
     return IQ_OK;
 }

@@ -40,6 +40,18 @@ __device__ __forceinline__ int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// Workgroup barrier ordering LDS only: global loads issued before it stay
+// in flight (a full __syncthreads would also wait for them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// a * b + c for |a|, |b| < 2^23 (full-rate v_mad_i32_i24 instead of the
+// quarter-rate 32-bit multiply); exact for every scale x lane-dot product here.
+__device__ __forceinline__ int32_t imad24(int32_t a, int32_t b, int32_t c) { return __mul24(a, b) + c; }
+
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
 __device__ __forceinline__ uint32_t ld16(const uint8_t* p) { return *(const uint16_t*)p; }
 

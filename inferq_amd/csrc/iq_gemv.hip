@@ -1,0 +1,522 @@
+// iq_gemv.hip -- y = x . W^T for many output rows and up to 8 input rows
+// (decode and verify shapes: LM head, dense projections), in the reference's
+// exact f32 order (src/qgemm.rs:175-397 via src/gguf.rs:608-690).
+//
+// Each wave owns groups of 8 consecutive weight rows.  A group is consumed
+// in slices of 2048 weights (Q8_0: 1024) per row: the wave copies the slice
+// bytes of its 8 rows -- one contiguous span per row -- with 16-byte loads
+// spread evenly over its 64 lanes, parks them in its own LDS region, and
+// decodes from there with the same lane structure as iq_lanes.h (lane
+// (slot, k) owns lane k of row `slot`).  Two slices are in flight per wave:
+// while one is decoded, the loads of the next two are outstanding.
+//
+// Every workgroup quantises the input rows itself (from_float, bit-exact to
+// iq_quant.h) into LDS, after issuing its first weight loads, so a call is
+// one launch and the quantisation hides under the first memory round trip.
+//
+// Weights are read with non-temporal loads: they stream through once, and
+// keeping them out of the caches' retention lifts sustained HBM throughput.
+//
+// LDS rows are padded so that the 8 rows of a wave start in different bank
+// groups.  Q6_K blocks at 2 (mod 4) bytes are read as aligned dword pairs and
+// funnel-shifted; the parity of every block in a slice is a compile-time
+// constant because slices hold a multiple of 8 blocks.
+#include "iq_lanes.h"
+#include "iq_quant.h"
+
+namespace iq {
+
+namespace {
+
+template <int FMT>
+struct GvFmt;
+template <>
+struct GvFmt<kQ4_K> {
+    static constexpr int UB = 144;  // bytes per 256-value unit
+    static constexpr int SU = 8;    // units per slice
+    static constexpr int PAD = 32;
+    static constexpr int DPU = 1;   // activation scales per unit
+};
+template <>
+struct GvFmt<kQ6_K> {
+    static constexpr int UB = 210, SU = 8, PAD = 16, DPU = 1;
+};
+template <>
+struct GvFmt<kQ8_0> {
+    static constexpr int UB = 272, SU = 4, PAD = 96, DPU = 8;  // unit = 8 blocks of 34 B
+};
+
+template <int FMT>
+struct GvGeom {
+    static constexpr int UB = GvFmt<FMT>::UB, SU = GvFmt<FMT>::SU, DPU = GvFmt<FMT>::DPU;
+    static constexpr int SB = UB * SU;               // slice bytes per row
+    static constexpr int RS = SB + GvFmt<FMT>::PAD;  // LDS row stride
+    static constexpr int CPR = SB / 16;              // 16-byte chunks per row slice
+    static constexpr int NL = (8 * CPR + 63) / 64;   // chunks per lane per slice
+    static constexpr int WAVE_LDS = 8 * RS;
+    static_assert(SB % 16 == 0 && RS % 16 == 0, "slices must be 16-byte granular");
+};
+
+struct GemvArgs {
+    const uint8_t* w;
+    int64_t n, row_bytes;
+    int nu;      // 256-value units per row
+    int groups;  // ceil(n / 8)
+    const float* x;  // f32 input rows [m][ldx]
+    int64_t ldx;
+    int m;
+    float* y;
+    int64_t ldy;
+    int act_lds;  // bytes of the activation tile in LDS
+};
+
+// Activation tile in LDS: q [MT][nu][256] (lane-transposed groups),
+// d [MT][nu * DPU], s8 [MT][nu][8] (K-quants), corr [MT][nu][64] int32
+// (Q6_K).  Every part starts 16-byte aligned.
+template <int FMT, int MT>
+__host__ __device__ constexpr int act_d_offset(int nu) { return MT * nu * 256; }
+template <int FMT, int MT>
+__host__ __device__ constexpr int act_s8_offset(int nu) {
+    return act_d_offset<FMT, MT>(nu) + ((MT * nu * GvFmt<FMT>::DPU * 4 + 15) & ~15);
+}
+template <int FMT, int MT>
+__host__ __device__ constexpr int act_corr_offset(int nu) {
+    return act_s8_offset<FMT, MT>(nu) + (FMT == kQ8_0 ? 0 : MT * nu * 16);
+}
+template <int FMT, int MT>
+__host__ __device__ constexpr int act_lds_bytes(int nu) {
+    return act_corr_offset<FMT, MT>(nu) + (FMT == kQ6_K ? MT * nu * 256 : 0);
+}
+
+template <int FMT, int MT>
+struct ActLds {
+    const uint8_t* q;
+    const float* d;
+    const int16_t* s8;
+    const uint8_t* corr;
+    int nu;
+    __device__ __forceinline__ ActLds(const uint8_t* base, int nu_) : nu(nu_) {
+        q = base;
+        d = (const float*)(base + act_d_offset<FMT, MT>(nu));
+        s8 = (const int16_t*)(base + act_s8_offset<FMT, MT>(nu));
+        corr = base + act_corr_offset<FMT, MT>(nu);
+    }
+    // Q6_K: -32 * (sum of the four int8 of dword (chunk c, lane k)), laid out
+    // like q, so that the dot of (q6 - 32) is the dot of q6 started at it
+    __device__ __forceinline__ void load_corr(int mi, int u, int k, int32_t (&cv)[8]) const {
+        const uint8_t* p = corr + ((size_t)mi * nu + u) * 256 + 32 * k;
+        const u32x4a16 a0 = *(const u32x4a16*)p, a1 = *(const u32x4a16*)(p + 16);
+        cv[0] = (int32_t)a0.x; cv[1] = (int32_t)a0.y; cv[2] = (int32_t)a0.z; cv[3] = (int32_t)a0.w;
+        cv[4] = (int32_t)a1.x; cv[5] = (int32_t)a1.y; cv[6] = (int32_t)a1.z; cv[7] = (int32_t)a1.w;
+    }
+    __device__ __forceinline__ void load_q(int mi, int u, int k, uint32_t (&av)[8]) const {
+        const uint8_t* p = q + ((size_t)mi * nu + u) * 256 + 32 * k;
+        const u32x4a16 a0 = *(const u32x4a16*)p, a1 = *(const u32x4a16*)(p + 16);
+        av[0] = a0.x; av[1] = a0.y; av[2] = a0.z; av[3] = a0.w;
+        av[4] = a1.x; av[5] = a1.y; av[6] = a1.z; av[7] = a1.w;
+    }
+};
+
+// The activation tile as an ActView over LDS (rows 0..MT-1).
+template <int FMT, int MT>
+__device__ __forceinline__ ActView act_view_lds(uint8_t* lds, int nu) {
+    ActView a;
+    a.q = (int8_t*)lds;
+    a.d = (float*)(lds + act_d_offset<FMT, MT>(nu));
+    a.s8 = (int16_t*)(lds + act_s8_offset<FMT, MT>(nu));
+    a.ldq = (int64_t)nu * 256;
+    a.ldd = (int64_t)nu * GvFmt<FMT>::DPU;
+    a.ng = nu;
+    a.m = MT;
+    return a;
+}
+
+// Input quantisation in passes of 8 groups of 256 values: in pass `ps`,
+// lane l holds values 32 (l % 8) .. +31 of tile group t = 8 ps + l / 8 (row
+// t / nu, group t % nu).  For Q8_0 these 32 values are exactly block
+// 8 (t % nu) + l % 8 of the row, so both formats load the same way.
+template <int MT>
+__device__ __forceinline__ void quant_pass_load(const GemvArgs& p, int m0, int mc, int ps, float (&v)[32]) {
+    const int lane = threadIdx.x & 63;
+    const int t = 8 * ps + (lane >> 3);
+    const int tt = min(t, MT * p.nu - 1);  // lanes past the tile re-read the last group
+    const int mi = tt / p.nu, g = tt - mi * p.nu;
+    const float* src = p.x + (int64_t)(m0 + min(mi, mc - 1)) * p.ldx + (int64_t)g * 256 + 32 * (lane & 7);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const f32x4 q = load4(src + 4 * j);
+        v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+    }
+}
+template <int FMT, int MT>
+__device__ __forceinline__ void quant_pass_store(const GemvArgs& p, const ActView& a, int32_t* corr, int ps,
+                                                 const float (&v)[32]) {
+    const int lane = threadIdx.x & 63;
+    const int t = 8 * ps + (lane >> 3);
+    const bool live = t < MT * p.nu;
+    const int tt = min(t, MT * p.nu - 1);
+    const int mi = tt / p.nu, g = tt - mi * p.nu;
+    if constexpr (FMT == kQ8_0) quant64_q80_vals(v, live, mi, (int64_t)g * 8 + (lane & 7), a);
+    else quant8_q8k_vals(v, live, mi, g, a, corr);
+}
+
+// ---- per-unit decode from LDS ------------------------------------------------
+
+// Q6_K block at LDS address b; A2: b == 2 (mod 4).
+template <bool A2>
+__device__ __forceinline__ Q6Dec q6_decode_lds(const uint8_t* b, int k) {
+    uint32_t ql[4], qh[2], sc[4];
+    if constexpr (!A2) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) ql[i] = *(const uint32_t*)(b + 32 * i + 4 * k);
+#pragma unroll
+        for (int j = 0; j < 2; j++) qh[j] = *(const uint32_t*)(b + 128 + 32 * j + 4 * k);
+#pragma unroll
+        for (int t = 0; t < 4; t++) sc[t] = *(const uint32_t*)(b + 192 + 4 * t);
+    } else {
+        const uint8_t* a = b - 2;  // 4-byte aligned
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x2 v = *(const u32x2*)(a + 32 * i + 4 * k);
+            ql[i] = __builtin_amdgcn_alignbyte(v.y, v.x, 2);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const u32x2 v = *(const u32x2*)(a + 128 + 32 * j + 4 * k);
+            qh[j] = __builtin_amdgcn_alignbyte(v.y, v.x, 2);
+        }
+        uint32_t s[5];
+#pragma unroll
+        for (int t = 0; t < 5; t++) s[t] = *(const uint32_t*)(a + 192 + 4 * t);
+#pragma unroll
+        for (int t = 0; t < 4; t++) sc[t] = __builtin_amdgcn_alignbyte(s[t + 1], s[t], 2);
+    }
+    Q6Dec r;
+    r.xd = f16_to_f32(*(const uint16_t*)(b + 208));
+    const int hk = k >= 4 ? 8 : 0;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t l = ql[2 * j + (i & 1)];
+            const uint32_t lo = i < 2 ? (l & 0x0f0f0f0fu) : ((l >> 4) & 0x0f0f0f0fu);
+            const uint32_t h = qh[j];
+            const uint32_t hs = i == 0 ? h << 4 : i == 1 ? h << 2 : i == 2 ? h : h >> 2;
+            r.v[4 * j + i] = (hs & 0x30303030u) | lo;  // bytes q6 in [0, 64); the -32 comes with the activation
+            // scale 8j + 2i + (k >= 4): byte (2i & 3) + (k >= 4) of word 2j + i/2
+            r.sc[4 * j + i] = __builtin_amdgcn_sbfe(sc[2 * j + (i >> 1)], 16 * (i & 1) + hk, 8);
+        }
+    }
+    return r;
+}
+
+__device__ __forceinline__ Q4Dec q4_decode_lds(const uint8_t* b, int k) {
+    Q4W w;
+    w.hdr = *(const u32x4a16*)b;
+#pragma unroll
+    for (int j = 0; j < 4; j++) w.q[j] = *(const uint32_t*)(b + 16 + 32 * j + 4 * k);
+    return q4_decode(w, k);
+}
+
+// Q8_0: the 8 blocks of a unit at LDS address b (16-byte aligned).
+struct Q8Dec {
+    uint32_t q[8];
+    float d[8];
+};
+__device__ __forceinline__ Q8Dec q8_decode_lds(const uint8_t* b, int k) {
+    Q8Dec r;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const uint8_t* blk = b + 34 * c;
+        if (c % 2 == 0) {  // window at 2 (mod 4)
+            const u32x2 v = *(const u32x2*)(blk + 4 * k);
+            r.q[c] = __builtin_amdgcn_alignbyte(v.y, v.x, 2);
+        } else {
+            r.q[c] = *(const uint32_t*)(blk + 2 + 4 * k);
+        }
+        r.d[c] = f16_to_f32(*(const uint16_t*)blk);
+    }
+    return r;
+}
+
+// ---- the kernel ----------------------------------------------------------------
+
+template <int FMT, int MT>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
+    using G = GvGeom<FMT>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    // wave-uniform in a register the compiler knows is uniform, so that
+    // every loop and branch on the item index is scalar
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int k = lane & 7, slot = lane >> 3;
+    const int m0 = blockIdx.y * MT;
+    const int mc = min(MT, p.m - m0);
+    const int nsl = p.nu / G::SU;
+    const int gstride = gridDim.x * 4;
+    const int grp0 = blockIdx.x * 4 + wave;
+    // this wave's items: (group grp0 + (i / nsl) * gstride, slice i % nsl)
+    const int my_groups = grp0 < p.groups ? (p.groups - grp0 + gstride - 1) / gstride : 0;
+    const int nitems = my_groups * nsl;
+
+    // this lane's 16-byte chunks of a slice: global offset from the slice
+    // base, and LDS offset (-1: no chunk)
+    uint32_t goff[G::NL];
+    int loff[G::NL];
+#pragma unroll
+    for (int i = 0; i < G::NL; i++) {
+        int q = i * 64 + lane;
+        const bool ok = q < 8 * G::CPR;
+        if (!ok) q = 8 * G::CPR - 1;
+        const int r = q / G::CPR, cq = q - r * G::CPR;
+        goff[i] = (uint32_t)(r * p.row_bytes + cq * 16);
+        loff[i] = ok ? r * G::RS + cq * 16 : -1;
+    }
+    // Loads are issued unconditionally (past the last item, the last item
+    // again: its lines are still in L2), so that the same number of loads is
+    // outstanding on every path and the compiler's vmcnt waits stay exact:
+    // parking one buffer waits only for that buffer's loads.  A wave with
+    // no items reads group 0, which always exists.
+    const int gbase = nitems > 0 ? grp0 : 0;
+    const int ilast = nitems > 0 ? nitems - 1 : 0;
+    auto issue = [&](u32x4a16 (&st)[G::NL], int it_) {
+        const int it = min(it_, ilast);
+        const int g8 = gbase + (it / nsl) * gstride, sl = it - (it / nsl) * nsl;
+        const uint8_t* base = p.w + (int64_t)g8 * 8 * p.row_bytes + (int64_t)sl * G::SB;
+        if ((int64_t)g8 * 8 + 8 <= p.n) {  // uniform: a full group
+#pragma unroll
+            for (int i = 0; i < G::NL; i++) st[i] = __builtin_nontemporal_load((const u32x4a16*)(base + goff[i]));
+        } else {  // the last group: rows past the end re-read the last row
+            const int last = (int)(p.n - (int64_t)g8 * 8) - 1;
+#pragma unroll
+            for (int i = 0; i < G::NL; i++) {
+                const int q = min(i * 64 + lane, 8 * G::CPR - 1);
+                const int r = q / G::CPR, cq = q - r * G::CPR;
+                st[i] = __builtin_nontemporal_load((const u32x4a16*)(base + (int64_t)min(r, last) * p.row_bytes + cq * 16));
+            }
+        }
+    };
+    auto park = [&](const u32x4a16 (&st)[G::NL], uint8_t* wl) {
+#pragma unroll
+        for (int i = 0; i < G::NL; i++)
+            if (loff[i] >= 0) *(u32x4a16*)(wl + loff[i]) = st[i];
+    };
+
+    // quantise the input tile into LDS
+    // Quantise the input tile into LDS.  One input row (at most 16 groups:
+    // waves 0 and 1, one pass each): the first two slices go out between
+    // loading and quantising it, so the quantisation runs under their memory
+    // latency.  Several rows: quantise first, then issue (an input load
+    // issued after the weight loads could only be waited for together with
+    // them).
+    constexpr bool kEarly = MT == 1;
+    const int npass = (MT * p.nu + 7) / 8;
+    u32x4a16 stA[G::NL], stB[G::NL];
+    const ActView al = act_view_lds<FMT, MT>(smem, p.nu);
+    int32_t* corr = FMT == kQ6_K ? (int32_t*)(smem + act_corr_offset<FMT, MT>(p.nu)) : nullptr;
+    if constexpr (kEarly) {
+        float xv[32];
+        if (wave < npass) quant_pass_load<MT>(p, m0, mc, wave, xv);
+        issue(stA, 0);
+        issue(stB, 1);
+        if (wave < npass) quant_pass_store<FMT, MT>(p, al, corr, wave, xv);
+    } else {
+        for (int ps = wave; ps < npass; ps += 4) {
+            float xv[32];
+            quant_pass_load<MT>(p, m0, mc, ps, xv);
+            quant_pass_store<FMT, MT>(p, al, corr, ps, xv);
+        }
+    }
+    lds_barrier();
+    if (nitems == 0) return;  // uniform per wave; no barrier follows
+    if constexpr (!kEarly) {
+        issue(stA, 0);
+        issue(stB, 1);
+    }
+
+    const ActLds<FMT, MT> act(smem, p.nu);
+    uint8_t* wl = smem + p.act_lds + wave * G::WAVE_LDS;
+    const uint8_t* rowl = wl + slot * G::RS;
+    float acc[MT], accm[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++) acc[i] = accm[i] = 0.f;
+
+    auto compute = [&](int it) {
+        const int g8 = grp0 + (it / nsl) * gstride, sl = it - (it / nsl) * nsl;
+        // LDS operations of one wave complete in order: the stores that
+        // parked this slice are visible to the loads below; keep the
+        // compiler from moving the loads above them.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int u = 0; u < G::SU; u++) {
+            const int ug = sl * G::SU + u;
+            const uint8_t* b = rowl + u * G::UB;
+            if constexpr (FMT == kQ4_K) {
+                const Q4Dec dec = q4_decode_lds(b, k);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    if (MT == 1 || mi < mc) {
+                        uint32_t av[8];
+                        act.load_q(mi, ug, k, av);
+                        const float yd = act.d[mi * p.nu + ug];
+                        const uint32_t q8s = *(const uint32_t*)(act.s8 + ((size_t)mi * p.nu + ug) * 8 + 2 * (k & 3));
+                        int32_t isum, msum;
+                        float d, dmin;
+                        q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
+                        acc[mi] = __builtin_fmaf(d, (float)isum, acc[mi]);
+                        accm[mi] = __builtin_fmaf(dmin, (float)msum, accm[mi]);
+                    }
+                }
+            } else if constexpr (FMT == kQ6_K) {
+                // block u of a slice sits at 2u (mod 4); u is a constant once unrolled
+                const Q6Dec dec = (u & 1) ? q6_decode_lds<true>(b, k) : q6_decode_lds<false>(b, k);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    if (MT == 1 || mi < mc) {
+                        uint32_t av[8];
+                        int32_t cv[8];
+                        act.load_q(mi, ug, k, av);
+                        act.load_corr(mi, ug, k, cv);
+                        const float yd = act.d[mi * p.nu + ug];
+                        int32_t isum = 0;
+#pragma unroll
+                        for (int c = 0; c < 8; c++) isum = imad24(dec.sc[c], sdot4(dec.v[c], av[c], cv[c]), isum);
+                        acc[mi] = __builtin_fmaf(yd * dec.xd, (float)isum, acc[mi]);
+                    }
+                }
+            } else {
+                const Q8Dec dec = q8_decode_lds(b, k);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    if (MT == 1 || mi < mc) {
+                        uint32_t av[8];
+                        act.load_q(mi, ug, k, av);
+                        const float* dp = act.d + ((size_t)mi * p.nu + ug) * 8;
+                        const f32x4 d0 = *(const f32x4*)dp, d1 = *(const f32x4*)(dp + 4);
+                        const float yd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                        for (int c = 0; c < 8; c++)
+                            acc[mi] = __builtin_fmaf(dec.d[c] * yd[c], (float)sdot4(dec.q[c], av[c], 0), acc[mi]);
+                    }
+                }
+            }
+        }
+        if (sl == nsl - 1) {
+            const int64_t row = (int64_t)g8 * 8 + slot;
+#pragma unroll
+            for (int mi = 0; mi < MT; mi++) {
+                float v = hsum8(acc[mi]);
+                if constexpr (FMT == kQ4_K) v = v + hsum4(accm[mi]);
+                if (k == 0 && row < p.n && (MT == 1 || mi < mc)) p.y[(int64_t)(m0 + mi) * p.ldy + row] = v;
+                acc[mi] = accm[mi] = 0.f;
+            }
+        }
+    };
+
+    // Two items per trip with one exit at the bottom: every path through
+    // the body parks and reissues both buffers in the same order (an odd
+    // last item parks and reloads B once more, from L2, without using it).
+    for (int it = 0; it < nitems; it += 2) {
+        park(stA, wl);
+        issue(stA, it + 2);
+        compute(it);
+        park(stB, wl);
+        issue(stB, it + 3);
+        if (it + 1 < nitems) compute(it + 1);
+    }
+}
+
+struct DevLimits {
+    int cus = 0, lds_block = 0, lds_cu = 0;
+};
+DevLimits g_limits[64];
+
+const DevLimits& limits() {
+    static const DevLimits fallback{256, 64 * 1024, 64 * 1024};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fallback;
+    DevLimits& L = g_limits[dev];
+    if (L.cus == 0) {
+        int v = 0;
+        L.lds_block = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0
+                          ? v : 64 * 1024;
+        L.lds_cu = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess &&
+                           v > 0 ? v : L.lds_block;
+        L.cus = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
+    }
+    return L;
+}
+
+template <int FMT, int MT>
+hipError_t launch_t(GemvArgs args, hipStream_t s) {
+    using G = GvGeom<FMT>;
+    args.act_lds = act_lds_bytes<FMT, MT>(args.nu);
+    const size_t lds = (size_t)args.act_lds + 4 * G::WAVE_LDS;
+    const DevLimits& L = limits();
+    if (lds > (size_t)L.lds_block) return hipErrorNotSupported;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv<FMT, MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorNotSupported;
+        }
+    }
+    const int per_cu = (int)(L.lds_cu / lds);
+    const int64_t wgs = ((int64_t)args.groups + 3) / 4;
+    const int64_t cap = (int64_t)L.cus * (per_cu < 1 ? 1 : per_cu);
+    dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)((args.m + MT - 1) / MT));
+    hipLaunchKernelGGL((k_gemv<FMT, MT>), grid, dim3(256), lds, s, args);
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
+    const int m = args.m;
+    if (m <= 1) return launch_t<FMT, 1>(args, s);
+    if (m <= 2) return launch_t<FMT, 2>(args, s);
+    if (m <= 4) return launch_t<FMT, 4>(args, s);
+    return launch_t<FMT, 8>(args, s);
+}
+
+}  // namespace
+
+bool gemv_supported(const WeightView& w, int64_t m) {
+    if (m < 1 || m > 8 || w.rows < 1) return false;
+    const int64_t nu = w.cols / 256;
+    if (w.cols % 256 != 0 || w.rows > (int64_t)1 << 31) return false;
+    if (m == 1 && nu > 16) return false;  // one quantisation batch per wave at one row
+    switch (w.dtype) {
+    case kQ4_K: return nu % GvFmt<kQ4_K>::SU == 0;
+    case kQ6_K: return nu % GvFmt<kQ6_K>::SU == 0;
+    case kQ8_0: return nu % GvFmt<kQ8_0>::SU == 0;
+    default: return false;
+    }
+}
+
+hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                       hipStream_t s) {
+    if (!gemv_supported(w, m)) return hipErrorNotSupported;
+    GemvArgs args;
+    args.w = w.w;
+    args.n = w.rows;
+    args.row_bytes = w.row_bytes;
+    args.nu = (int)(w.cols / 256);
+    args.groups = (int)((w.rows + 7) / 8);
+    args.x = x;
+    args.ldx = ldx;
+    args.m = (int)m;
+    args.y = y;
+    args.ldy = ldy;
+    args.act_lds = 0;
+    switch (w.dtype) {
+    case kQ4_K: return launch_fmt<kQ4_K>(args, s);
+    case kQ6_K: return launch_fmt<kQ6_K>(args, s);
+    case kQ8_0: return launch_fmt<kQ8_0>(args, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace iq

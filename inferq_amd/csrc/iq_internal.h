@@ -49,4 +49,12 @@ struct WeightView {
 hipError_t launch_matmul_lanes(const WeightView& w, const ActView& a, float* y, int64_t ldy, int32_t* isum,
                                int32_t* msum, hipStream_t s);
 
+// The LDS-staged kernel for many output rows at 1..8 input rows
+// (iq_gemv.hip); it quantises the f32 input rows x [m][ldx] itself.
+// gemv_supported tells whether it covers a shape; launch_gemv returns
+// hipErrorNotSupported when it does not.
+bool gemv_supported(const WeightView& w, int64_t m);
+hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                       hipStream_t s);
+
 }  // namespace iq

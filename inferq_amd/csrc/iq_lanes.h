@@ -169,8 +169,11 @@ __device__ __forceinline__ void q4_dot(const Q4Dec& r, const uint32_t (&av)[8], 
                                        int32_t& msum, float& d, float& dmin) {
     isum = 0;
 #pragma unroll
-    for (int j = 0; j < 4; j++) isum += r.sc[2 * j] * sdot4(r.lo[j], av[2 * j], 0) + r.sc[2 * j + 1] * sdot4(r.hi[j], av[2 * j + 1], 0);
-    msum = r.mA * (int32_t)(int16_t)(q8s & 0xffffu) + r.mB * (int32_t)(int16_t)(q8s >> 16);
+    for (int j = 0; j < 4; j++) {
+        isum = imad24(r.sc[2 * j], sdot4(r.lo[j], av[2 * j], 0), isum);
+        isum = imad24(r.sc[2 * j + 1], sdot4(r.hi[j], av[2 * j + 1], 0), isum);
+    }
+    msum = imad24(r.mA, (int32_t)(int16_t)(q8s & 0xffffu), imad24(r.mB, (int32_t)(int16_t)(q8s >> 16), 0));
     d = yd * r.xd;
     dmin = -yd * r.xdmin;
 }
@@ -203,7 +206,7 @@ __device__ __forceinline__ Q6Dec q6_decode(const Q6W& wb, int k) {
 __device__ __forceinline__ void q6_dot(const Q6Dec& r, const uint32_t (&av)[8], float yd, int32_t& isum, float& d) {
     isum = 0;
 #pragma unroll
-    for (int c = 0; c < 8; c++) isum += r.sc[c] * sdot4(r.v[c], av[c], 0);
+    for (int c = 0; c < 8; c++) isum = imad24(r.sc[c], sdot4(r.v[c], av[c], 0), isum);
     d = yd * r.xd;
 }
 

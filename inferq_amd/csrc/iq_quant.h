@@ -28,11 +28,11 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// Q8K: xs points at the 256 values of group g of activation row `row`.
-// `ref`, when not null, receives the reference 292-byte block.
-__device__ __forceinline__ void quant_q8k_wave(const float* xs, int64_t row, int g, const ActView& a, uint8_t* ref) {
+// Q8K of one 256-value group whose values 4l..4l+3 lane l already holds
+// (all 64 lanes call it): writes row `row`, group `g` of `a` and, when `ref`
+// is not null, the reference 292-byte block.
+__device__ __forceinline__ void quant_q8k_vals4(const f32x4 v, int64_t row, int g, const ActView& a, uint8_t* ref) {
     const int lane = threadIdx.x & 63;
-    const f32x4 v = load4(xs + 4 * lane);
     // amax and the first index reaching it (the reference updates only on a
     // strictly larger |x| while scanning upwards)
     float am = 0.f;
@@ -87,17 +87,32 @@ __device__ __forceinline__ void quant_q8k_wave(const float* xs, int64_t row, int
     }
 }
 
-// Q8_0: the 8 blocks of group g of a row of width k (xrow = row start).
-// `ref_row`, when not null, receives the row's reference 34-byte blocks.
-__device__ __forceinline__ void quant_q80_wave(const float* xrow, int64_t k, int64_t row, int g, const ActView& a,
-                                               uint8_t* ref_row) {
+// Q8K: xs points at the 256 values of group g of activation row `row`.
+__device__ __forceinline__ void quant_q8k_wave(const float* xs, int64_t row, int g, const ActView& a, uint8_t* ref) {
+    const int lane = threadIdx.x & 63;
+    quant_q8k_vals4(load4(xs + 4 * lane), row, g, a, ref);
+}
+
+// The values lane l quantises in quant_q80_vals4: 4 values of block
+// 8g + l/8 of a row of width k (zeros past the row's last block).
+__device__ __forceinline__ f32x4 q80_vals4_load(const float* xrow, int64_t k, int g) {
+    const int lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)g * 8 + (lane >> 3);
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (b < k / 32) v = load4(xrow + b * 32 + 4 * (lane & 7));
+    return v;
+}
+
+// Q8_0 of the 8 blocks of group g of a row of width k (values from
+// q80_vals4_load); `ref_row`, when not null, receives the row's reference
+// 34-byte blocks.
+__device__ __forceinline__ void quant_q80_vals4(const f32x4 v, int64_t k, int64_t row, int g, const ActView& a,
+                                                uint8_t* ref_row) {
     const int lane = threadIdx.x & 63;
     const int c = lane >> 3, kk = lane & 7;
     const int64_t nb32 = k / 32;
     const int64_t b = (int64_t)g * 8 + c;  // this lane's Q8_0 block
     const bool valid = b < nb32;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (valid) v = load4(xrow + b * 32 + 4 * kk);
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     am = fmaxf(am, __shfl_xor(am, 1));
     am = fmaxf(am, __shfl_xor(am, 2));
@@ -118,6 +133,12 @@ __device__ __forceinline__ void quant_q80_wave(const float* xrow, int64_t k, int
         *(uint16_t*)(blk + 2 + 4 * kk) = (uint16_t)(packed & 0xffffu);
         *(uint16_t*)(blk + 4 + 4 * kk) = (uint16_t)(packed >> 16);
     }
+}
+
+// Q8_0: the 8 blocks of group g of a row of width k (xrow = row start).
+__device__ __forceinline__ void quant_q80_wave(const float* xrow, int64_t k, int64_t row, int g, const ActView& a,
+                                               uint8_t* ref_row) {
+    quant_q80_vals4(q80_vals4_load(xrow, k, g), k, row, g, a, ref_row);
 }
 
 }  // namespace iq
@@ -154,7 +175,7 @@ __device__ __forceinline__ void q8k_chunk_load(const float* src, float (&v)[32])
 // `a` (live == false: an idle 8-lane group).  All 64 lanes must call it.
 // Same arithmetic as quant_q8k_wave.
 __device__ __forceinline__ void quant8_q8k_vals(const float (&v)[32], bool live, int64_t row, int g,
-                                                const ActView& a) {
+                                                const ActView& a, int32_t* corr = nullptr) {
     const int c = threadIdx.x & 7;
     // first index of the largest |x| in this chunk, then across the 8 chunks
     float am = 0.f, mv = 0.f;
@@ -199,8 +220,12 @@ __device__ __forceinline__ void quant8_q8k_vals(const float (&v)[32], bool live,
     for (int j = 0; j < 32; j++) s += q[j];
     uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
 #pragma unroll
-    for (int kk = 0; kk < 8; kk++)
-        qrow[perm_dword(c, kk)] = pack4(q[4 * kk], q[4 * kk + 1], q[4 * kk + 2], q[4 * kk + 3]);
+    for (int kk = 0; kk < 8; kk++) {
+        const uint32_t pk = pack4(q[4 * kk], q[4 * kk + 1], q[4 * kk + 2], q[4 * kk + 3]);
+        qrow[perm_dword(c, kk)] = pk;
+        // optional Q6_K offset term, laid out like q: -32 * (sum of the dword's four int8)
+        if (corr) corr[(row * a.ng + g) * 64 + perm_dword(c, kk)] = sdot4(pk, 0xe0e0e0e0u, 0);
+    }
     a.s8[(row * a.ng + g) * 8 + c] = (int16_t)s;
     if (c == 0) a.d[row * a.ldd + g] = dval;
 }

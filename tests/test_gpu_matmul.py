@@ -20,11 +20,14 @@ Q4, Q6, Q8 = S.Q4_K, S.Q6_K, S.Q8_0
 
 # (dtype, rows, cols): the reference test matrix shape [96 x 512] for each
 # format (src/gguf.rs:1630-1677), the BASELINE shapes, ragged row counts
-# (not a multiple of 8) and an odd number of Q6_K blocks per row.
+# (not a multiple of 8) and an odd number of Q6_K blocks per row.  Widths
+# that are a multiple of 2048 (Q8_0: 1024) at 1..8 input rows run the
+# LDS-staged kernel (iq_gemv.hip); the others, and 9+ rows, the direct one.
 SHAPES = [
     (Q4, 96, 512), (Q6, 96, 512), (Q8, 96, 512),
     (Q4, 1024, 2048), (Q6, 2048, 512), (Q8, 4096, 2048),
     (Q4, 2048, 4096), (Q6, 37, 768), (Q8, 45, 96), (Q4, 13, 256),
+    (Q6, 300, 2048), (Q6, 64, 4096), (Q4, 77, 2048), (Q8, 19, 1024), (Q6, 5, 6144),
 ]
 ROWS = [1, 2, 3, 4, 7, 8, 9, 15, 16, 17, 33]
 
@@ -95,6 +98,18 @@ def test_quantize_q80_bitexact(gpu, oracle):
     got = Q.quantize_q80(torch.from_numpy(x).to(gpu)).cpu().numpy()
     expected = np.concatenate([oracle.quantize_q80(r) for r in x]).view(np.uint8)
     assert np.array_equal(got, expected.reshape(-1))
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_lm_head_slice_bitexact(gpu, oracle, m):
+    """A 20000-row slice of the Q6_K LM head shape [248320 x 2048]: many row
+    groups per wave in the LDS-staged kernel."""
+    rng = np.random.default_rng(4242 + m)
+    w = S.random_matrix(Q6, 20000, 2048, rng)
+    x = S.normal((m, 2048), rng)
+    mat = Q.QuantizedMatrix.upload(w, Q6, 20000, 2048)
+    got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    assert_bitexact(got, oracle.matmul(Q6, w, 20000, 2048, x, nthreads=8), f"LM-head slice m={m}")
 
 
 def test_m_invariance_bitwise(gpu):
