@@ -292,6 +292,30 @@ def secondary(args, hip, stream, device, layers):
     return extra
 
 
+def prefill(args, hip, stream, device):
+    """BASELINE configs[3], dense part: Q4_K [256 x 2048] -> 8192 and
+    [256 x 4096] -> 2048 on the int8-MFMA path (activation quantisation,
+    MFMA kernel and, for the narrow output, the split-K reduction all inside
+    the timed call).  TOPS = 2 M N K / time; peak = 5.0 POPS dense int8."""
+    import torch
+
+    from inferq_amd import qgemm, synth
+
+    res = {}
+    for n, k in ((8192, 2048), (2048, 4096)):
+        copies = 8
+        mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, n, k, device, 90 + c), synth.Q4_K,
+                                           n, k) for c in range(copies)]
+        x = torch.randn(256, k, device=device)
+        y = torch.empty(256, n, device=device)
+        ms = time_calls(lambda i: mats[i % copies].forward_into(x, y), max(20, args.steps // 4), hip, stream)
+        tops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
+        res[f"q4k_256x{k}_to_{n}"] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
+                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        del mats
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,7 +446,7 @@ def main():
 
     if not args.no_secondary:
         result["extra"] = secondary(args, hip, stream, device, layers)
-        result["extra"]["prefill_int8_tops"] = None
+        result["extra"]["prefill_int8_tops"] = prefill(args, hip, stream, device)
         log(f"secondary: {result['extra']}")
 
     print(json.dumps(result), flush=True)

@@ -132,6 +132,18 @@ int iq_quantize_q80(const float *x, int64_t m, int64_t k, void *blocks_out, iq_s
 int iq_block_sums(iq_weight_t w, const float *x, int64_t m, float *y, int32_t *isum, int32_t *msum,
                   iq_stream_t stream);
 
+/* Per-block integer totals of the int8-MFMA (prefill) path: for Q4_K
+ * matrices at 64 or more input rows, iq_matmul runs this path, whose f32
+ * combination order differs from the reference's (results agree within the
+ * path's 1e-4 normwise tolerance) while each block's integers are exact.
+ * isum and msum are [m][rows][cols / 256]: isum the block's total integer
+ * dot (the sum of the reference's eight `sumi` lanes), msum its mins term
+ * (the sum of the four `prod` lanes).  y receives the product.
+ * Replaces: the per-block integers of q4k_tile (src/qgemm.rs:204-237) on the
+ * wide-M prefill path (tiled_multi_row, src/gguf.rs:493-520). */
+int iq_prefill_block_sums(iq_weight_t w, const float *x, int64_t m, float *y, int32_t *isum, int32_t *msum,
+                          iq_stream_t stream);
+
 /* ---- MoE sublayer ---------------------------------------------------------- */
 
 /* One quantised MoE sublayer: routed experts resident in HBM as the GGUF

@@ -49,6 +49,7 @@ _SIGNATURES = {
     "iq_quantize_q8k": ([P, I64, I64, P, P], INT),
     "iq_quantize_q80": ([P, I64, I64, P, P], INT),
     "iq_block_sums": ([P, P, I64, P, P, P, P], INT),
+    "iq_prefill_block_sums": ([P, P, I64, P, P, P, P], INT),
     "iq_moe_create": ([P, ctypes.POINTER(P)], INT),
     "iq_moe_destroy": ([P], INT),
     "iq_moe_forward": ([P, P, P, I64, P, P, P, P], INT),

@@ -162,13 +162,20 @@ int quantize_for(const iq_weight* w, const float* x, int64_t m, const ActView& a
     return IQ_OK;
 }
 
+// Device workspace a product of m rows needs (activation quantisation, and
+// for the int8-MFMA path its layouts and split-K partial tiles).
+size_t matmul_ws_bytes(const iq_weight* w, int64_t m) {
+    const size_t a = act_bytes(m, w->cols), p = prefill_workspace_size(view_of(w), m);
+    return a > p ? a : p;
+}
+
 int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* ws, size_t ws_bytes, int32_t* isum,
                 int32_t* msum, hipStream_t s) {
     if (int rc = check_weight(w)) return rc;
     if (m < 0) return fail(IQ_ERR_SHAPE, "negative input row count %lld", (long long)m);
     if (m == 0) return IQ_OK;
     if (!x || !y) return fail(IQ_ERR_INVALID, "null input or output pointer");
-    const size_t need = act_bytes(m, w->cols);
+    const size_t need = matmul_ws_bytes(w, m);
     if (!ws) {
         if (int rc = workspace(need, &ws)) return rc;
     } else if (ws_bytes < need) {
@@ -176,6 +183,8 @@ int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* w
     }
     hipError_t e = hipErrorNotSupported;
     if (!isum && gemv_supported(view_of(w), m)) e = launch_gemv(view_of(w), x, w->cols, m, y, w->rows, s);
+    if (e == hipErrorNotSupported && !isum && prefill_supported(view_of(w), m))
+        e = launch_prefill(view_of(w), x, w->cols, m, y, w->rows, ws, nullptr, nullptr, s);
     if (e == hipErrorNotSupported) {
         ActView a = act_carve(ws, m, w->cols);
         if (int rc = quantize_for(w, x, m, a, nullptr, s)) return rc;
@@ -310,7 +319,7 @@ IQ_API int iq_matmul(iq_weight_t w, const float* x, int64_t m, float* y, iq_stre
 
 IQ_API size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m) {
     if (!w || m <= 0) return 0;
-    return act_bytes(m, w->cols);
+    return matmul_ws_bytes(w, m);
 }
 
 IQ_API int iq_matmul_ws(iq_weight_t w, const float* x, int64_t m, float* y, void* workspace_ptr,
@@ -325,7 +334,7 @@ IQ_API int iq_matmul_host(iq_weight_t w, const float* x_host, int64_t m, float* 
     if (!x_host || !y_host) return fail(IQ_ERR_INVALID, "null input or output pointer");
     const size_t xb = (size_t)(m * w->cols) * 4, yb = (size_t)(m * w->rows) * 4;
     const size_t xo = 0, yo = (xb + 255) & ~(size_t)255, ao = yo + ((yb + 255) & ~(size_t)255);
-    const size_t need = ao + act_bytes(m, w->cols);
+    const size_t need = ao + matmul_ws_bytes(w, m);
     void* ws;
     if (int rc = workspace(need, &ws)) return rc;
     uint8_t* base = (uint8_t*)ws;
@@ -361,6 +370,20 @@ IQ_API int iq_quantize_q8k(const float* x, int64_t m, int64_t k, void* blocks_ou
 
 IQ_API int iq_quantize_q80(const float* x, int64_t m, int64_t k, void* blocks_out, iq_stream_t stream) {
     return quantize_entry(kQ8_0, x, m, k, blocks_out, (hipStream_t)stream);
+}
+
+IQ_API int iq_prefill_block_sums(iq_weight_t w, const float* x, int64_t m, float* y, int32_t* isum, int32_t* msum,
+                                 iq_stream_t stream) {
+    if (int rc = check_weight(w)) return rc;
+    if (!x || !y || !isum || !msum) return fail(IQ_ERR_INVALID, "null input, output or integer buffer");
+    if (!prefill_supported(view_of(w), m))
+        return fail(IQ_ERR_SHAPE, "the int8-MFMA path covers Q4_K matrices at %lld or more input rows (got %s, %lld)",
+                    (long long)kPrefillMinRows, dtype_name(w->dtype), (long long)m);
+    void* ws;
+    if (int rc = workspace(prefill_workspace_size(view_of(w), m), &ws)) return rc;
+    hipError_t e = launch_prefill(view_of(w), x, w->cols, m, y, w->rows, ws, isum, msum, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return IQ_OK;
 }
 
 IQ_API int iq_block_sums(iq_weight_t w, const float* x, int64_t m, float* y, int32_t* isum, int32_t* msum,

@@ -57,4 +57,15 @@ bool gemv_supported(const WeightView& w, int64_t m);
 hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                        hipStream_t s);
 
+// The int8-MFMA kernel for Q4_K weights at kPrefillMinRows or more input
+// rows (iq_prefill.hip): per-block integers exact, f32 combination in its own
+// order.  launch_prefill quantises x itself into `ws` (at least
+// prefill_workspace_size bytes); dbg_isum / dbg_msum, when not null, receive
+// the per-block integer totals [m][rows][cols / 256].
+constexpr int64_t kPrefillMinRows = 64;
+bool prefill_supported(const WeightView& w, int64_t m);
+size_t prefill_workspace_size(const WeightView& w, int64_t m);
+hipError_t launch_prefill(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                          void* ws, int32_t* dbg_isum, int32_t* dbg_msum, hipStream_t s);
+
 }  // namespace iq

@@ -1,0 +1,349 @@
+// iq_prefill.hip -- y = x . W^T for Q4_K weights at many input rows
+// (prefill), on int8 MFMA (v_mfma_i32_32x32x32_i8).
+//
+// Arithmetic.  Per block b of 256 weights, the reference's exact integers
+// are isum = sum_j sc_j * sum_{e in sub-block j} q_e a_e and msum =
+// sum_j m_j * bsum32_j (src/qgemm.rs:175-245; sc_j, m_j six-bit, q_e four-bit,
+// a_e the Q8K int8 activations).  A six-bit scale times a four-bit quant
+// does not fit int8, so the scale is split, sc = 8 sc_hi + sc_lo with both
+// parts in 0..7: the MFMA streams w1 = sc_hi q and w2 = sc_lo q (bytes
+// <= 105) give isum = 8 acc1 + acc2 exactly (one 32-wide K step is one
+// sub-block, so each step has a single scale per column).  msum comes from
+// one f16 MFMA per block over the 16 bsums of 16 values (|bsum16| <= 2048 and
+// the mins are exact in f16; products and sums stay below 2^24 in the f32
+// accumulator).  Every per-block integer is therefore the reference's, bit
+// for bit.  The f32 combination y += dx_b (dw_b isum_b - dmin_b msum_b) runs
+// in a different order than the reference's per-lane FMA chains: results
+// agree within the path's 1e-4 normwise tolerance, not bitwise (this kernel
+// serves 64+ input rows; fewer rows keep the bit-exact kernels).
+//
+// Tiling.  A workgroup (4 waves) owns 64 input rows and 128 output columns;
+// wave w owns all 64 rows and columns 32w..32w+31 (two 32 x 32 tiles).
+// Per block the workgroup stages the int8 activation tile (16 KiB), the 128
+// raw Q4_K blocks (18 KiB), the bsums and the block scales in LDS, double
+// buffered, the next block's loads in flight while the current one is
+// multiplied.  Each wave dequantises its B fragments in registers (nibbles,
+// then one packed 16-bit multiply per dword and stream).  Narrow outputs are
+// split over K, with partial tiles summed in a fixed order by a second pass.
+#include "iq_lanes.h"
+#include "iq_quant.h"
+
+namespace iq {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kPfRows = 64;   // input rows per workgroup
+constexpr int kPfCols = 128;  // output columns per workgroup (32 per wave)
+
+// Bytes of q (each < 16) times s (< 8) byte by byte: every product is below
+// 128, so two 16-bit lanes never carry into each other.
+__device__ __forceinline__ uint32_t bytes_mul_small(uint32_t q, uint32_t s) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 a = __builtin_bit_cast(u16x2, q);
+    const u16x2 b = {(unsigned short)s, (unsigned short)s};
+    return __builtin_bit_cast(uint32_t, a * b);
+}
+
+// ---- activation quantisation --------------------------------------------------
+// Q8K (bit-exact from_float) into the layouts the MFMA kernel reads:
+// q [mp][k] int8 row-major, dT [nb][mp] block scales, hs [mp][nb][16] the
+// block's sixteen 16-value sums as f16 (exact: |bsum16| <= 2048).  Rows
+// m..mp-1 are zero.
+__global__ __launch_bounds__(256) void k_quant_prefill(const float* __restrict__ x, int64_t ldx, int m, int mp,
+                                                       int nb, int8_t* __restrict__ q, float* __restrict__ dT,
+                                                       _Float16* __restrict__ hs) {
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= (int64_t)mp * nb) return;  // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int row = (int)(wid / nb), b = (int)(wid % nb);
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (row < m) v = load4(x + (int64_t)row * ldx + (int64_t)b * 256 + 4 * lane);
+    const Q8KLane r = quant_q8k_core(v);
+    ((uint32_t*)(q + (int64_t)row * nb * 256 + (int64_t)b * 256))[lane] = r.packed;
+    if (lane == 0) dT[(int64_t)b * mp + row] = r.d;
+    if ((lane & 3) == 0) hs[((int64_t)row * nb + b) * 16 + (lane >> 2)] = (_Float16)r.bsum16;
+}
+
+struct PrefillArgs {
+    const uint8_t* w;  // Q4_K [n][nb]
+    int64_t n, row_bytes;
+    int nb;
+    const int8_t* q;
+    const float* dT;
+    const _Float16* hs;
+    int m, mp;
+    float* y;  // [m][ldy] when splits == 1
+    int64_t ldy;
+    float* part;  // [splits][m][n] otherwise
+    int splits, bps;
+    int32_t* dbg_isum;  // optional [m][n][nb] per-block integers
+    int32_t* dbg_msum;
+};
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+// LDS stage: A int8 [64][kAS], B raw Q4_K [128][144], H f16 bsums [64][16],
+// D block scales [64].
+constexpr int kAS = 272;  // padded activation row stride
+constexpr int kStA = 0, kStB = kStA + kPfRows * kAS, kStH = kStB + kPfCols * 144, kStD = kStH + kPfRows * 32;
+constexpr int kStage = kStD + kPfRows * 4;
+// staging chunks of 16 bytes: A 1024, B 1152, H 128, D 16 (2320 over 256 threads: 10 each, the last partly idle)
+constexpr int kChA = kPfRows * 16, kChB = kPfCols * 9, kChH = kPfRows * 2, kChD = kPfRows / 4;
+constexpr int kChunks = kChA + kChB + kChH + kChD;
+constexpr int kChPer = (kChunks + 255) / 256;
+
+template <bool DBG>
+__global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
+    __shared__ __align__(16) uint8_t st[2][kStage];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5, li = lane & 31;
+    // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs, so
+    // ids L, L + 8, L + 16, ... (same XCD) take the m-tiles of one column
+    // tile and share its weights in that XCD's L2.
+    const int mtiles = p.mp / kPfRows;
+    const int grp = blockIdx.x / (8 * mtiles), rem = blockIdx.x - grp * 8 * mtiles;
+    const int ntile = 8 * grp + (rem & 7), mtile = rem >> 3;
+    if ((int64_t)ntile * kPfCols >= p.n) return;  // padding workgroup (whole group uniform)
+    const int n0 = ntile * kPfCols;
+    const int row0 = mtile * kPfRows;
+    const int b0 = blockIdx.z * p.bps;
+    const int b1 = min(p.nb, b0 + p.bps);
+    const int64_t K = (int64_t)p.nb * 256;
+
+    // staging: chunk t = threadIdx.x + 256 i; its global source (block b) and
+    // LDS offset (-1: none).  Every thread issues kChPer loads per block
+    // (idle ones re-read a valid chunk) so that waits stay exact.
+    int loff[kChPer];
+    auto src = [&](int t, int b) -> const u32x4a16* {
+        if (t < kChA) {
+            const int r = t >> 4, c = t & 15;
+            return (const u32x4a16*)(p.q + (int64_t)(row0 + r) * K + (int64_t)b * 256 + 16 * c);
+        }
+        t -= kChA;
+        if (t < kChB) {
+            const int col = t / 9, pc = t - 9 * col;
+            const int64_t gc = min((int64_t)n0 + col, p.n - 1);
+            return (const u32x4a16*)(p.w + gc * p.row_bytes + (int64_t)b * 144 + 16 * pc);
+        }
+        t -= kChB;
+        if (t < kChH) {
+            const int r = t >> 1, c = t & 1;
+            return (const u32x4a16*)(p.hs + ((int64_t)(row0 + r) * p.nb + b) * 16 + 8 * c);
+        }
+        t -= kChH;
+        t = min(t, kChD - 1);
+        return (const u32x4a16*)(p.dT + (int64_t)b * p.mp + row0 + 4 * t);
+    };
+#pragma unroll
+    for (int i = 0; i < kChPer; i++) {
+        int t = threadIdx.x + 256 * i;
+        if (t >= kChunks) {
+            loff[i] = -1;
+            continue;
+        }
+        if (t < kChA) loff[i] = kStA + (t >> 4) * kAS + 16 * (t & 15);
+        else if ((t -= kChA) < kChB) loff[i] = kStB + 16 * t;
+        else if ((t -= kChB) < kChH) loff[i] = kStH + 16 * t;
+        else loff[i] = kStD + 16 * (t - kChH);
+    }
+    u32x4a16 stg[kChPer];
+    auto issue = [&](int b) {
+        b = min(b, b1 - 1);
+#pragma unroll
+        for (int i = 0; i < kChPer; i++) {
+            const int t = min((int)threadIdx.x + 256 * i, kChunks - 1);
+            stg[i] = *src(t, b);
+        }
+    };
+    auto park = [&](uint8_t* s) {
+#pragma unroll
+        for (int i = 0; i < kChPer; i++)
+            if (loff[i] >= 0) *(u32x4a16*)(s + loff[i]) = stg[i];
+    };
+
+    float out[2][16];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) out[mt][r] = 0.f;
+
+    issue(b0);
+    park(st[0]);
+    lds_barrier();
+
+    const int col = 32 * wave + li;  // this lane's column within the tile (B and D layouts)
+    for (int b = b0; b < b1; b++) {
+        const uint8_t* S = st[(b - b0) & 1];
+        issue(b + 1);
+        const uint8_t* bcol = S + kStB + col * 144;
+        const u32x4a16 hdr = *(const u32x4a16*)bcol;
+        const float dw = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
+        const Q4Scales sc = q4_scales(hdr.y, hdr.z, hdr.w);
+
+        v16i acc1[2], acc2[2];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {  // K step c = sub-block c
+            // B: weights 16h..16h+15 of sub-block c = low (c even) or high
+            // nibbles of qs bytes 32 (c / 2) + 16 h ..
+            const u32x4a16 raw = *(const u32x4a16*)(bcol + 16 + 32 * (c >> 1) + 16 * h);
+            const int shn = (c & 1) * 4;
+            const uint32_t s6 = byte_of(c < 4 ? sc.sc_lo : sc.sc_hi, c & 3);
+            const uint32_t hi = s6 >> 3, lo = s6 & 7u;
+            const uint32_t qv[4] = {(raw.x >> shn) & 0x0f0f0f0fu, (raw.y >> shn) & 0x0f0f0f0fu,
+                                    (raw.z >> shn) & 0x0f0f0f0fu, (raw.w >> shn) & 0x0f0f0f0fu};
+            const v4i w1 = {(int)bytes_mul_small(qv[0], hi), (int)bytes_mul_small(qv[1], hi),
+                            (int)bytes_mul_small(qv[2], hi), (int)bytes_mul_small(qv[3], hi)};
+            const v4i w2 = {(int)bytes_mul_small(qv[0], lo), (int)bytes_mul_small(qv[1], lo),
+                            (int)bytes_mul_small(qv[2], lo), (int)bytes_mul_small(qv[3], lo)};
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                // A: row 32 mt + li, activations 16h..16h+15 of sub-block c
+                const v4i a = *(const v4i*)(S + kStA + (32 * mt + li) * kAS + 32 * c + 16 * h);
+                const v16i z = {};
+                acc1[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w1, c == 0 ? z : acc1[mt], 0, 0, 0);
+                acc2[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w2, c == 0 ? z : acc2[mt], 0, 0, 0);
+            }
+        }
+
+        // mins: msum = sum_t m_{t/2} bsum16_t, K = 16 (lane half h: t = 8h..8h+7)
+        v8h bm;
+        {
+            const uint32_t mw = h == 0 ? sc.mn_lo : sc.mn_hi;  // m_{4h} .. m_{4h+3}
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const _Float16 mv = (_Float16)(float)byte_of(mw, d);
+                bm[2 * d] = mv;
+                bm[2 * d + 1] = mv;
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            const v8h am = *(const v8h*)(S + kStH + (32 * mt + li) * 32 + 16 * h);
+            const v16f z = {};
+            const v16f msum = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, z, 0, 0, 0);
+            // D layout: lane (h, li) holds column li, rows 8 (r / 4) + 4 h + r % 4
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const f32x4 dx = *(const f32x4*)(S + kStD + 4 * (32 * mt + 8 * g + 4 * h));
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int r = 4 * g + e;
+                    const int32_t isum = 8 * acc1[mt][r] + acc2[mt][r];
+                    const float t = __builtin_fmaf(-dmin, msum[r], dw * (float)isum);
+                    out[mt][r] = __builtin_fmaf(dx[e], t, out[mt][r]);
+                    if constexpr (DBG) {
+                        const int64_t row = row0 + 32 * mt + 8 * g + 4 * h + e, gc = n0 + col;
+                        if (row < p.m && gc < p.n) {
+                            p.dbg_isum[(row * p.n + gc) * p.nb + b] = isum;
+                            p.dbg_msum[(row * p.n + gc) * p.nb + b] = (int32_t)msum[r];
+                        }
+                    }
+                }
+            }
+        }
+        // the next block's loads have had this whole block to land
+        __builtin_amdgcn_sched_barrier(0);
+        park(st[(b - b0 + 1) & 1]);
+        lds_barrier();
+    }
+
+    float* dst = p.splits == 1 ? p.y : p.part + (int64_t)blockIdx.z * p.m * p.n;
+    const int64_t ld = p.splits == 1 ? p.ldy : p.n;
+    const int64_t gc = (int64_t)n0 + col;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int64_t row = row0 + 32 * mt + 8 * (r / 4) + 4 * h + (r % 4);
+            if (row < p.m && gc < p.n) dst[row * ld + gc] = out[mt][r];
+        }
+}
+
+// y = sum over splits of the partial tiles, in split order.
+__global__ __launch_bounds__(256) void k_prefill_reduce(const float* __restrict__ part, int splits, int m, int64_t n,
+                                                        float* __restrict__ y, int64_t ldy) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)m * n) return;
+    const int64_t row = i / n, col = i - row * n;
+    float s = part[i];
+    for (int z = 1; z < splits; z++) s = s + part[(int64_t)z * m * n + i];
+    y[row * ldy + col] = s;
+}
+
+constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct PfPlan {
+    int mp, nb, splits, bps;
+    size_t q_bytes, d_bytes, hs_bytes, part_bytes;
+    size_t total() const { return q_bytes + d_bytes + hs_bytes + part_bytes; }
+};
+
+PfPlan plan(const WeightView& w, int64_t m) {
+    PfPlan P;
+    P.nb = (int)(w.cols / 256);
+    P.mp = (int)((m + kPfRows - 1) / kPfRows * kPfRows);
+    const int64_t tiles = ((w.rows + kPfCols - 1) / kPfCols) * (P.mp / kPfRows);  // real tiles (padding aside)
+    int splits = 1;
+    while (tiles * splits < 256 && splits * 2 <= P.nb && splits < 8) splits *= 2;
+    P.bps = (P.nb + splits - 1) / splits;
+    P.splits = (P.nb + P.bps - 1) / P.bps;
+    P.q_bytes = align256((size_t)P.mp * P.nb * 256);
+    P.d_bytes = align256((size_t)P.nb * P.mp * 4);
+    P.hs_bytes = align256((size_t)P.mp * P.nb * 32);
+    P.part_bytes = P.splits > 1 ? align256((size_t)P.splits * m * w.rows * 4) : 0;
+    return P;
+}
+
+}  // namespace
+
+bool prefill_supported(const WeightView& w, int64_t m) {
+    return w.dtype == kQ4_K && m >= kPrefillMinRows && w.cols % 256 == 0 && w.rows >= 1 && m <= (1 << 20);
+}
+
+size_t prefill_workspace_size(const WeightView& w, int64_t m) { return prefill_supported(w, m) ? plan(w, m).total() : 0; }
+
+hipError_t launch_prefill(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                          void* ws, int32_t* dbg_isum, int32_t* dbg_msum, hipStream_t s) {
+    if (!prefill_supported(w, m)) return hipErrorNotSupported;
+    const PfPlan P = plan(w, m);
+    uint8_t* base = (uint8_t*)ws;
+    PrefillArgs a;
+    a.w = w.w;
+    a.n = w.rows;
+    a.row_bytes = w.row_bytes;
+    a.nb = P.nb;
+    a.q = (const int8_t*)base;
+    a.dT = (const float*)(base + P.q_bytes);
+    a.hs = (const _Float16*)(base + P.q_bytes + P.d_bytes);
+    a.part = P.splits > 1 ? (float*)(base + P.q_bytes + P.d_bytes + P.hs_bytes) : nullptr;
+    a.m = (int)m;
+    a.mp = P.mp;
+    a.y = y;
+    a.ldy = ldy;
+    a.splits = P.splits;
+    a.bps = P.bps;
+    a.dbg_isum = dbg_isum;
+    a.dbg_msum = dbg_msum;
+    const int64_t qwaves = (int64_t)P.mp * P.nb;
+    hipLaunchKernelGGL(k_quant_prefill, dim3((unsigned)((qwaves + 3) / 4)), dim3(256), 0, s, x, ldx, (int)m, P.mp,
+                       P.nb, (int8_t*)a.q, (float*)a.dT, (_Float16*)a.hs);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t ntiles = (w.rows + kPfCols - 1) / kPfCols;
+    dim3 grid((unsigned)((ntiles + 7) / 8 * 8 * (P.mp / kPfRows)), 1, (unsigned)P.splits);
+    if (dbg_isum) hipLaunchKernelGGL(k_prefill_q4k<true>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(k_prefill_q4k<false>, grid, dim3(256), 0, s, a);
+    e = hipGetLastError();
+    if (e != hipSuccess || P.splits == 1) return e;
+    const int64_t tot = m * w.rows;
+    hipLaunchKernelGGL(k_prefill_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, (const float*)a.part,
+                       P.splits, (int)m, w.rows, y, ldy);
+    return hipGetLastError();
+}
+
+}  // namespace iq

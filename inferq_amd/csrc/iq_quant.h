@@ -29,9 +29,16 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 }
 
 // Q8K of one 256-value group whose values 4l..4l+3 lane l already holds
-// (all 64 lanes call it): writes row `row`, group `g` of `a` and, when `ref`
-// is not null, the reference 292-byte block.
-__device__ __forceinline__ void quant_q8k_vals4(const f32x4 v, int64_t row, int g, const ActView& a, uint8_t* ref) {
+// (all 64 lanes call it).  Returns lane l's four int8 packed in a dword,
+// the block scale d (every lane), the sum of the lane's 16-value sub-block
+// (lanes 4j..4j+3: bsums[j]) and of its 32-value sub-block (lanes
+// 8c..8c+7).
+struct Q8KLane {
+    uint32_t packed;
+    float d;
+    int bsum16, sum32;
+};
+__device__ __forceinline__ Q8KLane quant_q8k_core(const f32x4 v) {
     const int lane = threadIdx.x & 63;
     // amax and the first index reaching it (the reference updates only on a
     // strictly larger |x| while scanning upwards)
@@ -68,22 +75,32 @@ __device__ __forceinline__ void quant_q8k_vals4(const f32x4 v, int64_t row, int 
         }
         dval = __fdiv_rn(1.f, iscale);
     }
-    const uint32_t packed = pack4(q[0], q[1], q[2], q[3]);
+    Q8KLane r;
+    r.packed = pack4(q[0], q[1], q[2], q[3]);
     int s = q[0] + q[1] + q[2] + q[3];
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
-    const int bsum16 = s;   // lanes 4j..4j+3: bsums[j]
-    s += __shfl_xor(s, 4);  // lanes 8c..8c+7: sum of 32-value sub-block c
+    r.bsum16 = s;
+    s += __shfl_xor(s, 4);
+    r.sum32 = s;
+    r.d = dval;
+    return r;
+}
 
+// quant_q8k_core into row `row`, group `g` of `a` and, when `ref` is not
+// null, the reference 292-byte block.
+__device__ __forceinline__ void quant_q8k_vals4(const f32x4 v, int64_t row, int g, const ActView& a, uint8_t* ref) {
+    const int lane = threadIdx.x & 63;
+    const Q8KLane r = quant_q8k_core(v);
     const int c = lane >> 3, k = lane & 7;
     uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
-    qrow[perm_dword(c, k)] = packed;
-    if (k == 0) a.s8[(row * a.ng + g) * 8 + c] = (int16_t)s;
-    if (lane == 0) a.d[row * a.ldd + g] = dval;
+    qrow[perm_dword(c, k)] = r.packed;
+    if (k == 0) a.s8[(row * a.ng + g) * 8 + c] = (int16_t)r.sum32;
+    if (lane == 0) a.d[row * a.ldd + g] = r.d;
     if (ref) {
-        if (lane == 0) *(float*)ref = dval;
-        *(uint32_t*)(ref + 4 + 4 * lane) = packed;
-        if ((lane & 3) == 0) *(int16_t*)(ref + 260 + 2 * (lane >> 2)) = (int16_t)bsum16;
+        if (lane == 0) *(float*)ref = r.d;
+        *(uint32_t*)(ref + 4 + 4 * lane) = r.packed;
+        if ((lane & 3) == 0) *(int16_t*)(ref + 260 + 2 * (lane >> 2)) = (int16_t)r.bsum16;
     }
 }
 

@@ -80,8 +80,9 @@ class QuantizedMatrix:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and _lib._lib is not None:
-            _lib._lib.iq_weights_free(h)
+        L = getattr(_lib, "_lib", None) if _lib is not None else None  # module globals are gone at interpreter exit
+        if h is not None and L is not None:
+            L.iq_weights_free(h)
             self._h = None
 
     # ---- reference accessors (src/gguf.rs:322-332) --------------------
@@ -190,6 +191,21 @@ class QuantizedMatrix:
         check(lib().iq_block_sums(self._h, xs.data_ptr(), m, y.data_ptr(), isum.data_ptr(), msum.data_ptr(),
                                   _stream()))
         return y, isum, (msum if self._dtype == IQ_Q4_K else None)
+
+    def prefill_block_sums(self, xs):
+        """Product and per-block integer totals of the int8-MFMA path (Q4_K,
+        64+ rows; see iq_prefill_block_sums): y, isum, msum [m, rows, blocks]."""
+        import torch
+
+        xs = self._validated_input(xs)
+        m = xs.numel() // self._cols
+        nb = self._cols // 256
+        y = torch.empty(m, self._rows, dtype=torch.float32, device=xs.device)
+        isum = torch.empty(m, self._rows, nb, dtype=torch.int32, device=xs.device)
+        msum = torch.empty(m, self._rows, nb, dtype=torch.int32, device=xs.device)
+        check(lib().iq_prefill_block_sums(self._h, xs.data_ptr(), m, y.data_ptr(), isum.data_ptr(), msum.data_ptr(),
+                                          _stream()))
+        return y, isum, msum
 
 
 def quantize_q8k(xs):

@@ -1,0 +1,79 @@
+"""GPU parity of the int8-MFMA prefill path (Q4_K, 64 or more input rows)
+through the C ABI.
+
+Tolerance: per-block integers (the block's total integer dot and its mins
+term) are compared bit for bit with the oracle; outputs within a normwise
+relative error of 1e-4 per output row (max_j |g - r| / max_j |r|), the
+path's stated f32 bar -- this path combines the block integers in f32 in a
+different order than the reference's per-lane FMA chains.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bitexact, assert_close_normwise
+from inferq_amd import qgemm as Q
+from inferq_amd import synth as S
+
+pytestmark = pytest.mark.gpu
+
+Q4 = S.Q4_K
+
+
+def _rowwise_close(got, ref, tol, what):
+    for r in range(ref.shape[0]):
+        assert_close_normwise(got[r], ref[r], tol, f"{what} row {r}")
+
+
+def test_prefill_block_integers_exact(gpu, oracle):
+    """Ragged rows (70, not a multiple of 16) and columns (40, not a
+    multiple of 32): every (row, column, block) integer pair equals the
+    oracle's textbook integers."""
+    rng = np.random.default_rng(61)
+    rows, cols, m = 40, 512, 70
+    w = S.random_matrix(Q4, rows, cols, rng)
+    x = S.normal((m, cols), rng)
+    mat = Q.QuantizedMatrix.upload(w, Q4, rows, cols)
+    y, isum, msum = mat.prefill_block_sums(torch.from_numpy(x).to(gpu))
+    isum, msum = isum.cpu().numpy(), msum.cpu().numpy()
+    wb = w.view(oracle.BLOCK[Q4]).reshape(rows, cols // 256)
+    for t in range(m):
+        q = oracle.quantize_q8k(x[t])
+        for n in range(rows):
+            for b in range(cols // 256):
+                ti, tm = oracle.block_textbook(Q4, wb[n, b], q[b])
+                assert isum[t, n, b] == ti and msum[t, n, b] == tm, (t, n, b)
+    _rowwise_close(y.cpu().numpy(), oracle.matmul(Q4, w, rows, cols, x), 1e-4, "prefill product")
+
+
+@pytest.mark.parametrize("rows,cols,m", [(1024, 2048, 256), (2048, 4096, 256), (300, 2048, 100), (64, 256, 64)])
+def test_prefill_matches_oracle(gpu, oracle, rows, cols, m):
+    """BASELINE configs[3] shapes scaled to what the oracle computes in
+    seconds, a split-K shape (narrow output, wide input), ragged sizes."""
+    rng = np.random.default_rng(rows + cols + m)
+    w = S.random_matrix(Q4, rows, cols, rng)
+    x = S.normal((m, cols), rng)
+    mat = Q.QuantizedMatrix.upload(w, Q4, rows, cols)
+    got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    ref = oracle.matmul(Q4, w, rows, cols, x, nthreads=8)
+    _rowwise_close(got, ref, 1e-4, f"prefill [{rows}x{cols}] m={m}")
+
+
+def test_prefill_is_deterministic(gpu):
+    rng = np.random.default_rng(62)
+    w = S.random_matrix(Q4, 2048, 4096, rng)
+    mat = Q.QuantizedMatrix.upload(w, Q4, 2048, 4096)
+    x = torch.from_numpy(S.normal((256, 4096), rng)).to(gpu)
+    a = mat.forward(x).cpu().numpy()
+    b = mat.forward(x).cpu().numpy()
+    assert_bitexact(a, b, "run to run")
+
+
+def test_below_prefill_threshold_stays_bitexact(gpu, oracle):
+    """63 rows run the bit-exact kernels, 64 the MFMA path."""
+    rng = np.random.default_rng(63)
+    w = S.random_matrix(Q4, 256, 2048, rng)
+    x = S.normal((63, 2048), rng)
+    mat = Q.QuantizedMatrix.upload(w, Q4, 256, 2048)
+    assert_bitexact(mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy(),
+                    oracle.matmul(Q4, w, 256, 2048, x), "63 rows")
