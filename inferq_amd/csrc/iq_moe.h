@@ -48,6 +48,11 @@ struct MoeParams {
 // events (may be null): 4 hipEvent_t recorded before and between the launches.
 hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
                       hipEvent_t const* events = nullptr);
+// The 2..16-token path (iq_moe_verify.hip); moev_supported tells whether it
+// covers a call.
+bool moev_supported(const MoeParams& p, int gate_dtype, int down_dtype);
+hipError_t launch_moe_verify(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
+                             hipEvent_t const* events);
 // One launch of a call already made with these parameters (stage 0 routing
 // of the grouped path, 1 gate/up, 2 down).
 hipError_t launch_moe_stage(const MoeParams& p, int gate_dtype, int down_dtype, int stage, hipStream_t s);
