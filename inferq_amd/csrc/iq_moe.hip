@@ -283,26 +283,24 @@ __device__ void moe1_route(const MoeParams& p, int wave) {
         int sel[kMoe1MaxSlots];
         route_load(p.logits, E, lv);
         route_topk_any<kMoe1MaxSlots>(lv, E, K, sel);
+        if (lane == 0)  // the down launch needs the ids first
+            for (int s = 0; s < K; s++) p.experts[s] = sel[s];
         route_weights<kMoe1MaxSlots>(lv, E, K, sel, p.normalize, s_scratch, wt);
-        if (lane == 0) {
-            for (int s = 0; s < K; s++) {
-                p.experts[s] = sel[s];
-                p.weights[s] = wt[s];
-            }
-        }
+        if (lane == 0)
+            for (int s = 0; s < K; s++) p.weights[s] = wt[s];
     } else if (wave == 1 && p.sdown_w) {
         const float gate = selector_gate(p.x, p.selector, p.H);
         if (lane == 0) p.sgate[0] = gate;
     }
 }
 
-// Grid (I/8, slots + 1).  Workgroup (x, s < slots): 8 intermediate rows of
+// Grid (I/8, slots + 1).  Workgroup (x, s + 1): 8 intermediate rows of
 // gate and up of the expert at route rank s (or the shared expert), 4 waves
 // each taking a quarter of the NG blocks along hidden.  Each wave forms its
 // blocks' exact lane integers and f32 scales; wave 0 then advances the
 // accumulators through all NG blocks in order (the reference's chain),
 // reduces them with the hsum trees, applies SwiGLU and stores act[s][i].
-// Row slots + 1 holds the routing workgroup (x == 0).
+// Row 0 holds the routing workgroup (x == 0).
 template <int GFMT, int NG>
 __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
@@ -316,12 +314,12 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = (int)p.K;
-    const int nslots = K + (p.sdown_w ? 1 : 0);
-    const int sidx = blockIdx.y;
-    if (sidx == nslots) {
+    // row 0 holds the routing workgroup, dispatched ahead of the slots
+    if (blockIdx.y == 0) {
         if (blockIdx.x == 0) moe1_route(p, wave);
         return;
     }
+    const int sidx = blockIdx.y - 1;
     // small inputs first: logits, and this wave's x blocks
     constexpr int LPB = 256 / VPL;
     const int g0 = wave * NB;

@@ -17,47 +17,11 @@
 
 namespace iq {
 
-// Order-preserving 64-bit key: logit (NaN ranks lowest, -0 equals +0) in
-// the high word, complemented index in the low word.  0 marks "taken".
-__device__ __forceinline__ uint64_t route_key(float x, int idx) {
-    if (x != x) x = -INFINITY;
-    if (x == 0.f) x = 0.f;
-    uint32_t b = __builtin_bit_cast(uint32_t, x);
-    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)b << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
-}
-
-__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-__device__ __forceinline__ uint64_t dpp64(uint64_t v, int ctrl_sel) {
-    int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
-    switch (ctrl_sel) {
-    case 0: lo = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, false); break;
-    case 1: lo = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xF, 0xF, false); break;
-    case 2: lo = __builtin_amdgcn_mov_dpp(lo, 0x124, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0x124, 0xF, 0xF, false); break;
-    default: lo = __builtin_amdgcn_mov_dpp(lo, 0x128, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0x128, 0xF, 0xF, false); break;
-    }
-    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
-}
-
-// Maximum of v over the 64 lanes of the wave (every lane gets it).
-__device__ __forceinline__ uint64_t wave_max64(uint64_t v) {
-    v = umax64(v, dpp64(v, 0));  // quad: xor 1
-    v = umax64(v, dpp64(v, 1));  // quad: xor 2
-    v = umax64(v, dpp64(v, 2));  // row: rotate 4
-    v = umax64(v, dpp64(v, 3));  // row: rotate 8
-    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
-    uint64_t r = 0;
-#pragma unroll
-    for (int row = 0; row < 4; row++) {
-        const uint64_t rv = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, 16 * row) << 32) |
-                            (uint32_t)__builtin_amdgcn_readlane(lo, 16 * row);
-        r = umax64(r, rv);
-    }
-    return r;
-}
-
 constexpr int kRoutePer = 8;  // logits per lane (E <= 512)
+
+// Logits per lane: lane l holds logits per*l .. per*l + per - 1, so lane
+// order is index order.
+__device__ __forceinline__ int route_per(int E) { return E <= 256 ? 4 : 8; }
 
 // Order-preserving 32-bit key of a logit (NaN lowest among logits, -0 == +0);
 // 0 is below every key and marks "taken" or "absent".
@@ -68,54 +32,65 @@ __device__ __forceinline__ uint32_t route_ukey(float x) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// Maximum of v over the 64 lanes, in every lane: two lane-half swaps
+// (v_permlane32_swap, v_permlane16_swap) and four DPP steps inside rows.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false));
-    const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
-    const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
-    return max(a, b);
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = max(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(b[0], b[1]);
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));  // row half mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));  // row mirror
+    return v;
 }
 
-// Lane l's logits l + 64 j (-inf past E).
+// The lane's logits (-inf past E), 16-byte loads when E is 256 or 512 and
+// the row is aligned.
 __device__ __forceinline__ void route_load(const float* lg, int E, float (&lv)[kRoutePer]) {
     const int lane = threadIdx.x & 63;
+    const int per = route_per(E);
+    if ((E == 256 || E == 512) && ((uintptr_t)lg & 15) == 0) {
+        const f32x4* v = (const f32x4*)(lg + per * lane);
+        const f32x4 a = v[0];
+        f32x4 b = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (E == 512) b = v[1];
+        lv[0] = a.x; lv[1] = a.y; lv[2] = a.z; lv[3] = a.w;
+        lv[4] = b.x; lv[5] = b.y; lv[6] = b.z; lv[7] = b.w;
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < kRoutePer; j++) {
-        const int i = lane + 64 * j;
-        lv[j] = i < E ? lg[i] : -INFINITY;
+        const int i = per * lane + j;
+        lv[j] = (j < per && i < E) ? lg[i] : -INFINITY;
     }
 }
 
 // Top-`count` experts by (logit desc, index asc) from route_load's values:
-// sel[0..count) wave-uniform.  PER = logits per lane actually present
-// (ceil(E / 64)).  Each round takes the wave maximum of the 32-bit keys,
-// then the lowest index holding it (first non-empty ballot, lowest lane).
+// sel[0..count) wave-uniform.  Each round takes the wave maximum of the
+// lanes' largest remaining keys; the lowest lane holding it holds the lowest
+// index among equal logits (lane order is index order), and within that lane
+// the first position holding it is the lowest.
 template <int MAXK, int PER>
 __device__ __forceinline__ void route_topk_vals(const float (&lv)[kRoutePer], int E, int count, int (&sel)[MAXK]) {
     const int lane = threadIdx.x & 63;
     uint32_t key[PER];
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int i = lane + 64 * j;
-        key[j] = i < E ? route_ukey(lv[j]) : 0u;
-    }
+    for (int j = 0; j < PER; j++) key[j] = PER * lane + j < E ? route_ukey(lv[j]) : 0u;
     for (int s = 0; s < count; s++) {
         uint32_t m = key[0];
 #pragma unroll
         for (int j = 1; j < PER; j++) m = max(m, key[j]);
         const uint32_t best = wave_max_u32(m);
-        int win = -1;
+        const int L = (int)__builtin_ctzll(__ballot(m == best));
+        int jf = PER - 1;
 #pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const unsigned long long b = __ballot(key[j] == best);
-            if (win < 0 && b) win = (__ffsll((long long)b) - 1) + 64 * j;
-        }
+        for (int j = PER - 2; j >= 0; j--) jf = key[j] == m ? j : jf;
+        const int j = __builtin_amdgcn_readlane(jf, L);
 #pragma unroll
-        for (int j = 0; j < PER; j++)
-            if (win == lane + 64 * j) key[j] = 0u;
-        sel[s] = win;
+        for (int q = 0; q < PER; q++) key[q] = (lane == L && q == j) ? 0u : key[q];
+        sel[s] = PER * L + j;
     }
 }
 
@@ -143,10 +118,11 @@ __device__ __forceinline__ void route_weights(const float (&lv)[kRoutePer], int 
     for (int j = 0; j < kRoutePer; j++) mx = fmaxf(mx, lv[j]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const int per = route_per(E);
 #pragma unroll
     for (int j = 0; j < kRoutePer; j++) {
-        const int i = lane + 64 * j;
-        if (i < E) scratch[i] = exp_f32(lv[j] - mx);
+        const int i = per * lane + j;
+        if (j < per && i < E) scratch[i] = exp_f32(lv[j] - mx);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
