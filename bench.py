@@ -199,18 +199,29 @@ def time_moe_graph(layers, xs, logits, out, steps, warmup, hip):
     return wall, per
 
 
-def time_calls(fn, iters, hip, stream, warmup=3):
+def time_graph(fn, iters, hip, warmup=3):
+    """`iters` calls of fn(i) captured once in a HIP graph and replayed: GPU
+    time per call without host submission gaps.  Every captured call runs
+    once eagerly first, which grows the library's per-layer workspaces, so
+    the capture itself allocates nothing."""
     import torch
 
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
     t0, t1 = hip.events(2)
-    hip.record(t0, stream)
-    for i in range(iters):
-        fn(warmup + i)
-    hip.record(t1, stream)
-    torch.cuda.synchronize()
+    with torch.cuda.stream(cap):
+        for i in range(warmup + iters):
+            fn(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(iters):
+                fn(warmup + i)
+        graph.replay()
+        torch.cuda.synchronize()
+        hip.record(t0, cap.cuda_stream)
+        graph.replay()
+        hip.record(t1, cap.cuda_stream)
+        torch.cuda.synchronize()
     ms = hip.ms(t0, t1) / iters
     hip.destroy([t0, t1])
     return ms
@@ -257,7 +268,7 @@ def secondary(args, hip, stream, device, layers):
                                        synth.Q8_0, 4096, 2048) for c in range(copies)]
     x = torch.randn(2048, 2048, device=device).reshape(-1, 1, 2048)
     y = torch.empty(1, 4096, device=device)
-    ms = time_calls(lambda i: mats[i % copies].forward_into(x[i % 2048], y), args.steps, hip, stream)
+    ms = time_graph(lambda i: mats[i % copies].forward_into(x[i % 2048], y), args.steps, hip)
     b = mats[0].storage_bytes() + 2048 * 4 + 4096 * 4
     extra["q8_0_matvec_4096x2048"] = {"us": round(ms * 1e3, 3), "GB_s": round(b / ms / 1e6, 1),
                                       "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
@@ -266,13 +277,13 @@ def secondary(args, hip, stream, device, layers):
     lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 60),
                                     synth.Q6_K, 248320, 2048)
     yl = torch.empty(1, 248320, device=device)
-    ms = time_calls(lambda i: lm.forward_into(x[i % 2048], yl), max(10, args.steps // 10), hip, stream)
+    ms = time_graph(lambda i: lm.forward_into(x[i % 2048], yl), max(10, args.steps // 10), hip)
     b = lm.storage_bytes() + 2048 * 4 + 248320 * 4
     extra["lm_head_q6k_248320x2048_m1"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1),
                                            "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
     x8 = torch.randn(8, 2048, device=device)
     y8 = torch.empty(8, 248320, device=device)
-    ms = time_calls(lambda i: lm.forward_into(x8, y8), 10, hip, stream, warmup=2)
+    ms = time_graph(lambda i: lm.forward_into(x8, y8), 10, hip, warmup=2)
     extra["lm_head_q6k_m8"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1)}
     del lm
     # config 3: verify pass MoE at M = 4 and 8 (independent routing per row)
@@ -283,12 +294,33 @@ def secondary(args, hip, stream, device, layers):
         xs = torch.randn(64, m, H, device=device, generator=g)
         lg = torch.randn(64, m, E, device=device, generator=g)
         out = torch.empty(m, H, device=device)
-        ms = time_calls(lambda i: layers[i % n][0].forward_into(xs[i % 64], lg[i % 64], out), 40, hip, stream)
+        ms = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 64], lg[i % 64], out), 40, hip)
         uniq = float(np.mean([len(torch.unique(torch.topk(lg[j], TOPK, dim=1).indices)) for j in range(64)]))
         kb = moe_kernel_bytes(m, uniq)
         tot = kb["gate_up"] + kb["down"] + kb["prep"]
         extra[f"moe_layer_m{m}"] = {"us": round(ms * 1e3, 2), "unique_experts": round(uniq, 1),
                                     "GB_s": round(tot / ms / 1e6, 1), "frac_hbm": round(tot / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    # configs 2/3: dense projections beside the MoE (attention q/gate, k, v, o),
+    # one call each per step, rotated over copies beyond the MALL
+    shapes = (("q_gate", 8192, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 4096))
+    copies = 8
+    proj = [[qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, n, k, device, 700 + 10 * c + j),
+                                        synth.Q4_K, n, k) for j, (_, n, k) in enumerate(shapes)] for c in range(copies)]
+    pbytes = sum(p.storage_bytes() for p in proj[0])
+    for m in (1, 4, 8):
+        xin = {k: torch.randn(m, k, device=device) for k in (2048, 4096)}
+        yout = [torch.empty(m, n, device=device) for _, n, _ in shapes]
+
+        def step(i):
+            mats = proj[i % copies]
+            for j, (_, n, k) in enumerate(shapes):
+                mats[j].forward_into(xin[k], yout[j])
+
+        ms = time_graph(step, 50, hip)
+        b = pbytes + m * 4 * sum(n + k for _, n, k in shapes)
+        extra[f"dense_projections_m{m}"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1),
+                                            "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    del proj
     return extra
 
 
@@ -308,12 +340,36 @@ def prefill(args, hip, stream, device):
                                            n, k) for c in range(copies)]
         x = torch.randn(256, k, device=device)
         y = torch.empty(256, n, device=device)
-        ms = time_calls(lambda i: mats[i % copies].forward_into(x, y), max(20, args.steps // 4), hip, stream)
+        ms = time_graph(lambda i: mats[i % copies].forward_into(x, y), max(20, args.steps // 4), hip)
         tops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
         res[f"q4k_256x{k}_to_{n}"] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
                                       "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         del mats
     return res
+
+
+def prefill_moe(args, hip, stream, device, layers):
+    """BASELINE configs[3], MoE part: 256 tokens, top-8 of 256 experts with
+    Dirichlet(0.3) router skew, plus the shared expert.  TOPS counts the
+    expert products actually routed: 2 * (rows routed + 256 shared) * 3 * I * H."""
+    import torch
+
+    n = len(layers)
+    g = np.random.default_rng(args.seed + 5)
+    m = 256
+    lgs, xs = [], []
+    for j in range(8):
+        p = g.dirichlet(np.full(E, 0.3))
+        lgs.append(torch.from_numpy((g.standard_normal((m, E)) + np.log(np.maximum(p, 1e-30))).astype(np.float32))
+                   .to(device))
+        xs.append(torch.randn(m, H, device=device))
+    out = torch.empty(m, H, device=device)
+    ms = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 8], lgs[i % 8], out), 20, hip)
+    ops = 2 * (m * TOPK + m) * 3 * I * H
+    uniq = float(np.mean([len(torch.unique(torch.topk(lg, TOPK, dim=1).indices)) for lg in lgs]))
+    tops = ops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 2), "unique_experts": round(uniq, 1), "TOPS": round(tops, 1),
+            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
 
 
 def main():
@@ -447,6 +503,7 @@ def main():
     if not args.no_secondary:
         result["extra"] = secondary(args, hip, stream, device, layers)
         result["extra"]["prefill_int8_tops"] = prefill(args, hip, stream, device)
+        result["extra"]["prefill_moe_m256_dirichlet"] = prefill_moe(args, hip, stream, device, layers)
         log(f"secondary: {result['extra']}")
 
     print(json.dumps(result), flush=True)

@@ -8,6 +8,7 @@ namespace iq {
 constexpr int kMoeMaxExperts = 512;   // routed experts per layer
 constexpr int kMoeMaxTopK = 16;       // experts per token
 constexpr int kMoeMaxAssign = 4096;   // tokens * top_k per call
+constexpr int kMoePrefillMinTokens = 17;  // the MFMA path serves calls of this many tokens or more
 
 struct MoeParams {
     // layer (device pointers, GGUF native layout)
@@ -42,6 +43,12 @@ struct MoeParams {
     float* act = nullptr;           // [P][I] SwiGLU output
     ActView aq;                     // act quantised, P rows of width I
     float* vals = nullptr;          // [P][H] expert outputs before the combine
+    // MFMA (prefill) path
+    _Float16* xhs = nullptr;        // [M][H/256][16] 16-value sums of quantised x
+    _Float16* ahs = nullptr;        // [P][I/256][16] the same of quantised act
+    int32_t* chunk_group = nullptr;  // [max_chunks] group of each 32-row chunk
+    int32_t* chunk_r0 = nullptr;     // [max_chunks] first row of the chunk in its group
+    int max_chunks = 0;
 };
 
 // Launch prep, gate_up and down for one layer call.
@@ -53,6 +60,12 @@ hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStr
 bool moev_supported(const MoeParams& p, int gate_dtype, int down_dtype);
 hipError_t launch_moe_verify(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
                              hipEvent_t const* events);
+// The many-token path on int8 MFMA (iq_moe_prefill.hip).
+bool moep_supported(const MoeParams& p, int gate_dtype, int down_dtype);
+hipError_t launch_moe_prefill(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
+                              hipEvent_t const* events);
+// Upper bound of the 32-row chunks a call of M tokens makes.
+int moep_max_chunks(int64_t M, int64_t K, int64_t E);
 // One launch of a call already made with these parameters (stage 0 routing
 // of the grouped path, 1 gate/up, 2 down).
 hipError_t launch_moe_stage(const MoeParams& p, int gate_dtype, int down_dtype, int stage, hipStream_t s);

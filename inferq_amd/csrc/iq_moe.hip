@@ -543,6 +543,7 @@ hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hip
         }
     }
     if (moev_supported(p, gfmt, dfmt)) return launch_moe_verify(p, gfmt, dfmt, s, ev);
+    if (moep_supported(p, gfmt, dfmt)) return launch_moe_prefill(p, gfmt, dfmt, s, ev);
     const int64_t qwaves = (int64_t)p.M * p.xq.ng;
     const unsigned prep_blocks = 1 + (unsigned)((qwaves + 3) / 4);
     if (ev) (void)hipEventRecord(ev[0], s);

@@ -53,6 +53,12 @@ size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
     uint8_t* act = take(P * I * 4);
     uint8_t* aq = take(act_bytes(P, I));
     uint8_t* vals = take(P * H * 4);
+    const int64_t ngH = (H + 255) / 256;
+    const int maxch = moep_max_chunks(m, K, L->layer.E);
+    uint8_t* xhs = take(m * ngH * 32);
+    uint8_t* ahs = take(P * ngI * 32);
+    uint8_t* chg = take((size_t)maxch * 4);
+    uint8_t* chr = take((size_t)maxch * 4);
     if (p) {
         p->experts = (int32_t*)experts;
         p->weights = (float*)weights;
@@ -68,6 +74,11 @@ size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
         p->act = (float*)act;
         p->aq = act_carve(aq, P, I);
         p->vals = (float*)vals;
+        p->xhs = (_Float16*)xhs;
+        p->ahs = (_Float16*)ahs;
+        p->chunk_group = (int32_t*)chg;
+        p->chunk_r0 = (int32_t*)chr;
+        p->max_chunks = maxch;
     }
     (void)ctr;
     return off;

@@ -82,6 +82,40 @@ def test_qwen_shaped_moe_matches_oracle(gpu, oracle, qwen_layer, m):
     assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, f"Qwen-shaped MoE m={m}")
 
 
+def _dirichlet_logits(m, n_experts, rng, alpha=0.3):
+    """Router logits N(0,1) plus log p with p ~ Dirichlet(alpha): per-expert
+    token counts follow that skew (prefill width)."""
+    p = rng.dirichlet(np.full(n_experts, alpha))
+    return (S.normal((m, n_experts), rng) + np.log(np.maximum(p, 1e-30))).astype(np.float32)
+
+
+@pytest.mark.parametrize("m", [17, 64, 256])
+def test_prefill_width_moe_matches_oracle(gpu, oracle, qwen_layer, m):
+    """Past the verify sizes (17 rows up to the prefill width of 256) with
+    skewed routing: large groups on a few experts, most experts idle."""
+    moe, _ = _device_layer(qwen_layer, 8, gpu)
+    rng = np.random.default_rng(300 + m)
+    x = S.normal((m, 2048), rng)
+    logits = _dirichlet_logits(m, 256, rng)
+    out = moe.forward(torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu))
+    ref, ref_e, ref_w = oracle.moe_forward(_oracle_layer(qwen_layer, 8), x, logits, mode=1, impl=_impl(oracle),
+                                           nthreads=8)
+    assert [r.experts for r in out.routes] == ref_e.tolist()
+    assert_close_normwise(np.array([r.weights for r in out.routes]), ref_w, 1e-6, "route weights")
+    assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, f"prefill-width MoE m={m}")
+
+
+def test_skewed_grouped_call_equals_single_token_calls(gpu, qwen_layer):
+    """32 rows with skewed routing in one call equal 32 one-row calls."""
+    moe, _ = _device_layer(qwen_layer, 8, gpu)
+    rng = np.random.default_rng(98)
+    x = torch.from_numpy(S.normal((32, 2048), rng)).to(gpu)
+    logits = torch.from_numpy(_dirichlet_logits(32, 256, rng)).to(gpu)
+    grouped = moe.forward(x, logits).hidden.cpu().numpy()
+    singles = np.concatenate([moe.forward(x[i:i + 1], logits[i:i + 1]).hidden.cpu().numpy() for i in range(32)])
+    assert_bitexact(grouped, singles, "skewed grouped vs per-token")
+
+
 def test_grouped_equals_single_token_calls(gpu, qwen_layer):
     """A multi-token (grouped) call equals one call per token, bitwise
     (src/qwen/quantized_moe.rs:570-591)."""
