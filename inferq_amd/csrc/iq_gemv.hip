@@ -21,6 +21,8 @@
 // groups.  Q6_K blocks at 2 (mod 4) bytes are read as aligned dword pairs and
 // funnel-shifted; the parity of every block in a slice is a compile-time
 // constant because slices hold a multiple of 8 blocks.
+#include <type_traits>
+
 #include "iq_lanes.h"
 #include "iq_quant.h"
 
@@ -302,37 +304,60 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
             if (loff[i] >= 0) *(u32x4a16*)(wl + loff[i]) = st[i];
     };
 
-    // quantise the input tile into LDS
-    // Quantise the input tile into LDS.  One input row (at most 16 groups:
-    // waves 0 and 1, one pass each): the first two slices go out between
-    // loading and quantising it, so the quantisation runs under their memory
-    // latency.  Several rows: quantise first, then issue (an input load
-    // issued after the weight loads could only be waited for together with
-    // them).
+    // Quantise the input tile into LDS.  Where every input load of a wave
+    // fits in its registers, the first two weight slices go out between
+    // loading and quantising, so the quantisation runs under their memory
+    // latency; larger tiles quantise first, then issue (an input load issued
+    // after the weight loads could only be waited for together with them).
     constexpr bool kEarly = MT == 1;
     const int npass = (MT * p.nu + 7) / 8;
     u32x4a16 stA[G::NL], stB[G::NL];
     const ActView al = act_view_lds<FMT, MT>(smem, p.nu);
     int32_t* corr = FMT == kQ6_K ? (int32_t*)(smem + act_corr_offset<FMT, MT>(p.nu)) : nullptr;
-    if constexpr (kEarly) {
+    if constexpr (kEarly && FMT != kQ8_0) {
+        // K-quants at one input row (nu = 8 or 16 groups): wave w quantises
+        // groups nu/4 * w .. +nu/4, nu values per lane
+        auto early = [&](auto vpl) {
+            constexpr int VPL = decltype(vpl)::value, LPB = 256 / VPL;
+            const int gq = (VPL / 4) * wave + lane / LPB;
+            float xv[VPL];
+            q8k_vpl_load<VPL>(p.x + (int64_t)m0 * p.ldx + (int64_t)gq * 256, xv);
+            issue(stA, 0);
+            issue(stB, 1);
+            quant_q8k_vpl<VPL>(xv, true, 0, gq, al, corr);
+        };
+        if (p.nu == 8) early(std::integral_constant<int, 8>{});
+        else early(std::integral_constant<int, 16>{});
+    } else if constexpr (kEarly) {
         float xv[32];
         if (wave < npass) quant_pass_load<MT>(p, m0, mc, wave, xv);
         issue(stA, 0);
         issue(stB, 1);
         if (wave < npass) quant_pass_store<FMT, MT>(p, al, corr, wave, xv);
+    } else if (npass <= 8) {
+        // up to two passes per wave: the wave's input loads, then the first
+        // weight loads, then the quantisation, which runs under their
+        // latency (the input loads, issued first, are waited for alone)
+        float xv[2][32];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            if (wave + 4 * i < npass) quant_pass_load<MT>(p, m0, mc, wave + 4 * i, xv[i]);
+        issue(stA, 0);
+        issue(stB, 1);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            if (wave + 4 * i < npass) quant_pass_store<FMT, MT>(p, al, corr, wave + 4 * i, xv[i]);
     } else {
         for (int ps = wave; ps < npass; ps += 4) {
             float xv[32];
             quant_pass_load<MT>(p, m0, mc, ps, xv);
             quant_pass_store<FMT, MT>(p, al, corr, ps, xv);
         }
-    }
-    lds_barrier();
-    if (nitems == 0) return;  // uniform per wave; no barrier follows
-    if constexpr (!kEarly) {
         issue(stA, 0);
         issue(stB, 1);
     }
+    lds_barrier();
+    if (nitems == 0) return;  // uniform per wave; no barrier follows
 
     const ActLds<FMT, MT> act(smem, p.nu);
     uint8_t* wl = smem + p.act_lds + wave * G::WAVE_LDS;
@@ -472,13 +497,22 @@ hipError_t launch_t(GemvArgs args, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Input rows per tile: the fewest tiles that still give every SIMD a few
+// waves.  A large matrix (LM head) takes all rows in one tile and streams
+// its weights once; a small one splits the rows over tiles, so that more
+// waves share the per-row work (the extra weight reads hit L2).
 template <int FMT>
 hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
     const int m = args.m;
-    if (m <= 1) return launch_t<FMT, 1>(args, s);
-    if (m <= 2) return launch_t<FMT, 2>(args, s);
-    if (m <= 4) return launch_t<FMT, 4>(args, s);
-    return launch_t<FMT, 8>(args, s);
+    int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    const int mt_min = args.nu <= 16 ? 1 : 2;  // one-row tiles quantise at most 16 groups
+    while (mt > mt_min && (int64_t)args.groups * ((m + mt - 1) / mt) < 2048) mt /= 2;
+    switch (mt) {
+    case 1: return launch_t<FMT, 1>(args, s);
+    case 2: return launch_t<FMT, 2>(args, s);
+    case 4: return launch_t<FMT, 4>(args, s);
+    default: return launch_t<FMT, 8>(args, s);
+    }
 }
 
 }  // namespace

@@ -333,7 +333,7 @@ __device__ __forceinline__ void q8k_vpl_load(const float* src, float (&v)[VPL]) 
 
 template <int VPL>
 __device__ __forceinline__ void quant_q8k_vpl(const float (&v)[VPL], bool live, int64_t row, int g,
-                                              const ActView& a) {
+                                              const ActView& a, int32_t* corr = nullptr) {
     constexpr int LPB = 256 / VPL, LPC = 32 / VPL > 0 ? 32 / VPL : 1;
     static_assert(VPL == 8 || VPL == 16 || VPL == 32, "VPL");
     const int pl = (threadIdx.x & 63) % LPB;
@@ -382,8 +382,12 @@ __device__ __forceinline__ void quant_q8k_vpl(const float (&v)[VPL], bool live, 
     const int c = (VPL * pl) / 32, kk0 = ((VPL * pl) % 32) / 4;
     uint32_t* qrow = (uint32_t*)(a.q + row * a.ldq + (int64_t)g * 256);
 #pragma unroll
-    for (int t = 0; t < VPL / 4; t++)
-        qrow[perm_dword(c, kk0 + t)] = pack4(q[4 * t], q[4 * t + 1], q[4 * t + 2], q[4 * t + 3]);
+    for (int t = 0; t < VPL / 4; t++) {
+        const uint32_t pk = pack4(q[4 * t], q[4 * t + 1], q[4 * t + 2], q[4 * t + 3]);
+        qrow[perm_dword(c, kk0 + t)] = pk;
+        // optional Q6_K offset term, laid out like q: -32 * (sum of the dword's four int8)
+        if (corr) corr[(row * a.ng + g) * 64 + perm_dword(c, kk0 + t)] = sdot4(pk, 0xe0e0e0e0u, 0);
+    }
     if (pl % LPC == 0) a.s8[(row * a.ng + g) * 8 + c] = (int16_t)s;
     if (pl == 0) a.d[row * a.ldd + g] = dval;
 }
