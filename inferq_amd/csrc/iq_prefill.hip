@@ -1,5 +1,5 @@
 // iq_prefill.hip -- y = x . W^T for Q4_K weights at many input rows
-// (prefill), on int8 MFMA (v_mfma_i32_32x32x32_i8).
+// (prefill), on int8 MFMA (v_mfma_i32_16x16x64_i8).
 //
 // Arithmetic.  Per block b of 256 weights, the reference's exact integers
 // are isum = sum_j sc_j * sum_{e in sub-block j} q_e a_e and msum =
@@ -7,8 +7,8 @@
 // a_e the Q8K int8 activations).  A six-bit scale times a four-bit quant
 // does not fit int8, so the scale is split, sc = 8 sc_hi + sc_lo with both
 // parts in 0..7: the MFMA streams w1 = sc_hi q and w2 = sc_lo q (bytes
-// <= 105) give isum = 8 acc1 + acc2 exactly (one 32-wide K step is one
-// sub-block, so each step has a single scale per column).  msum comes from
+// <= 105) give isum = 8 acc1 + acc2 exactly (each weight byte carries its
+// sub-block's scale, so a K step may span sub-blocks).  msum comes from
 // one f16 MFMA per block over the 16 bsums of 16 values (|bsum16| <= 2048 and
 // the mins are exact in f16; products and sums stay below 2^24 in the f32
 // accumulator).  Every per-block integer is therefore the reference's, bit
@@ -17,14 +17,15 @@
 // agree within the path's 1e-4 normwise tolerance, not bitwise (this kernel
 // serves 64+ input rows; fewer rows keep the bit-exact kernels).
 //
-// Tiling.  A workgroup (4 waves) owns 64 input rows and 128 output columns;
-// wave w owns all 64 rows and columns 32w..32w+31 (two 32 x 32 tiles).
-// Per block the workgroup stages the int8 activation tile (16 KiB), the 128
-// raw Q4_K blocks (18 KiB), the bsums and the block scales in LDS, double
-// buffered, the next block's loads in flight while the current one is
-// multiplied.  Each wave dequantises its B fragments in registers (nibbles,
-// then one packed 16-bit multiply per dword and stream).  Narrow outputs are
-// split over K, with partial tiles summed in a fixed order by a second pass.
+// Tiling.  A workgroup (8 waves, two per SIMD) owns 64 input rows and 128
+// output columns; each wave all 64 rows of 16 columns as four 16 x 16 tiles
+// of the double-rate v_mfma_i32_16x16x64_i8.  Per block the workgroup
+// stages the int8 activation tile (16 KiB), the 128 raw Q4_K blocks
+// (18 KiB), the bsums and the block scales in LDS, double buffered, the next
+// block's loads in flight while the current one is multiplied.  Each wave
+// dequantises its B fragments in registers (nibbles, then one packed 16-bit
+// multiply per dword and stream).  Narrow outputs are split over K, with
+// partial tiles summed in a fixed order by a second pass.
 #include "iq_lanes.h"
 #include "iq_quant.h"
 
@@ -82,26 +83,34 @@ struct PrefillArgs {
     int32_t* dbg_msum;
 };
 
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+constexpr int kPfThreads = 512;  // 8 waves of 16 columns each
 
 // LDS stage: A int8 [64][kAS], B raw Q4_K [128][144], H f16 bsums [64][16],
 // D block scales [64].
 constexpr int kAS = 272;  // padded activation row stride
 constexpr int kStA = 0, kStB = kStA + kPfRows * kAS, kStH = kStB + kPfCols * 144, kStD = kStH + kPfRows * 32;
 constexpr int kStage = kStD + kPfRows * 4;
-// staging chunks of 16 bytes: A 1024, B 1152, H 128, D 16 (2320 over 256 threads: 10 each, the last partly idle)
+// staging chunks of 16 bytes: A 1024, B 1152, H 128, D 16 (2320 over 512 threads: 5 each, the last partly idle)
 constexpr int kChA = kPfRows * 16, kChB = kPfCols * 9, kChH = kPfRows * 2, kChD = kPfRows / 4;
 constexpr int kChunks = kChA + kChB + kChH + kChD;
-constexpr int kChPer = (kChunks + 255) / 256;
+constexpr int kChPer = (kChunks + kPfThreads - 1) / kPfThreads;
 
+// Wave w owns all 64 rows and columns 16w .. 16w+15 of the tile as four
+// 16 x 16 tiles of v_mfma_i32_16x16x64_i8 (one decoded B fragment serves
+// four row tiles).  For lane l (g = l / 16,
+// j = l % 16) a fragment holds K 16g..16g+15 of row / column j, and the
+// result rows 4g..4g+3 of column j.  One K step is 64 values: sub-blocks
+// 2s and 2s+1 of the block, whose weights are the low and the high nibbles
+// of qs bytes 32s..32s+31.
 template <bool DBG>
-__global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
+__global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
     __shared__ __align__(16) uint8_t st[2][kStage];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int h = lane >> 5, li = lane & 31;
+    const int g = lane >> 4, jj = lane & 15;
     // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs, so
     // ids L, L + 8, L + 16, ... (same XCD) take the m-tiles of one column
     // tile and share its weights in that XCD's L2.
@@ -115,7 +124,7 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
     const int b1 = min(p.nb, b0 + p.bps);
     const int64_t K = (int64_t)p.nb * 256;
 
-    // staging: chunk t = threadIdx.x + 256 i; its global source (block b) and
+    // staging: chunk t = threadIdx.x + 512 i; its global source (block b) and
     // LDS offset (-1: none).  Every thread issues kChPer loads per block
     // (idle ones re-read a valid chunk) so that waits stay exact.
     int loff[kChPer];
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
     };
 #pragma unroll
     for (int i = 0; i < kChPer; i++) {
-        int t = threadIdx.x + 256 * i;
+        int t = threadIdx.x + kPfThreads * i;
         if (t >= kChunks) {
             loff[i] = -1;
             continue;
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
         b = min(b, b1 - 1);
 #pragma unroll
         for (int i = 0; i < kChPer; i++) {
-            const int t = min((int)threadIdx.x + 256 * i, kChunks - 1);
+            const int t = min((int)threadIdx.x + kPfThreads * i, kChunks - 1);
             stg[i] = *src(t, b);
         }
     };
@@ -166,34 +175,31 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
             if (loff[i] >= 0) *(u32x4a16*)(s + loff[i]) = stg[i];
     };
 
-    float out[2][16];
+    float out[4][4];  // [row tile][r]
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int rt = 0; rt < 4; rt++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) out[mt][r] = 0.f;
+        for (int r = 0; r < 4; r++) out[rt][r] = 0.f;
 
     issue(b0);
     park(st[0]);
     lds_barrier();
 
-    const int col = 32 * wave + li;  // this lane's column within the tile (B and D layouts)
     for (int b = b0; b < b1; b++) {
         const uint8_t* S = st[(b - b0) & 1];
         issue(b + 1);
-        const uint8_t* bcol = S + kStB + col * 144;
+        const uint8_t* bcol = S + kStB + (16 * wave + jj) * 144;
         const u32x4a16 hdr = *(const u32x4a16*)bcol;
         const float dw = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
         const Q4Scales sc = q4_scales(hdr.y, hdr.z, hdr.w);
-
-        v16i acc1[2], acc2[2];
+        v4i acc1[4], acc2[4];
 #pragma unroll
-        for (int c = 0; c < 8; c++) {  // K step c = sub-block c
-            // B: weights 16h..16h+15 of sub-block c = low (c even) or high
-            // nibbles of qs bytes 32 (c / 2) + 16 h ..
-            const u32x4a16 raw = *(const u32x4a16*)(bcol + 16 + 32 * (c >> 1) + 16 * h);
-            const int shn = (c & 1) * 4;
-            const uint32_t s6 = byte_of(c < 4 ? sc.sc_lo : sc.sc_hi, c & 3);
+        for (int st4 = 0; st4 < 4; st4++) {  // K step: values 64 st4 .. +63
+            const int shn = (g >> 1) * 4;
+            // sub-block 2 st4 + (g >> 1): byte (2 st4 + (g >> 1)) & 3 of the low or high scale word
+            const uint32_t s6 = byte_of(st4 < 2 ? sc.sc_lo : sc.sc_hi, (2 * st4 + (g >> 1)) & 3);
             const uint32_t hi = s6 >> 3, lo = s6 & 7u;
+            const u32x4a16 raw = *(const u32x4a16*)(bcol + 16 + 32 * st4 + 16 * (g & 1));
             const uint32_t qv[4] = {(raw.x >> shn) & 0x0f0f0f0fu, (raw.y >> shn) & 0x0f0f0f0fu,
                                     (raw.z >> shn) & 0x0f0f0f0fu, (raw.w >> shn) & 0x0f0f0f0fu};
             const v4i w1 = {(int)bytes_mul_small(qv[0], hi), (int)bytes_mul_small(qv[1], hi),
@@ -201,47 +207,35 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
             const v4i w2 = {(int)bytes_mul_small(qv[0], lo), (int)bytes_mul_small(qv[1], lo),
                             (int)bytes_mul_small(qv[2], lo), (int)bytes_mul_small(qv[3], lo)};
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                // A: row 32 mt + li, activations 16h..16h+15 of sub-block c
-                const v4i a = *(const v4i*)(S + kStA + (32 * mt + li) * kAS + 32 * c + 16 * h);
-                const v16i z = {};
-                acc1[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w1, c == 0 ? z : acc1[mt], 0, 0, 0);
-                acc2[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w2, c == 0 ? z : acc2[mt], 0, 0, 0);
+            for (int rt = 0; rt < 4; rt++) {
+                const v4i a = *(const v4i*)(S + kStA + (16 * rt + jj) * kAS + 64 * st4 + 16 * g);
+                const v4i z = {};
+                acc1[rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w1, st4 == 0 ? z : acc1[rt], 0, 0, 0);
+                acc2[rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w2, st4 == 0 ? z : acc2[rt], 0, 0, 0);
             }
         }
 
-        // mins: msum = sum_t m_{t/2} bsum16_t, K = 16 (lane half h: t = 8h..8h+7)
-        v8h bm;
-        {
-            const uint32_t mw = h == 0 ? sc.mn_lo : sc.mn_hi;  // m_{4h} .. m_{4h+3}
+        // mins: msum = sum_t m_{t/2} bsum16_t (K = 16; lane group g: t = 4g..4g+3)
+        const uint32_t mw = g < 2 ? sc.mn_lo : sc.mn_hi;  // m_{2g}, m_{2g+1}: bytes 2 (g & 1) + 0, 1
+        const _Float16 mA = (_Float16)(float)byte_of(mw, 2 * (g & 1));
+        const _Float16 mB = (_Float16)(float)byte_of(mw, 2 * (g & 1) + 1);
+        const v4h bm = {mA, mA, mB, mB};
 #pragma unroll
-            for (int d = 0; d < 4; d++) {
-                const _Float16 mv = (_Float16)(float)byte_of(mw, d);
-                bm[2 * d] = mv;
-                bm[2 * d + 1] = mv;
-            }
-        }
+        for (int rt = 0; rt < 4; rt++) {
+            const v4h am = *(const v4h*)(S + kStH + (16 * rt + jj) * 32 + 8 * g);
+            const f32x4 dx = *(const f32x4*)(S + kStD + 4 * (16 * rt + 4 * g));
+            const v4f z = {};
+            const v4f msum = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
-            const v8h am = *(const v8h*)(S + kStH + (32 * mt + li) * 32 + 16 * h);
-            const v16f z = {};
-            const v16f msum = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, z, 0, 0, 0);
-            // D layout: lane (h, li) holds column li, rows 8 (r / 4) + 4 h + r % 4
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const f32x4 dx = *(const f32x4*)(S + kStD + 4 * (32 * mt + 8 * g + 4 * h));
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int r = 4 * g + e;
-                    const int32_t isum = 8 * acc1[mt][r] + acc2[mt][r];
-                    const float t = __builtin_fmaf(-dmin, msum[r], dw * (float)isum);
-                    out[mt][r] = __builtin_fmaf(dx[e], t, out[mt][r]);
-                    if constexpr (DBG) {
-                        const int64_t row = row0 + 32 * mt + 8 * g + 4 * h + e, gc = n0 + col;
-                        if (row < p.m && gc < p.n) {
-                            p.dbg_isum[(row * p.n + gc) * p.nb + b] = isum;
-                            p.dbg_msum[(row * p.n + gc) * p.nb + b] = (int32_t)msum[r];
-                        }
+            for (int r = 0; r < 4; r++) {
+                const int32_t isum = 8 * acc1[rt][r] + acc2[rt][r];
+                const float t = __builtin_fmaf(-dmin, msum[r], dw * (float)isum);
+                out[rt][r] = __builtin_fmaf(dx[r], t, out[rt][r]);
+                if constexpr (DBG) {
+                    const int64_t row = row0 + 16 * rt + 4 * g + r, gc = n0 + 16 * wave + jj;
+                    if (row < p.m && gc < p.n) {
+                        p.dbg_isum[(row * p.n + gc) * p.nb + b] = isum;
+                        p.dbg_msum[(row * p.n + gc) * p.nb + b] = (int32_t)msum[r];
                     }
                 }
             }
@@ -254,13 +248,13 @@ __global__ __launch_bounds__(256) void k_prefill_q4k(PrefillArgs p) {
 
     float* dst = p.splits == 1 ? p.y : p.part + (int64_t)blockIdx.z * p.m * p.n;
     const int64_t ld = p.splits == 1 ? p.ldy : p.n;
-    const int64_t gc = (int64_t)n0 + col;
+    const int64_t gc = (int64_t)n0 + 16 * wave + jj;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int rt = 0; rt < 4; rt++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int64_t row = row0 + 32 * mt + 8 * (r / 4) + 4 * h + (r % 4);
-            if (row < p.m && gc < p.n) dst[row * ld + gc] = out[mt][r];
+        for (int r = 0; r < 4; r++) {
+            const int64_t row = row0 + 16 * rt + 4 * g + r;
+            if (row < p.m && gc < p.n) dst[row * ld + gc] = out[rt][r];
         }
 }
 
@@ -336,8 +330,8 @@ hipError_t launch_prefill(const WeightView& w, const float* x, int64_t ldx, int6
     if (e != hipSuccess) return e;
     const int64_t ntiles = (w.rows + kPfCols - 1) / kPfCols;
     dim3 grid((unsigned)((ntiles + 7) / 8 * 8 * (P.mp / kPfRows)), 1, (unsigned)P.splits);
-    if (dbg_isum) hipLaunchKernelGGL(k_prefill_q4k<true>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(k_prefill_q4k<false>, grid, dim3(256), 0, s, a);
+    if (dbg_isum) hipLaunchKernelGGL(k_prefill_q4k<true>, grid, dim3(kPfThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_prefill_q4k<false>, grid, dim3(kPfThreads), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess || P.splits == 1) return e;
     const int64_t tot = m * w.rows;
