@@ -348,6 +348,57 @@ def prefill(args, hip, stream, device):
     return res
 
 
+def decode_sweep(args, hip, device, layers):
+    """the quantized matmuls of one decode step over the
+    resident layers -- per layer the attention projections q/gate
+    [8192 x 2048], k and v [512 x 2048], o [2048 x 4096] (Q4_K) and the MoE
+    layer -- then the LM head [248320 x 2048] Q6_K, at M = 1 and M = 8 rows.
+    Every call of a step is launched in order on one stream (graph replay);
+    reported: matmul time per step, tokens per second of matmul time, and
+    the step's algorithmic HBM bytes over that time."""
+    import torch
+
+    from inferq_amd import qgemm, synth
+
+    n = len(layers)
+    shapes = ((8192, 2048), (512, 2048), (512, 2048), (2048, 4096))
+    dense = [[qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, r, c, device, 5000 + 10 * li + j),
+                                         synth.Q4_K, r, c) for j, (r, c) in enumerate(shapes)] for li in range(n)]
+    lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 6000), synth.Q6_K,
+                                    248320, 2048)
+    dense_bytes = n * sum(m_.storage_bytes() for m_ in dense[0])
+    gu, dn = expert_bytes()
+    g = torch.Generator(device=device)
+    g.manual_seed(args.seed + 9)
+    res = {"layers": n}
+    for m in (1, 8):
+        x2 = torch.randn(m, 2048, device=device, generator=g)
+        x4 = torch.randn(m, 4096, device=device, generator=g)
+        lg = torch.randn(n, m, E, device=device, generator=g)
+        ys = [torch.empty(m, r, device=device) for r, _ in shapes]
+        out = torch.empty(m, H, device=device)
+        ylm = torch.empty(m, 248320, device=device)
+
+        def step(i):
+            for li in range(n):
+                mats = dense[li]
+                mats[0].forward_into(x2, ys[0])
+                mats[1].forward_into(x2, ys[1])
+                mats[2].forward_into(x2, ys[2])
+                mats[3].forward_into(x4, ys[3])
+                layers[li][0].forward_into(x2, lg[li], out)
+            lm.forward_into(x2, ylm)
+
+        ms = time_graph(step, 2, hip, warmup=1)
+        uniq = float(np.mean([len(torch.unique(torch.topk(lg[li], TOPK, dim=1).indices)) for li in range(n)]))
+        total = n * (uniq + 1) * (gu + dn) + dense_bytes + lm.storage_bytes()
+        res[f"m{m}"] = {"us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(m / (ms * 1e-3), 1),
+                        "unique_experts_per_layer": round(uniq, 1), "GB_per_step": round(total / 1e9, 3),
+                        "GB_s": round(total / ms / 1e6, 1), "frac_hbm": round(total / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    del dense, lm
+    return res
+
+
 def prefill_moe(args, hip, stream, device, layers):
     """BASELINE configs[3], MoE part: 256 tokens, top-8 of 256 experts with
     Dirichlet(0.3) router skew, plus the shared expert.  TOPS counts the
@@ -504,6 +555,7 @@ def main():
         result["extra"] = secondary(args, hip, stream, device, layers)
         result["extra"]["prefill_int8_tops"] = prefill(args, hip, stream, device)
         result["extra"]["prefill_moe_m256_dirichlet"] = prefill_moe(args, hip, stream, device, layers)
+        result["extra"]["decode_step_sweep"] = decode_sweep(args, hip, device, layers)
         log(f"secondary: {result['extra']}")
 
     print(json.dumps(result), flush=True)
