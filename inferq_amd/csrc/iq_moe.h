@@ -55,11 +55,6 @@ struct MoeParams {
 // events (may be null): 4 hipEvent_t recorded before and between the launches.
 hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
                       hipEvent_t const* events = nullptr);
-// The 2..16-token path (iq_moe_verify.hip); moev_supported tells whether it
-// covers a call.
-bool moev_supported(const MoeParams& p, int gate_dtype, int down_dtype);
-hipError_t launch_moe_verify(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
-                             hipEvent_t const* events);
 // The many-token path on int8 MFMA (iq_moe_prefill.hip).
 bool moep_supported(const MoeParams& p, int gate_dtype, int down_dtype);
 hipError_t launch_moe_prefill(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
@@ -69,5 +64,4 @@ int moep_max_chunks(int64_t M, int64_t K, int64_t E);
 // One launch of a call already made with these parameters (stage 0 routing
 // of the grouped path, 1 gate/up, 2 down).
 hipError_t launch_moe_stage(const MoeParams& p, int gate_dtype, int down_dtype, int stage, hipStream_t s);
-
 }  // namespace iq

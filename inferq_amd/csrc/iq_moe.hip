@@ -265,42 +265,49 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeParams p) {
     }
 }
 
-// ------------------------------------------------ M = 1 (decode) kernels
-// One token: no grouping is needed, so the routing is recomputed where it
-// is used and each launch has a single dependent memory round trip before
-// its weight loads (logits -> weights).
+// ------------------------------------- token-major kernels (decode, verify)
+// Each token runs on its own slice of the grid (routed_token_major,
+// src/qwen/quantized_moe.rs:283-318): no grouping is needed, so the routing
+// is recomputed where it is used and each launch has a single dependent
+// memory round trip before its weight loads (logits -> weights).  A token's
+// output is bitwise the one-token call's, which is the grouped execution's
+// too (the reference asserts grouped == token-major).  An expert picked by
+// several tokens is read once per token, mostly from L2: up to a few dozen
+// tokens this beats grouping, whose per-expert launches wait on the grouping
+// pass and have far less weight traffic in flight per CU.
 
 constexpr int kMoe1MaxSlots = 12;  // top-k routes plus the shared expert
+constexpr int kMoeTokenMajorMax = 48;  // widest call served token-major
 
-// Routing workgroup of the M = 1 gate/up launch: wave 0 routes the token
+// Routing workgroup of token t's gate/up slice: wave 0 routes the token
 // (top-k, exact softmax weights), wave 1 computes the shared-expert gate.
 // Both run beside the matmul workgroups, off their critical path.
-__device__ void moe1_route(const MoeParams& p, int wave) {
+__device__ void moe1_route(const MoeParams& p, int wave, int t) {
     const int K = (int)p.K, E = (int)p.E, lane = threadIdx.x & 63;
     __shared__ __align__(16) float s_scratch[kMoeMaxExperts];
     if (wave == 0) {
         float lv[kRoutePer], wt[kMoe1MaxSlots];
         int sel[kMoe1MaxSlots];
-        route_load(p.logits, E, lv);
+        route_load(p.logits + (int64_t)t * E, E, lv);
         route_topk_any<kMoe1MaxSlots>(lv, E, K, sel);
         if (lane == 0)  // the down launch needs the ids first
-            for (int s = 0; s < K; s++) p.experts[s] = sel[s];
+            for (int s = 0; s < K; s++) p.experts[t * K + s] = sel[s];
         route_weights<kMoe1MaxSlots>(lv, E, K, sel, p.normalize, s_scratch, wt);
         if (lane == 0)
-            for (int s = 0; s < K; s++) p.weights[s] = wt[s];
+            for (int s = 0; s < K; s++) p.weights[t * K + s] = wt[s];
     } else if (wave == 1 && p.sdown_w) {
-        const float gate = selector_gate(p.x, p.selector, p.H);
-        if (lane == 0) p.sgate[0] = gate;
+        const float gate = selector_gate(p.x + (int64_t)t * p.H, p.selector, p.H);
+        if (lane == 0) p.sgate[t] = gate;
     }
 }
 
-// Grid (I/8, slots + 1).  Workgroup (x, s + 1): 8 intermediate rows of
-// gate and up of the expert at route rank s (or the shared expert), 4 waves
+// Grid (I/8, slots + 1, M).  Workgroup (x, s + 1, t): 8 intermediate rows of
+// gate and up of token t's expert at route rank s (or the shared expert), 4 waves
 // each taking a quarter of the NG blocks along hidden.  Each wave forms its
 // blocks' exact lane integers and f32 scales; wave 0 then advances the
 // accumulators through all NG blocks in order (the reference's chain),
-// reduces them with the hsum trees, applies SwiGLU and stores act[s][i].
-// Row 0 holds the routing workgroup (x == 0).
+// reduces them with the hsum trees, applies SwiGLU and stores act[t][s][i].
+// Row 0 of each token holds its routing workgroup (x == 0).
 template <int GFMT, int NG>
 __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
@@ -313,10 +320,11 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     __shared__ float s_dd[2][8][NG], s_dm[2][8][NG];
     const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K = (int)p.K;
+    const int K = (int)p.K, t = blockIdx.z;
+    const int nslots = K + (p.sdown_w ? 1 : 0);
     // row 0 holds the routing workgroup, dispatched ahead of the slots
     if (blockIdx.y == 0) {
-        if (blockIdx.x == 0) moe1_route(p, wave);
+        if (blockIdx.x == 0) moe1_route(p, wave, t);
         return;
     }
     const int sidx = blockIdx.y - 1;
@@ -325,8 +333,8 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     const int g0 = wave * NB;
     const int gx = g0 + lane / LPB;  // x block this lane quantises
     float lv[kRoutePer], xv[VPL];
-    route_load(p.logits, (int)p.E, lv);
-    q8k_vpl_load<VPL>(p.x + (int64_t)gx * 256, xv);
+    route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
+    q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
     int e = (int)p.E;
     if (sidx < K) {
         int sel[kMoe1MaxSlots];
@@ -401,10 +409,11 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
         o[r] = v;
     }
     // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
-    if (k == 0 && ok) p.act[(int64_t)sidx * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
+    if (k == 0 && ok) p.act[((int64_t)t * nslots + sidx) * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
 }
 
-// Grid H/8; one wave per route slot (blockDim 64 * slots), all on the same
+// Grid (H/8, M); one wave per route slot of token t = blockIdx.y (blockDim
+// 64 * slots), all on the same
 // 8 hidden rows.  Each wave loads its slot's expert id and SwiGLU row, issues
 // its down-row burst, quantises the SwiGLU row into LDS while the weights
 // fly, and forms the row products; the 8 rows are then combined in route
@@ -419,14 +428,14 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
     __shared__ float s_vals[kMoe1MaxSlots][8];
     const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = route slot
-    const int K = (int)p.K;
+    const int K = (int)p.K, t = blockIdx.y;
     const bool has_shared = p.sdown_w != nullptr;
     const int nslots = K + (has_shared ? 1 : 0);
     constexpr int LPB = 256 / VPL;
     const int gq = lane / LPB;
     float av[VPL];
-    q8k_vpl_load<VPL>(p.act + (int64_t)wave * p.I + (int64_t)gq * 256, av);
-    const int e = wave < K ? __builtin_amdgcn_readfirstlane(p.experts[wave]) : 0;
+    q8k_vpl_load<VPL>(p.act + ((int64_t)t * nslots + wave) * p.I + (int64_t)gq * 256, av);
+    const int e = wave < K ? __builtin_amdgcn_readfirstlane(p.experts[t * K + wave]) : 0;
     const int64_t n = (int64_t)blockIdx.x * 8 + slot;
     const bool ok = n < p.H;
     const int64_t nc = ok ? n : p.H - 1;
@@ -458,19 +467,19 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
         const int64_t nn = (int64_t)blockIdx.x * 8 + threadIdx.x;
         if (nn < p.H) {
             float v = 0.f;
-            for (int j = 0; j < K; j++) v = v + s_vals[j][threadIdx.x] * p.weights[j];
-            if (has_shared) v = v + s_vals[K][threadIdx.x] * p.sgate[0];
-            p.out[nn] = v;
+            for (int j = 0; j < K; j++) v = v + s_vals[j][threadIdx.x] * p.weights[t * K + j];
+            if (has_shared) v = v + s_vals[K][threadIdx.x] * p.sgate[t];
+            p.out[(int64_t)t * p.H + nn] = v;
         }
     }
 }
 
-// The M = 1 kernels cover K-quant experts with hidden 2048 and
-// intermediate 512 (Qwen3.6-35B-A3B and Qwen3-Next); other shapes take the
-// grouped path.
+// The token-major kernels cover K-quant experts with hidden 2048 and
+// intermediate 512 (Qwen3.6-35B-A3B and Qwen3-Next) up to
+// kMoeTokenMajorMax tokens; other calls take the grouped paths.
 bool moe1_supported(const MoeParams& p, int gfmt, int dfmt) {
     const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
-    return p.M == 1 && gfmt != kQ8_0 && dfmt != kQ8_0 && p.H == 2048 && p.I == 512 && nslots <= kMoe1MaxSlots &&
+    return p.M >= 1 && p.M <= kMoeTokenMajorMax && gfmt != kQ8_0 && dfmt != kQ8_0 && p.H == 2048 && p.I == 512 && nslots <= kMoe1MaxSlots &&
            p.E <= kMoeMaxExperts;
 }
 
@@ -478,10 +487,10 @@ template <int GFMT, int DFMT>
 hipError_t launch_moe1(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
     const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
     if (ev) (void)hipEventRecord(ev[1], s);
-    hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1, (unsigned)p.M), dim3(256), 0, s, p);
     if (hipError_t e = hipGetLastError()) return e;
     if (ev) (void)hipEventRecord(ev[2], s);
-    hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8)), dim3(64 * nslots), 0, s, p);
+    hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), (unsigned)p.M), dim3(64 * nslots), 0, s, p);
     if (hipError_t e = hipGetLastError()) return e;
     if (ev) (void)hipEventRecord(ev[3], s);
     return hipSuccess;
@@ -542,7 +551,6 @@ hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hip
         default: return hipErrorInvalidValue;
         }
     }
-    if (moev_supported(p, gfmt, dfmt)) return launch_moe_verify(p, gfmt, dfmt, s, ev);
     if (moep_supported(p, gfmt, dfmt)) return launch_moe_prefill(p, gfmt, dfmt, s, ev);
     const int64_t qwaves = (int64_t)p.M * p.xq.ng;
     const unsigned prep_blocks = 1 + (unsigned)((qwaves + 3) / 4);
@@ -568,9 +576,9 @@ template <int GFMT, int DFMT>
 hipError_t stage_moe1(const MoeParams& p, int stage, hipStream_t s) {
     const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
     if (stage == 1)
-        hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1), dim3(256), 0, s, p);
+        hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1, (unsigned)p.M), dim3(256), 0, s, p);
     else if (stage == 2)
-        hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8)), dim3(64 * nslots), 0, s, p);
+        hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), (unsigned)p.M), dim3(64 * nslots), 0, s, p);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -88,12 +88,16 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int kPfThreads = 512;  // 8 waves of 16 columns each
 
-// LDS stage: A int8 [64][kAS], B raw Q4_K [128][144], H f16 bsums [64][16],
-// D block scales [64].
-constexpr int kAS = 272;  // padded activation row stride
-constexpr int kStA = 0, kStB = kStA + kPfRows * kAS, kStH = kStB + kPfCols * 144, kStD = kStH + kPfRows * 32;
+// LDS stage: A int8 [64][kAS], B raw Q4_K [128][kBS], H f16 bsums [64][16],
+// D block scales [64], then a 16-byte sink for idle staging lanes.  Row
+// strides of 32 mod 64 bytes let the fragment reads (16 rows, four 16-byte
+// columns per row) run without bank conflicts on gfx950; strides of 16 mod
+// 64 bytes measure 1.5x slower.
+constexpr int kAS = 288;  // activation row stride (256 bytes + pad)
+constexpr int kBS = 160;  // Q4_K block stride (144 bytes + pad)
+constexpr int kStA = 0, kStB = kStA + kPfRows * kAS, kStH = kStB + kPfCols * kBS, kStD = kStH + kPfRows * 32;
 constexpr int kStage = kStD + kPfRows * 4;
-// staging chunks of 16 bytes: A 1024, B 1152, H 128, D 16 (2320 over 512 threads: 5 each, the last partly idle)
+// staging chunks of 16 bytes per block: A 1024, B 1152, H 128, D 16
 constexpr int kChA = kPfRows * 16, kChB = kPfCols * 9, kChH = kPfRows * 2, kChD = kPfRows / 4;
 constexpr int kChunks = kChA + kChB + kChH + kChD;
 constexpr int kChPer = (kChunks + kPfThreads - 1) / kPfThreads;
@@ -107,7 +111,7 @@ constexpr int kChPer = (kChunks + kPfThreads - 1) / kPfThreads;
 // of qs bytes 32s..32s+31.
 template <bool DBG>
 __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
-    __shared__ __align__(16) uint8_t st[2][kStage];
+    __shared__ __align__(16) uint8_t st[2][kStage + 16];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, jj = lane & 15;
@@ -124,55 +128,49 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
     const int b1 = min(p.nb, b0 + p.bps);
     const int64_t K = (int64_t)p.nb * 256;
 
-    // staging: chunk t = threadIdx.x + 512 i; its global source (block b) and
-    // LDS offset (-1: none).  Every thread issues kChPer loads per block
-    // (idle ones re-read a valid chunk) so that waits stay exact.
+    // staging: chunk t = threadIdx.x + 512 i of a block.  Per chunk a thread
+    // keeps its source in block 0, the stride per block and its LDS offset
+    // (chunks past the block: the sink).  Every thread issues and parks
+    // kChPer chunks per block without branches, so that the waits before the
+    // LDS stores stay exact (a store under a branch leaves the compiler's
+    // count of loads in flight unknown there, and it then waits for more).
+    const uint8_t* gsrc[kChPer];
+    uint32_t gstr[kChPer];
     int loff[kChPer];
-    auto src = [&](int t, int b) -> const u32x4a16* {
-        if (t < kChA) {
-            const int r = t >> 4, c = t & 15;
-            return (const u32x4a16*)(p.q + (int64_t)(row0 + r) * K + (int64_t)b * 256 + 16 * c);
-        }
-        t -= kChA;
-        if (t < kChB) {
-            const int col = t / 9, pc = t - 9 * col;
-            const int64_t gc = min((int64_t)n0 + col, p.n - 1);
-            return (const u32x4a16*)(p.w + gc * p.row_bytes + (int64_t)b * 144 + 16 * pc);
-        }
-        t -= kChB;
-        if (t < kChH) {
-            const int r = t >> 1, c = t & 1;
-            return (const u32x4a16*)(p.hs + ((int64_t)(row0 + r) * p.nb + b) * 16 + 8 * c);
-        }
-        t -= kChH;
-        t = min(t, kChD - 1);
-        return (const u32x4a16*)(p.dT + (int64_t)b * p.mp + row0 + 4 * t);
-    };
 #pragma unroll
     for (int i = 0; i < kChPer; i++) {
-        int t = threadIdx.x + kPfThreads * i;
-        if (t >= kChunks) {
-            loff[i] = -1;
-            continue;
+        int t = min((int)threadIdx.x + kPfThreads * i, kChunks - 1);
+        if (t < kChA) {
+            gsrc[i] = (const uint8_t*)p.q + (int64_t)(row0 + (t >> 4)) * K + 16 * (t & 15);
+            gstr[i] = 256;
+            loff[i] = kStA + (t >> 4) * kAS + 16 * (t & 15);
+        } else if ((t -= kChA) < kChB) {
+            const int col = t / 9, pc = t - 9 * col;
+            const int64_t gc = min((int64_t)n0 + col, p.n - 1);
+            gsrc[i] = p.w + gc * p.row_bytes + 16 * pc;
+            gstr[i] = 144;
+            loff[i] = kStB + col * kBS + 16 * pc;
+        } else if ((t -= kChB) < kChH) {
+            gsrc[i] = (const uint8_t*)(p.hs + (int64_t)(row0 + (t >> 1)) * p.nb * 16 + 8 * (t & 1));
+            gstr[i] = 32;
+            loff[i] = kStH + 16 * t;
+        } else {
+            t -= kChH;
+            gsrc[i] = (const uint8_t*)(p.dT + row0 + 4 * t);
+            gstr[i] = (uint32_t)p.mp * 4;
+            loff[i] = kStD + 16 * t;
         }
-        if (t < kChA) loff[i] = kStA + (t >> 4) * kAS + 16 * (t & 15);
-        else if ((t -= kChA) < kChB) loff[i] = kStB + 16 * t;
-        else if ((t -= kChB) < kChH) loff[i] = kStH + 16 * t;
-        else loff[i] = kStD + 16 * (t - kChH);
+        if ((int)threadIdx.x + kPfThreads * i >= kChunks) loff[i] = kStage;  // sink
     }
     u32x4a16 stg[kChPer];
     auto issue = [&](int b) {
         b = min(b, b1 - 1);
 #pragma unroll
-        for (int i = 0; i < kChPer; i++) {
-            const int t = min((int)threadIdx.x + kPfThreads * i, kChunks - 1);
-            stg[i] = *src(t, b);
-        }
+        for (int i = 0; i < kChPer; i++) stg[i] = *(const u32x4a16*)(gsrc[i] + (int64_t)b * gstr[i]);
     };
     auto park = [&](uint8_t* s) {
 #pragma unroll
-        for (int i = 0; i < kChPer; i++)
-            if (loff[i] >= 0) *(u32x4a16*)(s + loff[i]) = stg[i];
+        for (int i = 0; i < kChPer; i++) *(u32x4a16*)(s + loff[i]) = stg[i];
     };
 
     float out[4][4];  // [row tile][r]
@@ -188,7 +186,10 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
     for (int b = b0; b < b1; b++) {
         const uint8_t* S = st[(b - b0) & 1];
         issue(b + 1);
-        const uint8_t* bcol = S + kStB + (16 * wave + jj) * 144;
+        // the next block's loads go out before this block's work (left to
+        // itself the scheduler sinks them next to the stores that wait on them)
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* bcol = S + kStB + (16 * wave + jj) * kBS;
         const u32x4a16 hdr = *(const u32x4a16*)bcol;
         const float dw = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
         const Q4Scales sc = q4_scales(hdr.y, hdr.z, hdr.w);

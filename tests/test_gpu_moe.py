@@ -82,6 +82,45 @@ def test_qwen_shaped_moe_matches_oracle(gpu, oracle, qwen_layer, m):
     assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, f"Qwen-shaped MoE m={m}")
 
 
+_NAMES = {Q4: "q4k", Q6: "q6k", Q8: "q80"}
+_FORMAT_PAIRS = [(Q4, Q6), (Q4, Q4), (Q6, Q6), (Q6, Q4), (Q8, Q8), (Q8, Q6)]
+
+
+@pytest.fixture(scope="module")
+def format_layers():
+    """hidden 2048, inter 512 (the shape of the token-major kernels), 16
+    experts, one shared expert, one layer per gate/down format pair."""
+    out = {}
+    for i, (g, d) in enumerate(_FORMAT_PAIRS):
+        out[(g, d)] = S.random_moe_layer(2048, 512, 16, g, d, np.random.default_rng(500 + i), shared=True)
+    return out
+
+
+@pytest.mark.parametrize("m", [1, 8, 64])
+@pytest.mark.parametrize("fmts", _FORMAT_PAIRS, ids=lambda f: f"{_NAMES[f[0]]}-{_NAMES[f[1]]}")
+def test_format_pairs_match_oracle(gpu, oracle, format_layers, fmts, m):
+    """Every gate/down format pair at one row, a verify width and a prefill
+    width (K-quant pairs take the token-major kernels up to 48 rows and the
+    grouped MFMA kernels past that; Q8_0 the generic grouped path); a
+    multi-row call equals one-row calls, bitwise."""
+    layer = format_layers[fmts]
+    moe, _ = _device_layer(layer, 4, gpu)
+    rng = np.random.default_rng(600 + m)
+    x = S.normal((m, 2048), rng)
+    logits = _dirichlet_logits(m, 16, rng, alpha=1.0)
+    xg, lg = torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu)
+    out = moe.forward(xg, lg)
+    ref, ref_e, ref_w = oracle.moe_forward(_oracle_layer(layer, 4), x, logits, mode=1, impl=_impl(oracle),
+                                           nthreads=8)
+    assert [r.experts for r in out.routes] == ref_e.tolist()
+    assert_close_normwise(np.array([r.weights for r in out.routes]), ref_w, 1e-6, "route weights")
+    got = out.hidden.cpu().numpy()
+    assert_close_normwise(got, ref, 1e-4, f"MoE {fmts} m={m}")
+    if m > 1:
+        singles = np.concatenate([moe.forward(xg[i:i + 1], lg[i:i + 1]).hidden.cpu().numpy() for i in range(m)])
+        assert_bitexact(got, singles, f"grouped vs per-token {fmts} m={m}")
+
+
 def _dirichlet_logits(m, n_experts, rng, alpha=0.3):
     """Router logits N(0,1) plus log p with p ~ Dirichlet(alpha): per-expert
     token counts follow that skew (prefill width)."""
@@ -89,10 +128,11 @@ def _dirichlet_logits(m, n_experts, rng, alpha=0.3):
     return (S.normal((m, n_experts), rng) + np.log(np.maximum(p, 1e-30))).astype(np.float32)
 
 
-@pytest.mark.parametrize("m", [17, 64, 256])
+@pytest.mark.parametrize("m", [17, 48, 49, 256])
 def test_prefill_width_moe_matches_oracle(gpu, oracle, qwen_layer, m):
-    """Past the verify sizes (17 rows up to the prefill width of 256) with
-    skewed routing: large groups on a few experts, most experts idle."""
+    """Wide calls with skewed routing (large groups on a few experts, most
+    experts idle): the widest token-major calls (17, 48 rows), the narrowest
+    grouped MFMA call (49) and the prefill width of 256."""
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     rng = np.random.default_rng(300 + m)
     x = S.normal((m, 2048), rng)
@@ -105,15 +145,17 @@ def test_prefill_width_moe_matches_oracle(gpu, oracle, qwen_layer, m):
     assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, f"prefill-width MoE m={m}")
 
 
-def test_skewed_grouped_call_equals_single_token_calls(gpu, qwen_layer):
-    """32 rows with skewed routing in one call equal 32 one-row calls."""
+@pytest.mark.parametrize("m", [32, 64])
+def test_skewed_grouped_call_equals_single_token_calls(gpu, qwen_layer, m):
+    """m rows with skewed routing in one call (token-major at 32, grouped by
+    expert at 64) equal m one-row calls."""
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     rng = np.random.default_rng(98)
-    x = torch.from_numpy(S.normal((32, 2048), rng)).to(gpu)
-    logits = torch.from_numpy(_dirichlet_logits(32, 256, rng)).to(gpu)
+    x = torch.from_numpy(S.normal((m, 2048), rng)).to(gpu)
+    logits = torch.from_numpy(_dirichlet_logits(m, 256, rng)).to(gpu)
     grouped = moe.forward(x, logits).hidden.cpu().numpy()
-    singles = np.concatenate([moe.forward(x[i:i + 1], logits[i:i + 1]).hidden.cpu().numpy() for i in range(32)])
-    assert_bitexact(grouped, singles, "skewed grouped vs per-token")
+    singles = np.concatenate([moe.forward(x[i:i + 1], logits[i:i + 1]).hidden.cpu().numpy() for i in range(m)])
+    assert_bitexact(grouped, singles, f"skewed {m}-row call vs per-token")
 
 
 def test_grouped_equals_single_token_calls(gpu, qwen_layer):
@@ -165,7 +207,7 @@ def test_moe_load_time_errors(gpu):
                               t["up"][:256 * 144], t["down"][:256 * 210], None)
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 64])
 def test_graph_replays_match_eager_calls(gpu, qwen_layer, m):
     """A layer call captured in a HIP graph and replayed several times, with
     fresh inputs copied into its buffers and eager work between replays,
