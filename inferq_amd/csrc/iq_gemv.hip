@@ -517,8 +517,15 @@ hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
 
 }  // namespace
 
+// Up to 8 rows every matrix takes this kernel.  Past 8 rows it runs one
+// tile of 8 rows per grid row, and each tile redoes the per-row lane work
+// while its weight reads hit L2: that wins (by 2x to 8x) on matrices up to
+// a few MiB, and up to 16 rows on anything short of an LM head; wider calls
+// on large matrices go to the lane kernel (iq_lanes.hip).
 bool gemv_supported(const WeightView& w, int64_t m) {
-    if (m < 1 || m > 8 || w.rows < 1) return false;
+    if (m < 1 || m >= kPrefillMinRows || w.rows < 1) return false;
+    const int64_t bytes = w.rows * w.row_bytes;
+    if (m > 8 && bytes > (m <= 16 ? (int64_t)64 << 20 : (int64_t)8 << 20)) return false;
     const int64_t nu = w.cols / 256;
     if (w.cols % 256 != 0 || w.rows > (int64_t)1 << 31) return false;
     if (m == 1 && nu > 16) return false;  // one quantisation batch per wave at one row

@@ -278,6 +278,7 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeParams p) {
 
 constexpr int kMoe1MaxSlots = 12;  // top-k routes plus the shared expert
 constexpr int kMoeTokenMajorMax = 48;  // widest call served token-major
+constexpr int kMoeRouteLaunchMin = 12;  // calls this wide route in a launch of their own
 
 // Routing workgroup of token t's gate/up slice: wave 0 routes the token
 // (top-k, exact softmax weights), wave 1 computes the shared-expert gate.
@@ -301,14 +302,17 @@ __device__ void moe1_route(const MoeParams& p, int wave, int t) {
     }
 }
 
-// Grid (I/8, slots + 1, M).  Workgroup (x, s + 1, t): 8 intermediate rows of
-// gate and up of token t's expert at route rank s (or the shared expert), 4 waves
-// each taking a quarter of the NG blocks along hidden.  Each wave forms its
-// blocks' exact lane integers and f32 scales; wave 0 then advances the
-// accumulators through all NG blocks in order (the reference's chain),
-// reduces them with the hsum trees, applies SwiGLU and stores act[t][s][i].
-// Row 0 of each token holds its routing workgroup (x == 0).
-template <int GFMT, int NG>
+// Grid (I/8, slots + 1, M).  Workgroup (x, s + 1, t): 8 intermediate rows
+// of gate and up of token t's expert at route rank s (or the shared
+// expert), 4 waves each taking a quarter of the NG blocks along hidden.
+// Each wave forms its blocks' exact lane integers and f32 scales; wave 0
+// then advances the accumulators through all NG blocks in order (the
+// reference's chain), reduces them with the hsum trees, applies SwiGLU and
+// stores act[t][s][i].  PRE = false: row 0 of each token holds its routing
+// workgroup (x == 0) and every workgroup finds its expert by a top-k of its
+// own; PRE = true (grid y = slots): a routing launch ran first and the
+// workgroups read the expert ids, which wide calls amortise better.
+template <int GFMT, int NG, bool PRE>
 __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
     static_assert(NG % NW == 0 && (VPL == 8 || VPL == 16 || VPL == 32), "shape");
@@ -322,24 +326,29 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = (int)p.K, t = blockIdx.z;
     const int nslots = K + (p.sdown_w ? 1 : 0);
-    // row 0 holds the routing workgroup, dispatched ahead of the slots
-    if (blockIdx.y == 0) {
+    if (!PRE && blockIdx.y == 0) {
         if (blockIdx.x == 0) moe1_route(p, wave, t);
         return;
     }
-    const int sidx = blockIdx.y - 1;
-    // small inputs first: logits, and this wave's x blocks
+    const int sidx = PRE ? (int)blockIdx.y : (int)blockIdx.y - 1;
+    // small inputs first: logits (or the expert id), and this wave's x blocks
     constexpr int LPB = 256 / VPL;
     const int g0 = wave * NB;
     const int gx = g0 + lane / LPB;  // x block this lane quantises
-    float lv[kRoutePer], xv[VPL];
-    route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
-    q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
+    float xv[VPL];
     int e = (int)p.E;
-    if (sidx < K) {
-        int sel[kMoe1MaxSlots];
-        route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
-        e = sel[sidx];
+    if constexpr (PRE) {
+        if (sidx < K) e = __builtin_amdgcn_readfirstlane(p.experts[t * K + sidx]);
+        q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
+    } else {
+        float lv[kRoutePer];
+        route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
+        q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
+        if (sidx < K) {
+            int sel[kMoe1MaxSlots];
+            route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
+            e = sel[sidx];
+        }
     }
     const bool shared = sidx >= K;
     const uint8_t* gb = shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes;
@@ -412,12 +421,15 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     if (k == 0 && ok) p.act[((int64_t)t * nslots + sidx) * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
 }
 
+// Routing of every token of a call (grid M, two waves each).
+__global__ __launch_bounds__(128) void k_moe1_route(MoeParams p) { moe1_route(p, (int)(threadIdx.x >> 6), blockIdx.x); }
+
 // Grid (H/8, M); one wave per route slot of token t = blockIdx.y (blockDim
-// 64 * slots), all on the same
-// 8 hidden rows.  Each wave loads its slot's expert id and SwiGLU row, issues
-// its down-row burst, quantises the SwiGLU row into LDS while the weights
-// fly, and forms the row products; the 8 rows are then combined in route
-// order (multiply, then add) plus shared * gate.
+// 64 * slots), all on the same 8 hidden rows.  Each wave loads its slot's
+// expert id and SwiGLU row, issues its down-row burst, quantises the SwiGLU
+// row into LDS while the weights fly, and forms the row products; the 8
+// rows are then combined in route order (multiply, then add) plus
+// shared * gate.
 template <int DFMT, int NG>
 __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
     constexpr int VPL = NG * 4;  // SwiGLU values per lane (I = NG * 256)
@@ -483,15 +495,33 @@ bool moe1_supported(const MoeParams& p, int gfmt, int dfmt) {
            p.E <= kMoeMaxExperts;
 }
 
+// Stage 1 (gate/up, with the routing launch of a wide call) or 2 (down) of
+// a token-major call.
+template <int GFMT, int DFMT>
+hipError_t launch_moe1_stage(const MoeParams& p, int stage, hipStream_t s) {
+    const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
+    const unsigned m = (unsigned)p.M, rows_i = (unsigned)(p.I / 8);
+    if (stage == 1) {
+        if (p.M >= kMoeRouteLaunchMin) {
+            hipLaunchKernelGGL(k_moe1_route, dim3(m), dim3(128), 0, s, p);
+            hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8, true>), dim3(rows_i, nslots, m), dim3(256), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8, false>), dim3(rows_i, nslots + 1, m), dim3(256), 0, s, p);
+        }
+    } else if (stage == 2) {
+        hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), m), dim3(64 * nslots), 0, s, p);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int GFMT, int DFMT>
 hipError_t launch_moe1(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
-    const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
     if (ev) (void)hipEventRecord(ev[1], s);
-    hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1, (unsigned)p.M), dim3(256), 0, s, p);
-    if (hipError_t e = hipGetLastError()) return e;
+    if (hipError_t e = launch_moe1_stage<GFMT, DFMT>(p, 1, s)) return e;
     if (ev) (void)hipEventRecord(ev[2], s);
-    hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), (unsigned)p.M), dim3(64 * nslots), 0, s, p);
-    if (hipError_t e = hipGetLastError()) return e;
+    if (hipError_t e = launch_moe1_stage<GFMT, DFMT>(p, 2, s)) return e;
     if (ev) (void)hipEventRecord(ev[3], s);
     return hipSuccess;
 }
@@ -567,30 +597,12 @@ hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hip
     }
 }
 
-}  // namespace iq
-
-namespace iq {
-
-namespace {
-template <int GFMT, int DFMT>
-hipError_t stage_moe1(const MoeParams& p, int stage, hipStream_t s) {
-    const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
-    if (stage == 1)
-        hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8>), dim3((unsigned)(p.I / 8), nslots + 1, (unsigned)p.M), dim3(256), 0, s, p);
-    else if (stage == 2)
-        hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), (unsigned)p.M), dim3(64 * nslots), 0, s, p);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-}  // namespace
-
 hipError_t launch_moe_stage(const MoeParams& p, int gfmt, int dfmt, int stage, hipStream_t s) {
     if (!moe1_supported(p, gfmt, dfmt)) return hipErrorNotSupported;
-    if (gfmt == kQ4_K && dfmt == kQ6_K) return stage_moe1<kQ4_K, kQ6_K>(p, stage, s);
-    if (gfmt == kQ4_K && dfmt == kQ4_K) return stage_moe1<kQ4_K, kQ4_K>(p, stage, s);
-    if (gfmt == kQ6_K && dfmt == kQ6_K) return stage_moe1<kQ6_K, kQ6_K>(p, stage, s);
-    if (gfmt == kQ6_K && dfmt == kQ4_K) return stage_moe1<kQ6_K, kQ4_K>(p, stage, s);
+    if (gfmt == kQ4_K && dfmt == kQ6_K) return launch_moe1_stage<kQ4_K, kQ6_K>(p, stage, s);
+    if (gfmt == kQ4_K && dfmt == kQ4_K) return launch_moe1_stage<kQ4_K, kQ4_K>(p, stage, s);
+    if (gfmt == kQ6_K && dfmt == kQ6_K) return launch_moe1_stage<kQ6_K, kQ6_K>(p, stage, s);
+    if (gfmt == kQ6_K && dfmt == kQ4_K) return launch_moe1_stage<kQ6_K, kQ4_K>(p, stage, s);
     return hipErrorNotSupported;
 }
 
