@@ -355,7 +355,11 @@ def decode_sweep(args, hip, device, layers):
     layer -- then the LM head [248320 x 2048] Q6_K, at M = 1 and M = 8 rows.
     Every call of a step is launched in order on one stream (graph replay);
     reported: matmul time per step, tokens per second of matmul time, and
-    the step's algorithmic HBM bytes over that time."""
+    the step's algorithmic HBM bytes over that time.  The *_qkv_rows lines
+    run the same step with q/gate, k and v of each layer joined into one
+    [9216 x 2048] matrix (QuantizedMatrix::concatenate_rows,
+    src/gguf.rs:379-404, as the reference joins DeltaNet's qkvz): one launch
+    instead of three, the same bytes and bitwise the same outputs."""
     import torch
 
     from inferq_amd import qgemm, synth
@@ -367,6 +371,7 @@ def decode_sweep(args, hip, device, layers):
     lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 6000), synth.Q6_K,
                                     248320, 2048)
     dense_bytes = n * sum(m_.storage_bytes() for m_ in dense[0])
+    qkv = [d[0].concatenate_rows(d[1]).concatenate_rows(d[2]) for d in dense]
     gu, dn = expert_bytes()
     g = torch.Generator(device=device)
     g.manual_seed(args.seed + 9)
@@ -376,6 +381,7 @@ def decode_sweep(args, hip, device, layers):
         x4 = torch.randn(m, 4096, device=device, generator=g)
         lg = torch.randn(n, m, E, device=device, generator=g)
         ys = [torch.empty(m, r, device=device) for r, _ in shapes]
+        yqkv = torch.empty(m, 9216, device=device)
         out = torch.empty(m, H, device=device)
         ylm = torch.empty(m, 248320, device=device)
 
@@ -389,13 +395,21 @@ def decode_sweep(args, hip, device, layers):
                 layers[li][0].forward_into(x2, lg[li], out)
             lm.forward_into(x2, ylm)
 
-        ms = time_graph(step, 2, hip, warmup=1)
+        def step_qkv(i):
+            for li in range(n):
+                qkv[li].forward_into(x2, yqkv)
+                dense[li][3].forward_into(x4, ys[3])
+                layers[li][0].forward_into(x2, lg[li], out)
+            lm.forward_into(x2, ylm)
+
         uniq = float(np.mean([len(torch.unique(torch.topk(lg[li], TOPK, dim=1).indices)) for li in range(n)]))
         total = n * (uniq + 1) * (gu + dn) + dense_bytes + lm.storage_bytes()
-        res[f"m{m}"] = {"us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(m / (ms * 1e-3), 1),
-                        "unique_experts_per_layer": round(uniq, 1), "GB_per_step": round(total / 1e9, 3),
-                        "GB_s": round(total / ms / 1e6, 1), "frac_hbm": round(total / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    del dense, lm
+        for name, fn in ((f"m{m}", step), (f"m{m}_qkv_rows", step_qkv)):
+            ms = time_graph(fn, 2, hip, warmup=1)
+            res[name] = {"us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(m / (ms * 1e-3), 1),
+                         "unique_experts_per_layer": round(uniq, 1), "GB_per_step": round(total / 1e9, 3),
+                         "GB_s": round(total / ms / 1e6, 1), "frac_hbm": round(total / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    del dense, qkv, lm
     return res
 
 

@@ -141,6 +141,19 @@ def test_concatenated_rows_match_separate_matrices(gpu):
         assert_bitexact(lead.forward(x).cpu().numpy(), a.forward(x).cpu().numpy(), "leading_rows")
 
 
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_joined_attention_projections_match_separate_calls(gpu, m):
+    """q/gate [8192 x 2048], k and v [512 x 2048] joined by rows give bitwise
+    the three separate products at decode and verify widths (the
+    decode-step benchmark's joined form)."""
+    mats = [Q.QuantizedMatrix.view(S.random_matrix_device(Q4, r, 2048, gpu, 40 + j), Q4, r, 2048)
+            for j, r in enumerate((8192, 512, 512))]
+    joined = mats[0].concatenate_rows(mats[1]).concatenate_rows(mats[2])
+    x = torch.randn(m, 2048, device=gpu, generator=torch.Generator(device=gpu).manual_seed(m))
+    expected = torch.cat([mt.forward(x) for mt in mats], dim=1).cpu().numpy()
+    assert_bitexact(joined.forward(x).cpu().numpy(), expected, f"joined qkv m={m}")
+
+
 def test_host_entry_matches_device_entry(gpu, oracle):
     rng = np.random.default_rng(6)
     w = S.random_matrix(Q4, 128, 1024, rng)
