@@ -166,7 +166,9 @@ int quantize_for(const iq_weight* w, const float* x, int64_t m, const ActView& a
 // for the int8-MFMA path its layouts and split-K partial tiles).
 size_t matmul_ws_bytes(const iq_weight* w, int64_t m) {
     const size_t a = act_bytes(m, w->cols), p = prefill_workspace_size(view_of(w), m);
-    return a > p ? a : p;
+    const size_t d = dense_mfma_workspace_size(view_of(w), m);
+    const size_t ap = a > p ? a : p;
+    return ap > d ? ap : d;
 }
 
 int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* ws, size_t ws_bytes, int32_t* isum,
@@ -182,7 +184,10 @@ int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* w
         return fail(IQ_ERR_SHAPE, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
     }
     hipError_t e = hipErrorNotSupported;
-    if (!isum && gemv_supported(view_of(w), m)) e = launch_gemv(view_of(w), x, w->cols, m, y, w->rows, s);
+    if (!isum && dense_mfma_supported(view_of(w), m))
+        e = launch_dense_mfma(view_of(w), x, w->cols, m, y, w->rows, ws, s);
+    if (e == hipErrorNotSupported && !isum && gemv_supported(view_of(w), m))
+        e = launch_gemv(view_of(w), x, w->cols, m, y, w->rows, s);
     if (e == hipErrorNotSupported && !isum && prefill_supported(view_of(w), m))
         e = launch_prefill(view_of(w), x, w->cols, m, y, w->rows, ws, nullptr, nullptr, s);
     if (e == hipErrorNotSupported) {

@@ -1,0 +1,150 @@
+// iq_dense_mfma.hip -- y = x . W^T for Q4_K / Q6_K weights at 2..63 input
+// rows on large matrices (the LM head at verify widths), on int8 MFMA in the
+// reference's exact per-lane order (iq_mfma_lanes.h): every output is
+// bitwise what the one-row kernel gives, as src/gguf.rs:493-520 requires of
+// its row tiles.  The per-lane GEMV (iq_gemv.hip) spends eight exact dot
+// chains of VALU work per weight at 8 rows; here the integer dots run on
+// MFMA and the VALU keeps only the f32 chains.
+//
+// Two launches per call: k_dm_quant quantises x (Q8K, the lane-transposed
+// activation layout, block scales, 16-value sums as f16); k_dm_mm<FMT, RT>
+// takes 64 weight rows x 16 RT input rows per workgroup.
+#include "iq_internal.h"
+#include "iq_mfma_lanes.h"
+#include "iq_quant.h"
+
+namespace iq {
+
+namespace {
+
+struct DmArgs {
+    const uint8_t* w;  // [n][row_bytes]
+    int64_t n, row_bytes;
+    int nb;            // blocks per row
+    const int8_t* q;   // [m][nb * 256] quantised x, lane-transposed
+    const float* d;    // [m][nb] block scales
+    const _Float16* hs;  // [m][nb][16] 16-value sums
+    int m;
+    float* y;  // [m][ldy]
+    int64_t ldy;
+};
+
+// One wave per (row, 256-value block): Q8K (bit-exact from_float).
+__global__ __launch_bounds__(256) void k_dm_quant(const float* __restrict__ x, int64_t ldx, int m, int nb,
+                                                  int8_t* __restrict__ q, float* __restrict__ d,
+                                                  _Float16* __restrict__ hs) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= (int64_t)m * nb) return;  // uniform per wave
+    const int64_t row = wid / nb;
+    const int b = (int)(wid - row * nb);
+    const Q8KLane r = quant_q8k_core(load4(x + row * ldx + (int64_t)b * 256 + 4 * lane));
+    ((uint32_t*)(q + (row * nb + b) * 256))[perm_dword(lane >> 3, lane & 7)] = r.packed;
+    if (lane == 0) d[row * nb + b] = r.d;
+    if ((lane & 3) == 0) hs[(row * nb + b) * 16 + (lane >> 2)] = (_Float16)(float)r.bsum16;
+}
+
+// Grid (n / 64, m / (16 RT)): 64 weight rows x 16 RT input rows.
+template <int FMT, int RT>
+__global__ __launch_bounds__(256) void k_dm_mm(DmArgs a) {
+    using L = MlStage<FMT, RT>;
+    __shared__ __align__(16) uint8_t st[2][L::END];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15;
+    const int64_t n0 = (int64_t)blockIdx.x * kMlCols;
+    const int row0 = (int)blockIdx.y * 16 * RT;
+    const int rows = min(16 * RT, a.m - row0);
+    MlOperands op;
+    op.aq = a.q;
+    op.ldq = (int64_t)a.nb * 256;
+    op.ad = a.d;
+    op.ldd = a.nb;
+    op.hs = a.hs;
+    op.b0 = op.b1 = a.w + n0 * a.row_bytes;  // byte offsets stay within the tile's 64 rows
+    op.bsplit = kMlCols;
+    op.brow_bytes = a.row_bytes;
+    op.nb = a.nb;
+    const int64_t last = a.n - 1 - n0;
+    auto brow = [&](int t) -> int64_t { return t < last ? (int64_t)t : last; };
+    auto arow = [&](int rr) -> int64_t { return row0 + min(rr, rows - 1); };
+    float v[4 * RT];
+    ml_product<FMT, RT>(op, arow, brow, st, v);
+    const int64_t n = n0 + 16 * wave + jj;
+#pragma unroll
+    for (int r = 0; r < 4 * RT; r++) {
+        const int rr = 16 * (r >> 2) + 4 * q + (r & 3);
+        if (rr < rows && n < a.n) a.y[(int64_t)(row0 + rr) * a.ldy + n] = v[r];
+    }
+}
+
+constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct DmPlan {
+    size_t q_bytes, d_bytes, hs_bytes;
+    size_t total() const { return q_bytes + d_bytes + hs_bytes; }
+};
+
+DmPlan dm_plan(const WeightView& w, int64_t m) {
+    const int64_t nb = w.cols / 256;
+    DmPlan P;
+    P.q_bytes = align256((size_t)(m * nb * 256));
+    P.d_bytes = align256((size_t)(m * nb * 4));
+    P.hs_bytes = align256((size_t)(m * nb * 32));
+    return P;
+}
+
+template <int FMT, int RT>
+hipError_t launch_t(const DmArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)((a.n + kMlCols - 1) / kMlCols), (unsigned)((a.m + 16 * RT - 1) / (16 * RT)));
+    hipLaunchKernelGGL((k_dm_mm<FMT, RT>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Large K-quant matrices at 2..63 rows: from 64 MiB of weights (an LM head:
+// 2.2x-4.5x over the GEMV at 8-48 rows), and from 8 MiB at 16 rows or more
+// (q/gate [8192 x 2048]: 1.8x-2.4x).  Smaller matrices keep the GEMV, whose
+// latency is lower there (64 weight rows per workgroup leave a [512 x 2048]
+// matrix 8 workgroups).  Staging reads 16-byte chunks of Q4_K rows and
+// 4-byte-aligned windows of Q6_K blocks, so rows must keep that alignment
+// (Q6_K: an even block count per row).
+bool dense_mfma_supported(const WeightView& w, int64_t m) {
+    if (m < 2 || m >= kPrefillMinRows || w.cols % 256 != 0 || w.rows < 1) return false;
+    const int64_t bytes = w.rows * w.row_bytes;
+    if (bytes < ((int64_t)64 << 20) && (m < 16 || bytes < ((int64_t)8 << 20))) return false;
+    if (w.dtype == kQ4_K) return ((uintptr_t)w.w & 15) == 0;
+    if (w.dtype == kQ6_K) return ((uintptr_t)w.w & 3) == 0 && w.row_bytes % 4 == 0;
+    return false;
+}
+
+size_t dense_mfma_workspace_size(const WeightView& w, int64_t m) {
+    return dense_mfma_supported(w, m) ? dm_plan(w, m).total() : 0;
+}
+
+hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                             void* ws, hipStream_t s) {
+    if (!dense_mfma_supported(w, m)) return hipErrorNotSupported;
+    const DmPlan P = dm_plan(w, m);
+    uint8_t* base = (uint8_t*)ws;
+    DmArgs a;
+    a.w = w.w;
+    a.n = w.rows;
+    a.row_bytes = w.row_bytes;
+    a.nb = (int)(w.cols / 256);
+    a.q = (const int8_t*)base;
+    a.d = (const float*)(base + P.q_bytes);
+    a.hs = (const _Float16*)(base + P.q_bytes + P.d_bytes);
+    a.m = (int)m;
+    a.y = y;
+    a.ldy = ldy;
+    const int64_t qwaves = m * a.nb;
+    hipLaunchKernelGGL(k_dm_quant, dim3((unsigned)((qwaves + 3) / 4)), dim3(256), 0, s, x, ldx, (int)m, a.nb,
+                       (int8_t*)a.q, (float*)a.d, (_Float16*)a.hs);
+    if (hipError_t e = hipGetLastError()) return e;
+    if (w.dtype == kQ4_K) return m <= 16 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);
+    return m <= 16 ? launch_t<kQ6_K, 1>(a, s) : launch_t<kQ6_K, 2>(a, s);
+}
+
+}  // namespace iq

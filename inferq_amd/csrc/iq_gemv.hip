@@ -517,11 +517,11 @@ hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
 
 }  // namespace
 
-// Up to 8 rows every matrix takes this kernel.  Past 8 rows it runs one
-// tile of 8 rows per grid row, and each tile redoes the per-row lane work
-// while its weight reads hit L2: that wins (by 2x to 8x) on matrices up to
-// a few MiB, and up to 16 rows on anything short of an LM head; wider calls
-// on large matrices go to the lane kernel (iq_lanes.hip).
+// Up to 8 rows every matrix the MFMA kernel (iq_dense_mfma.hip) leaves
+// takes this kernel.  Past 8 rows it runs one tile of 8 rows per grid row,
+// and each tile redoes the per-row lane work while its weight reads hit L2:
+// that wins (by 2x to 8x) on matrices up to a few MiB; wider calls on other
+// matrices go to the lane kernel (iq_lanes.hip).
 bool gemv_supported(const WeightView& w, int64_t m) {
     if (m < 1 || m >= kPrefillMinRows || w.rows < 1) return false;
     const int64_t bytes = w.rows * w.row_bytes;

@@ -68,4 +68,13 @@ size_t prefill_workspace_size(const WeightView& w, int64_t m);
 hipError_t launch_prefill(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                           void* ws, int32_t* dbg_isum, int32_t* dbg_msum, hipStream_t s);
 
+// The exact lane-order int8-MFMA kernel for large Q4_K / Q6_K matrices at
+// 2..63 input rows (iq_dense_mfma.hip): bitwise the one-row results.
+// launch_dense_mfma quantises x itself into `ws` (at least
+// dense_mfma_workspace_size bytes).
+bool dense_mfma_supported(const WeightView& w, int64_t m);
+size_t dense_mfma_workspace_size(const WeightView& w, int64_t m);
+hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                             void* ws, hipStream_t s);
+
 }  // namespace iq

@@ -1,0 +1,321 @@
+// iq_mfma_lanes.h -- the reference's exact per-lane products on int8 MFMA,
+// for a tile of up to 16 RT activation rows against 64 weight rows (Q4_K or
+// Q6_K), shared by the grouped MoE kernels and the multi-row dense kernel.
+//
+// The reference's lane k (src/qgemm.rs:175-346) owns bytes 4k..4k+3 of every
+// 32-value chunk c of a block: isum_k = sum_c sc_c * dot4(w[c][k], a[c][k])
+// with one scale per dword, and it advances acc_k = fma(y.d * x.d, isum_k,
+// acc_k) once per block; the eight lanes meet in hsum_f32_8 (Q4_K mins: four
+// lanes, hsum_f32_4).  Int8 MFMAs whose K index runs over (c, e) for one
+// fixed k yield isum_k for a whole 16 x 16 tile: A holds the activation
+// dwords (c, k), c = 0..7, which the activation layout keeps contiguous
+// (dword 8k + c), and B the weight dwords (c, k) with each dword's scale
+// folded in.  Scaled weights exceed int8, so each is split into two int8
+// streams whose integer sums recombine exactly: Q4_K sc*q = 8 (sc >> 3) q +
+// (sc & 7) q; Q6_K sc*(q - 32) = 64 hi + lo with lo in 0..63 and hi in
+// -64..64.  The Q4_K mins msum_k = m_2k s_2k + m_2k+1 s_2k+1 (s = 32-value
+// activation sums) come from an f16 MFMA over the 16-value sums (integers
+// below 2^24: exact).  A lane keeps the f32 chains of all eight reference
+// lanes for its outputs and joins them at the end in the hsum trees' order,
+// ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) plus (m0+m2) + (m1+m3).
+#pragma once
+
+#include "iq_lanes.h"
+
+namespace iq {
+
+typedef int v4i_ml __attribute__((ext_vector_type(4)));
+typedef float v4f_ml __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h_ml __attribute__((ext_vector_type(4)));
+typedef short s16x2_ml __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_ml __attribute__((ext_vector_type(2)));
+
+constexpr int kMlCols = 64;  // weight rows per tile (16 per wave)
+constexpr int kMlAS = 272;   // LDS stride of an activation row (256 + pad)
+
+template <int FMT>
+struct MlFmt;
+template <>
+struct MlFmt<kQ4_K> {
+    static constexpr int BB = 144;  // block bytes
+    static constexpr int BS = 144;  // LDS bytes per staged row-block
+    static constexpr int NL = 9;    // staging loads per row-block (16 bytes each)
+    static constexpr bool kMins = true;
+};
+template <>
+struct MlFmt<kQ6_K> {
+    static constexpr int BB = 210;
+    static constexpr int BS = 224;  // the block's 212-byte dword window, padded
+    static constexpr int NL = 14;   // staging loads per row-block (16 bytes each)
+    static constexpr bool kMins = false;
+};
+
+// LDS stage of RT 16-row tiles: A int8 [16 RT][kMlAS], B [64][BS], D f32
+// [16 RT], H f16 [16 RT][16].
+template <int FMT, int RT>
+struct MlStage {
+    static constexpr int R = 16 * RT;
+    static constexpr int A = 0;
+    static constexpr int B = A + R * kMlAS;
+    static constexpr int D = B + kMlCols * MlFmt<FMT>::BS;
+    static constexpr int H = D + R * 4;
+    static constexpr int END = H + (MlFmt<FMT>::kMins ? R * 32 : 0);
+};
+
+// Bytes of q (each < 16) times s (< 8) byte by byte: every product is below
+// 128, so two 16-bit lanes never carry into each other.
+__device__ __forceinline__ uint32_t ml_bytes_mul_small(uint32_t q, uint32_t s) {
+    const u16x2_ml a = __builtin_bit_cast(u16x2_ml, q);
+    const u16x2_ml b = {(unsigned short)s, (unsigned short)s};
+    return __builtin_bit_cast(uint32_t, a * b);
+}
+
+// Four unsigned six-bit values u (bytes) times a signed scale sc, minus
+// 32 sc: p = sc * (u - 32) in -4064..4096, split p = 64 hi + lo; returns the
+// lo bytes (0..63) and the hi bytes (-64..64), byte order kept.
+__device__ __forceinline__ void ml_q6_scaled_split(uint32_t u, int sc, uint32_t& lo, uint32_t& hi) {
+    const s16x2_ml s2 = {(short)sc, (short)sc}, m2 = {(short)(-32 * sc), (short)(-32 * sc)};
+    const s16x2_ml u02 = __builtin_bit_cast(s16x2_ml, u & 0x00ff00ffu);         // bytes 0, 2
+    const s16x2_ml u13 = __builtin_bit_cast(s16x2_ml, (u >> 8) & 0x00ff00ffu);  // bytes 1, 3
+    const s16x2_ml p02 = u02 * s2 + m2, p13 = u13 * s2 + m2;
+    const uint32_t l02 = __builtin_bit_cast(uint32_t, p02) & 0x003f003fu;
+    const uint32_t l13 = __builtin_bit_cast(uint32_t, p13) & 0x003f003fu;
+    lo = l02 | (l13 << 8);
+    const s16x2_ml six = {6, 6};
+    const uint32_t h02 = __builtin_bit_cast(uint32_t, (s16x2_ml)(p02 >> six));
+    const uint32_t h13 = __builtin_bit_cast(uint32_t, (s16x2_ml)(p13 >> six));
+    // bytes 0 and 2 of h02 and of h13, interleaved
+    hi = __builtin_amdgcn_perm(h13, h02, 0x06020400u);
+}
+
+// The 4 bytes at byte offset o of a block staged with a dword shift of sh
+// (0 or 2) bytes.
+__device__ __forceinline__ uint32_t ml_lds_win(const uint8_t* row, int sh, int o) {
+    const uint32_t w0 = *(const uint32_t*)(row + o), w1 = *(const uint32_t*)(row + o + 4);
+    return __builtin_amdgcn_alignbyte(w1, w0, (uint32_t)sh);
+}
+
+// Operands of one tile.  Activation row rr (0 .. 16 RT - 1) of the tile is
+// row arow(rr) of aq (Q8K in the lane-transposed layout, ldq bytes a row),
+// ad (block scales, ldd a row) and hs ([row][nb][16] f16 16-value sums,
+// Q4_K only).  Weight row c (0..63) of the tile is row brow(c) of the
+// matrix at b0 (c < bsplit) or b1 (c >= bsplit), brow_bytes a row, nb blocks
+// along K.  All byte offsets within a matrix fit 32 bits.
+struct MlOperands {
+    const int8_t* aq;
+    int64_t ldq;
+    const float* ad;
+    int64_t ldd;
+    const _Float16* hs;
+    const uint8_t* b0;
+    const uint8_t* b1;
+    int bsplit;
+    int64_t brow_bytes;
+    int nb;
+};
+
+// The tile's products on a 256-thread workgroup: lane (q = l / 16, j = l % 16)
+// of wave w ends with v[r] = output (row 16 (r / 4) + 4 q + r % 4, weight
+// row 16 w + j), r < 4 RT.  `st` is the caller's LDS (2 stages).
+//
+// Fragments of v_mfma_i32_16x16x32_i8 for lane l (q = l / 16, j = l % 16):
+// A row j, K 8q..8q+7; B column j, the same K; the result holds rows
+// 4q..4q+3 of column j.  For lane k of the reference, K 8q..8q+7 are the
+// dwords (c, k) with c = 2q, 2q+1.
+template <int FMT, int RT, class ARow, class BRow>
+__device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow brow, uint8_t (*st)[MlStage<FMT, RT>::END],
+                                           float (&v)[4 * RT]) {
+    using F = MlFmt<FMT>;
+    using L = MlStage<FMT, RT>;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15;
+    const int nb = op.nb;
+
+    // ---- staging: every thread owns fixed slots, the same for every block.
+    // Sources are a wave-uniform base plus a 32-bit offset.
+    constexpr int kA = L::R * 16;              // 16-byte A chunks
+    constexpr int kB = kMlCols * F::NL;        // 16-byte B chunks
+    constexpr int kAPer = (kA + 255) / 256;    // 1 or 2
+    constexpr int kBPer = (kB + 255) / 256;    // Q4_K 3, Q6_K 4
+    uint32_t a_src[kAPer];
+    int a_off[kAPer];
+#pragma unroll
+    for (int i = 0; i < kAPer; i++) {
+        const int t = min((int)threadIdx.x + 256 * i, kA - 1);
+        const int rr = t >> 4, part = t & 15;
+        a_src[i] = (uint32_t)(arow(rr) * op.ldq + 16 * part);
+        a_off[i] = (int)threadIdx.x + 256 * i < kA ? L::A + rr * kMlAS + 16 * part : -1;
+    }
+    // B chunk t: column t / NL, part t % NL; columns past bsplit come from
+    // the second matrix.  Q6_K: the block's dword window (it starts 0 or 2
+    // bytes before the block) as 13 chunks plus one ending at its last byte.
+    uint32_t b_src[kBPer];
+    int b_off[kBPer];
+    bool b_hi[kBPer];
+#pragma unroll
+    for (int i = 0; i < kBPer; i++) {
+        const int t = min((int)threadIdx.x + 256 * i, kB - 1);
+        const int c2 = t / F::NL, part = t - c2 * F::NL;
+        const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
+        b_hi[i] = c2 >= op.bsplit;
+        b_src[i] = (uint32_t)(brow(c2) * op.brow_bytes + po);
+        b_off[i] = (int)threadIdx.x + 256 * i < kB ? L::B + c2 * F::BS + po : -1;
+    }
+    // D (row scales) on threads 0 .. R-1, H (16-value sums, Q4_K) on 64 .. 64 + 2R - 1
+    static_assert((L::R & (L::R - 1)) == 0, "tile rows");
+    const int tD = threadIdx.x, tH = threadIdx.x - 64;
+    const int64_t d_row = arow(tD & (L::R - 1));
+    const int64_t h_row = arow((tH >> 1) & (L::R - 1));  // in range for idle threads too
+
+    v4i_ml sa[kAPer];
+    u32x4 sb[kBPer];
+    float sd = 0.f;
+    v4i_ml sh16 = {};
+    auto issue = [&](int b) {
+        const int8_t* abase = op.aq + (int64_t)b * 256;
+#pragma unroll
+        for (int i = 0; i < kAPer; i++) sa[i] = *(const v4i_ml*)(abase + a_src[i]);
+        const int64_t boff = FMT == kQ6_K ? ((int64_t)b * F::BB) & ~(int64_t)3 : (int64_t)b * F::BB;
+#pragma unroll
+        for (int i = 0; i < kBPer; i++) sb[i] = *(const u32x4*)((b_hi[i] ? op.b1 : op.b0) + boff + b_src[i]);
+        if (tD < L::R) sd = op.ad[d_row * op.ldd + b];
+        if constexpr (F::kMins)
+            if (tH >= 0 && tH < 2 * L::R) sh16 = *(const v4i_ml*)(op.hs + (h_row * nb + b) * 16 + 8 * (tH & 1));
+    };
+    auto park = [&](uint8_t* s) {
+#pragma unroll
+        for (int i = 0; i < kAPer; i++)
+            if (a_off[i] >= 0) *(v4i_ml*)(s + a_off[i]) = sa[i];
+#pragma unroll
+        for (int i = 0; i < kBPer; i++)
+            if (b_off[i] >= 0) *(u32x4*)(s + b_off[i]) = sb[i];
+        if (tD < L::R) *(float*)(s + L::D + 4 * tD) = sd;
+        if constexpr (F::kMins)
+            if (tH >= 0 && tH < 2 * L::R) *(v4i_ml*)(s + L::H + 32 * (tH >> 1) + 16 * (tH & 1)) = sh16;
+    };
+
+    const int col = 16 * wave + jj;  // this lane's staged weight row
+    // output r of the lane: tile r / 4, row 16 (r / 4) + 4 q + r % 4;
+    // acc[k]: the f32 chain of reference lane k, accm[k] of mins lane k
+    float acc[8][4 * RT], accm[4][4 * RT];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int r = 0; r < 4 * RT; r++) acc[k][r] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int r = 0; r < 4 * RT; r++) accm[k][r] = 0.f;
+    issue(0);
+    park(st[0]);
+    lds_barrier();
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* S = st[b & 1];
+        if (b + 1 < nb) issue(b + 1);
+        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
+        const uint8_t* bcol = S + L::B + col * F::BS;
+        float dd[4 * RT], dm[4 * RT];
+        float xd, xdm = 0.f;
+        uint32_t s6a = 0, s6b = 0;  // Q4_K: six-bit scales of sub-blocks 2q, 2q+1
+        uint32_t q6s = 0;           // Q6_K: scale bytes 4q..4q+3
+        Q4Scales sc{};
+        if constexpr (FMT == kQ4_K) {
+            const u32x4a16 hdr = *(const u32x4a16*)bcol;
+            xd = f16_to_f32(hdr.x);
+            xdm = f16_to_f32(hdr.x >> 16);
+            sc = q4_scales(hdr.y, hdr.z, hdr.w);
+            const uint32_t sw = q < 2 ? sc.sc_lo : sc.sc_hi;
+            s6a = byte_of(sw, 2 * (q & 1));
+            s6b = byte_of(sw, 2 * (q & 1) + 1);
+        } else {
+            xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
+            q6s = ml_lds_win(bcol, sh, 192 + 4 * q);
+        }
+#pragma unroll
+        for (int r = 0; r < 4 * RT; r++) {
+            const float yd = *(const float*)(S + L::D + 4 * (16 * (r >> 2) + 4 * q + (r & 3)));
+            dd[r] = yd * xd;
+            if constexpr (F::kMins) dm[r] = -yd * xdm;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            uint32_t w1[2], w2[2];
+            int mul;  // isum = mul * (stream 1) + (stream 2)
+            if constexpr (FMT == kQ4_K) {
+                const uint32_t qd = *(const uint32_t*)(bcol + 16 + 32 * q + 4 * k);
+                const uint32_t lo = qd & 0x0f0f0f0fu, hi = (qd >> 4) & 0x0f0f0f0fu;
+                w1[0] = ml_bytes_mul_small(lo, s6a >> 3);
+                w1[1] = ml_bytes_mul_small(hi, s6b >> 3);
+                w2[0] = ml_bytes_mul_small(lo, s6a & 7u);
+                w2[1] = ml_bytes_mul_small(hi, s6b & 7u);
+                mul = 8;
+            } else {
+                const int hk = k >= 4;
+                const int qo = 64 * (q >> 1) + 4 * k;
+                const uint32_t l0 = ml_lds_win(bcol, sh, qo), l1 = ml_lds_win(bcol, sh, qo + 32);
+                const uint32_t qh = ml_lds_win(bcol, sh, 128 + 32 * (q >> 1) + 4 * k);
+#pragma unroll
+                for (int cc = 0; cc < 2; cc++) {
+                    const uint32_t l = cc ? l1 : l0;
+                    const uint32_t lo4 = (q & 1) ? ((l >> 4) & 0x0f0f0f0fu) : (l & 0x0f0f0f0fu);
+                    const uint32_t u = lo4 | (((qh >> (2 * (2 * (q & 1) + cc))) & 0x03030303u) << 4);
+                    const int scv = (int)(int8_t)(uint8_t)(q6s >> (8 * (2 * cc + hk)));
+                    ml_q6_scaled_split(u, scv, w2[cc], w1[cc]);
+                }
+                mul = 64;
+            }
+            const long b1 = (long)(((uint64_t)w1[1] << 32) | w1[0]);
+            const long b2 = (long)(((uint64_t)w2[1] << 32) | w2[0]);
+#pragma unroll
+            for (int t = 0; t < RT; t++) {
+                const long a = *(const long*)(S + L::A + (16 * t + jj) * kMlAS + 32 * k + 8 * q);
+                const v4i_ml z = {};
+                const v4i_ml i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, z, 0, 0, 0);
+                const v4i_ml i2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b2, z, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc[k][4 * t + r] = __builtin_fmaf(dd[4 * t + r], (float)(i1[r] * mul + i2[r]), acc[k][4 * t + r]);
+            }
+            // one lane's products at a time: the chains are advanced here
+            // (not sunk to the end of the block), which bounds the live
+            // MFMA results
+#pragma unroll
+            for (int r = 0; r < 4 * RT; r++) asm volatile("" : "+v"(acc[k][r]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (F::kMins) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t mwd = k < 2 ? sc.mn_lo : sc.mn_hi;
+                const _Float16 mA = (_Float16)(float)byte_of(mwd, 2 * (k & 1));
+                const _Float16 mB = (_Float16)(float)byte_of(mwd, 2 * (k & 1) + 1);
+                // B[kappa][col], kappa = 4 q + e: nonzero for q == k
+                const _Float16 zh = (_Float16)0.f;
+                const v4h_ml bm = q == k ? v4h_ml{mA, mA, mB, mB} : v4h_ml{zh, zh, zh, zh};
+#pragma unroll
+                for (int t = 0; t < RT; t++) {
+                    const v4h_ml am = *(const v4h_ml*)(S + L::H + (16 * t + jj) * 32 + 8 * q);
+                    const v4f_ml z = {};
+                    const v4f_ml ms = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) accm[k][4 * t + r] = __builtin_fmaf(dm[4 * t + r], ms[r], accm[k][4 * t + r]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4 * RT; r++) asm volatile("" : "+v"(accm[k][r]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + 1 < nb) park(st[(b + 1) & 1]);
+        lds_barrier();
+    }
+    // hsum_f32_8 and hsum_f32_4 over the lane chains
+#pragma unroll
+    for (int r = 0; r < 4 * RT; r++) {
+        v[r] = ((acc[0][r] + acc[4][r]) + (acc[2][r] + acc[6][r])) + ((acc[1][r] + acc[5][r]) + (acc[3][r] + acc[7][r]));
+        if constexpr (F::kMins) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
+    }
+}
+
+}  // namespace iq

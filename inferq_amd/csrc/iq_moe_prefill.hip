@@ -4,23 +4,9 @@
 // per-lane order: every token's output is bitwise what a one-token call
 // gives.
 //
-// Exact lane order on MFMA.  The reference's lane k (src/qgemm.rs:175-346)
-// owns bytes 4k..4k+3 of every 32-value chunk c of a block: isum_k =
-// sum_c sc_c * dot4(w[c][k], a[c][k]) with one scale per dword, and it
-// advances acc_k = fma(y.d * x.d, isum_k, acc_k) once per block; the eight
-// lanes meet in hsum_f32_8 (Q4_K mins: four lanes, hsum_f32_4).  Int8
-// MFMAs whose K index runs over (c, e) for one fixed k yield isum_k for a
-// whole 16 x 16 tile: A holds the activation dwords (c, k),
-// c = 0..7, which the activation layout keeps contiguous (dword 8k + c), and
-// B the weight dwords (c, k) with each dword's scale folded in.  Scaled
-// weights exceed int8, so each is split into two int8 streams whose integer
-// sums recombine exactly: Q4_K sc*q = 8 (sc >> 3) q + (sc & 7) q; Q6_K
-// sc*(q - 32) = 64 hi + lo with lo in 0..63 and hi in -64..64.  The Q4_K
-// mins msum_k = m_2k s_2k + m_2k+1 s_2k+1 (s = 32-value activation sums)
-// come from an f16 MFMA over the 16-value sums (integers below 2^24: exact).
-// A lane keeps the f32 chains of all eight reference lanes for its eight
-// outputs and joins them at the end in the hsum trees' order,
-// ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) plus (m0+m2) + (m1+m3).
+// The expert products are the exact lane-order MFMA tiles of
+// iq_mfma_lanes.h, so the bit pattern of every output matches the
+// reference's per-lane FMA chains.
 //
 // Six launches per call:
 //   k_mp_route    one wave per token: top-k, routing weights, shared gate;
@@ -37,6 +23,7 @@
 #include <type_traits>
 
 #include "iq_lanes.h"
+#include "iq_mfma_lanes.h"
 #include "iq_moe.h"
 #include "iq_quant.h"
 #include "iq_route.h"
@@ -45,16 +32,8 @@ namespace iq {
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-
 constexpr int kMpThreads = 1024;  // routing and grouping workgroups
 constexpr int kMpRows = 32;       // grouped rows per chunk (one MFMA row tile)
-constexpr int kMpCols = 64;       // weight rows per product workgroup (16 per wave)
-constexpr int kMpAS = 272;        // LDS stride of an activation row (256 + pad)
 
 // ------------------------------------------------------------ routing
 __global__ __launch_bounds__(kMpThreads) void k_mp_route(MoeParams p) {
@@ -194,81 +173,15 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
 }
 
 // ------------------------------------------------------ expert products
-template <int FMT>
-struct MpFmt;
-template <>
-struct MpFmt<kQ4_K> {
-    static constexpr int BB = 144;  // block bytes
-    static constexpr int BS = 144;  // LDS bytes per staged row-block
-    static constexpr int NL = 9;    // staging loads per row-block (16 bytes each)
-    static constexpr bool kMins = true;
-};
-template <>
-struct MpFmt<kQ6_K> {
-    static constexpr int BB = 210;
-    static constexpr int BS = 224;  // the block's 212-byte dword window, padded
-    static constexpr int NL = 14;   // staging loads per row-block (16 bytes each)
-    static constexpr bool kMins = false;
-};
-
-// LDS stage: A int8 [32][kMpAS], B [64][BS], D f32 [32], H f16 [32][16]
-template <int FMT>
-struct MpStage {
-    static constexpr int A = 0;
-    static constexpr int B = A + kMpRows * kMpAS;
-    static constexpr int D = B + kMpCols * MpFmt<FMT>::BS;
-    static constexpr int H = D + kMpRows * 4;
-    static constexpr int END = H + (MpFmt<FMT>::kMins ? kMpRows * 32 : 0);
-};
-
-// Bytes of q (each < 16) times s (< 8) byte by byte: every product is below
-// 128, so two 16-bit lanes never carry into each other.
-__device__ __forceinline__ uint32_t bytes_mul_small(uint32_t q, uint32_t s) {
-    const u16x2 a = __builtin_bit_cast(u16x2, q);
-    const u16x2 b = {(unsigned short)s, (unsigned short)s};
-    return __builtin_bit_cast(uint32_t, a * b);
-}
-
-// Four unsigned six-bit values u (bytes) times a signed scale sc, minus
-// 32 sc: p = sc * (u - 32) in -4064..4096, split p = 64 hi + lo; returns the
-// lo bytes (0..63) and the hi bytes (-64..64), byte order kept.
-__device__ __forceinline__ void q6_scaled_split(uint32_t u, int sc, uint32_t& lo, uint32_t& hi) {
-    const s16x2 s2 = {(short)sc, (short)sc}, m2 = {(short)(-32 * sc), (short)(-32 * sc)};
-    const s16x2 u02 = __builtin_bit_cast(s16x2, u & 0x00ff00ffu);         // bytes 0, 2
-    const s16x2 u13 = __builtin_bit_cast(s16x2, (u >> 8) & 0x00ff00ffu);  // bytes 1, 3
-    const s16x2 p02 = u02 * s2 + m2, p13 = u13 * s2 + m2;
-    const uint32_t l02 = __builtin_bit_cast(uint32_t, p02) & 0x003f003fu;
-    const uint32_t l13 = __builtin_bit_cast(uint32_t, p13) & 0x003f003fu;
-    lo = l02 | (l13 << 8);
-    const s16x2 six = {6, 6};
-    const uint32_t h02 = __builtin_bit_cast(uint32_t, (s16x2)(p02 >> six));
-    const uint32_t h13 = __builtin_bit_cast(uint32_t, (s16x2)(p13 >> six));
-    // bytes 0 and 2 of h02 and of h13, interleaved
-    hi = __builtin_amdgcn_perm(h13, h02, 0x06020400u);
-}
-
-// The 4 bytes at byte offset o of a block staged with a dword shift of sh
-// (0 or 2) bytes.
-__device__ __forceinline__ uint32_t lds_win(const uint8_t* row, int sh, int o) {
-    const uint32_t w0 = *(const uint32_t*)(row + o), w1 = *(const uint32_t*)(row + o + 4);
-    return __builtin_amdgcn_alignbyte(w1, w0, (uint32_t)sh);
-}
-
 // Grid (column tiles, chunk bound).  A workgroup owns one chunk (32 grouped
-// rows) and 64 weight rows; wave w owns 16 of them and both 16-row halves of
-// the chunk (two 16 x 16 MFMA tiles).  MODE 0: gate/up, weight rows
-// i0 + 0..31 of gate (waves 0, 1) and of up (waves 2, 3), A the chunk's
-// tokens of x; SwiGLU into act.  MODE 1: down, 64 hidden rows, A the chunk's
-// act rows; results into vals.
-//
-// Fragments of v_mfma_i32_16x16x32_i8 for lane l (q = l / 16, j = l % 16):
-// A row j, K 8q..8q+7; B column j, the same K; the result holds rows
-// 4q..4q+3 of column j.  For lane k of the reference, K 8q..8q+7 are the
-// dwords (c, k) with c = 2q, 2q+1.
+// rows) and 64 weight rows (ml_product: wave w owns 16 of them and both
+// 16-row halves of the chunk).  MODE 0: gate/up, weight rows i0 + 0..31 of
+// gate (waves 0, 1) and of up (waves 2, 3), A the chunk's tokens of x;
+// SwiGLU into act.  MODE 1: down, 64 hidden rows, A the chunk's act rows;
+// results into vals.
 template <int FMT, int MODE>
 __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
-    using F = MpFmt<FMT>;
-    using L = MpStage<FMT>;
+    using L = MlStage<FMT, 2>;
     __shared__ __align__(16) uint8_t st[2][L::END];
     const int c = blockIdx.y;
     if (c >= p.meta[1]) return;  // whole workgroup
@@ -281,216 +194,35 @@ __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
     const bool shared = e == (int)p.E;
     const int pos0 = start + r0;
 
-    // operands of this call
+    MlOperands op;
     const ActView& av = MODE == 0 ? p.xq : p.aq;
-    const _Float16* hsrc = MODE == 0 ? p.xhs : p.ahs;
-    const int nb = MODE == 0 ? p.g_nbw : p.d_nbw;  // weight blocks per row = activation blocks
-    const int64_t wrow_bytes = MODE == 0 ? p.g_row_bytes : p.d_row_bytes;
-
-    // ---- staging: every thread owns fixed slots, the same for every block.
-    // Sources are a wave-uniform base plus a 32-bit offset.
-    const uint8_t* gbase = nullptr;  // matrix of staged columns 0..31 (MODE 0) or all
-    const uint8_t* ubase = nullptr;  // matrix of staged columns 32..63 (MODE 0)
+    op.aq = av.q;
+    op.ldq = av.ldq;
+    op.ad = av.d;
+    op.ldd = av.ldd;
+    op.hs = MODE == 0 ? p.xhs : p.ahs;
+    op.nb = MODE == 0 ? p.g_nbw : p.d_nbw;  // weight blocks per row = activation blocks
+    op.brow_bytes = MODE == 0 ? p.g_row_bytes : p.d_row_bytes;
     if constexpr (MODE == 0) {
-        gbase = shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes;
-        ubase = shared ? p.sup_w : p.up + (int64_t)e * p.g_exp_bytes;
+        op.b0 = shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes;
+        op.b1 = shared ? p.sup_w : p.up + (int64_t)e * p.g_exp_bytes;
+        op.bsplit = 32;
     } else {
-        gbase = shared ? p.sdown_w : p.down + (int64_t)e * p.d_exp_bytes;
-        ubase = gbase;
+        op.b0 = op.b1 = shared ? p.sdown_w : p.down + (int64_t)e * p.d_exp_bytes;
+        op.bsplit = kMlCols;
     }
-    // weight row (within its matrix) of staged column t, clamped
-    auto wrow = [&](int t) -> int64_t {
+    // weight row (within its matrix) of tile column t, clamped
+    auto brow = [&](int t) -> int64_t {
         if constexpr (MODE == 0) return min((int64_t)blockIdx.x * 32 + (t & 31), p.I - 1);
-        else return min((int64_t)blockIdx.x * kMpCols + t, p.H - 1);
+        else return min((int64_t)blockIdx.x * kMlCols + t, p.H - 1);
     };
-    // activation row of staged row rr (0..31), clamped to the chunk
+    // activation row of tile row rr (0..31), clamped to the chunk
     auto arow = [&](int rr) -> int64_t {
         const int pos = pos0 + min(rr, rows - 1);
         return MODE == 0 ? (int64_t)p.assign_row[pos] : (int64_t)pos;
     };
-
-    constexpr int kA = kMpRows * 16;         // 16-byte A chunks
-    constexpr int kB = kMpCols * F::NL;      // 16-byte B chunks
-    constexpr int kAPer = kA / 256;          // 2
-    constexpr int kBPer = (kB + 255) / 256;  // Q4_K 3, Q6_K 4
-    uint32_t a_src[kAPer];
-    int a_off[kAPer];
-#pragma unroll
-    for (int i = 0; i < kAPer; i++) {
-        const int t = threadIdx.x + 256 * i;
-        const int rr = t >> 4, part = t & 15;
-        a_src[i] = (uint32_t)(arow(rr) * av.ldq + 16 * part);
-        a_off[i] = L::A + rr * kMpAS + 16 * part;
-    }
-    // B chunk t: column t / NL, part t % NL.  Columns 0..31 and 32..63 of
-    // MODE 0 split at t = 32 NL, a multiple of 32 but not of 64: the matrix
-    // is chosen per lane.  Q6_K: the block's dword window (it starts 0 or 2
-    // bytes before the block) as 13 chunks plus one ending at its last byte.
-    uint32_t b_src[kBPer];
-    int b_off[kBPer];
-    bool b_up[kBPer];
-#pragma unroll
-    for (int i = 0; i < kBPer; i++) {
-        const int t = min((int)threadIdx.x + 256 * i, kB - 1);
-        const int c2 = t / F::NL, part = t - c2 * F::NL;
-        const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
-        b_up[i] = MODE == 0 && c2 >= 32;
-        b_src[i] = (uint32_t)(wrow(c2) * wrow_bytes + po);
-        b_off[i] = (int)threadIdx.x + 256 * i < kB ? L::B + c2 * F::BS + po : -1;
-    }
-    // D (row scales) on threads 0..31, H (16-value sums, Q4_K) on 64..127
-    const int tD = threadIdx.x, tH = threadIdx.x - 64;
-    const int64_t d_row = arow(tD & 31);
-    const int64_t h_row = arow((tH >> 1) & 31);
-
-    v4i sa[kAPer];
-    u32x4 sb[kBPer];
-    float sd = 0.f;
-    v4i sh16 = {};
-    auto issue = [&](int b) {
-        const int8_t* abase = av.q + (int64_t)b * 256;
-#pragma unroll
-        for (int i = 0; i < kAPer; i++) sa[i] = *(const v4i*)(abase + a_src[i]);
-        const int64_t boff = FMT == kQ6_K ? ((int64_t)b * F::BB) & ~(int64_t)3 : (int64_t)b * F::BB;
-#pragma unroll
-        for (int i = 0; i < kBPer; i++) sb[i] = *(const u32x4*)((b_up[i] ? ubase : gbase) + boff + b_src[i]);
-        if (tD < 32) sd = av.d[d_row * av.ldd + b];
-        if constexpr (F::kMins)
-            if (tH >= 0 && tH < 64) sh16 = *(const v4i*)(hsrc + (h_row * nb + b) * 16 + 8 * (tH & 1));
-    };
-    auto park = [&](uint8_t* s) {
-#pragma unroll
-        for (int i = 0; i < kAPer; i++) *(v4i*)(s + a_off[i]) = sa[i];
-#pragma unroll
-        for (int i = 0; i < kBPer; i++)
-            if (b_off[i] >= 0) *(u32x4*)(s + b_off[i]) = sb[i];
-        if (tD < 32) *(float*)(s + L::D + 4 * tD) = sd;
-        if constexpr (F::kMins)
-            if (tH >= 0 && tH < 64) *(v4i*)(s + L::H + 32 * (tH >> 1) + 16 * (tH & 1)) = sh16;
-    };
-
-    const int col = 16 * wave + jj;  // this lane's staged weight row
-    // output r of the lane: tile r / 4, row 16 (r / 4) + 4 q + r % 4;
-    // acc[k]: the f32 chain of reference lane k, accm[k] of mins lane k
-    float acc[8][8], accm[4][8];
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-#pragma unroll
-        for (int r = 0; r < 8; r++) acc[k][r] = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int r = 0; r < 8; r++) accm[k][r] = 0.f;
-    issue(0);
-    park(st[0]);
-    lds_barrier();
-    for (int b = 0; b < nb; b++) {
-        const uint8_t* S = st[b & 1];
-        if (b + 1 < nb) issue(b + 1);
-        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
-        const uint8_t* bcol = S + L::B + col * F::BS;
-        float dd[8], dm[8];
-        float xd, xdm = 0.f;
-        uint32_t s6a = 0, s6b = 0;  // Q4_K: six-bit scales of sub-blocks 2q, 2q+1
-        uint32_t q6s = 0;           // Q6_K: scale bytes 4q..4q+3
-        Q4Scales sc{};
-        if constexpr (FMT == kQ4_K) {
-            const u32x4a16 hdr = *(const u32x4a16*)bcol;
-            xd = f16_to_f32(hdr.x);
-            xdm = f16_to_f32(hdr.x >> 16);
-            sc = q4_scales(hdr.y, hdr.z, hdr.w);
-            const uint32_t sw = q < 2 ? sc.sc_lo : sc.sc_hi;
-            s6a = byte_of(sw, 2 * (q & 1));
-            s6b = byte_of(sw, 2 * (q & 1) + 1);
-        } else {
-            xd = f16_to_f32(lds_win(bcol, sh, 208) & 0xffffu);
-            q6s = lds_win(bcol, sh, 192 + 4 * q);
-        }
-#pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const float yd = *(const float*)(S + L::D + 4 * (16 * (r >> 2) + 4 * q + (r & 3)));
-            dd[r] = yd * xd;
-            if constexpr (F::kMins) dm[r] = -yd * xdm;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            uint32_t w1[2], w2[2];
-            int mul;  // isum = mul * (stream 1) + (stream 2)
-            if constexpr (FMT == kQ4_K) {
-                const uint32_t qd = *(const uint32_t*)(bcol + 16 + 32 * q + 4 * k);
-                const uint32_t lo = qd & 0x0f0f0f0fu, hi = (qd >> 4) & 0x0f0f0f0fu;
-                w1[0] = bytes_mul_small(lo, s6a >> 3);
-                w1[1] = bytes_mul_small(hi, s6b >> 3);
-                w2[0] = bytes_mul_small(lo, s6a & 7u);
-                w2[1] = bytes_mul_small(hi, s6b & 7u);
-                mul = 8;
-            } else {
-                const int hk = k >= 4;
-                const int qo = 64 * (q >> 1) + 4 * k;
-                const uint32_t l0 = lds_win(bcol, sh, qo), l1 = lds_win(bcol, sh, qo + 32);
-                const uint32_t qh = lds_win(bcol, sh, 128 + 32 * (q >> 1) + 4 * k);
-#pragma unroll
-                for (int cc = 0; cc < 2; cc++) {
-                    const uint32_t l = cc ? l1 : l0;
-                    const uint32_t lo4 = (q & 1) ? ((l >> 4) & 0x0f0f0f0fu) : (l & 0x0f0f0f0fu);
-                    const uint32_t u = lo4 | (((qh >> (2 * (2 * (q & 1) + cc))) & 0x03030303u) << 4);
-                    const int scv = (int)(int8_t)(uint8_t)(q6s >> (8 * (2 * cc + hk)));
-                    q6_scaled_split(u, scv, w2[cc], w1[cc]);
-                }
-                mul = 64;
-            }
-            const long b1 = (long)(((uint64_t)w1[1] << 32) | w1[0]);
-            const long b2 = (long)(((uint64_t)w2[1] << 32) | w2[0]);
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const long a = *(const long*)(S + L::A + (16 * t + jj) * kMpAS + 32 * k + 8 * q);
-                const v4i z = {};
-                const v4i i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, z, 0, 0, 0);
-                const v4i i2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b2, z, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc[k][4 * t + r] = __builtin_fmaf(dd[4 * t + r], (float)(i1[r] * mul + i2[r]), acc[k][4 * t + r]);
-            }
-            // one lane's products at a time: the chains are advanced here
-            // (not sunk to the end of the block), which bounds the live
-            // MFMA results
-#pragma unroll
-            for (int r = 0; r < 8; r++) asm volatile("" : "+v"(acc[k][r]));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (F::kMins) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t mwd = k < 2 ? sc.mn_lo : sc.mn_hi;
-                const _Float16 mA = (_Float16)(float)byte_of(mwd, 2 * (k & 1));
-                const _Float16 mB = (_Float16)(float)byte_of(mwd, 2 * (k & 1) + 1);
-                // B[kappa][col], kappa = 4 q + e: nonzero for q == k
-                const _Float16 zh = (_Float16)0.f;
-                const v4h bm = q == k ? v4h{mA, mA, mB, mB} : v4h{zh, zh, zh, zh};
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const v4h am = *(const v4h*)(S + L::H + (16 * t + jj) * 32 + 8 * q);
-                    const v4f z = {};
-                    const v4f ms = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) accm[k][4 * t + r] = __builtin_fmaf(dm[4 * t + r], ms[r], accm[k][4 * t + r]);
-                }
-#pragma unroll
-                for (int r = 0; r < 8; r++) asm volatile("" : "+v"(accm[k][r]));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (b + 1 < nb) park(st[(b + 1) & 1]);
-        lds_barrier();
-    }
-    // hsum_f32_8 and hsum_f32_4 over the lane chains
     float v[8];
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-        v[r] = ((acc[0][r] + acc[4][r]) + (acc[2][r] + acc[6][r])) + ((acc[1][r] + acc[5][r]) + (acc[3][r] + acc[7][r]));
-        if constexpr (F::kMins) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
-    }
+    ml_product<FMT, 2>(op, arow, brow, st, v);
 
     if constexpr (MODE == 0) {
         // waves 2, 3 hold up of the columns waves 0, 1 hold gate of
@@ -511,7 +243,7 @@ __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
             }
         }
     } else {
-        const int64_t n = (int64_t)blockIdx.x * kMpCols + col;
+        const int64_t n = (int64_t)blockIdx.x * kMlCols + 16 * wave + jj;
 #pragma unroll
         for (int r = 0; r < 8; r++) {
             const int rr = 16 * (r >> 2) + 4 * q + (r & 3);
@@ -581,7 +313,7 @@ hipError_t launch_p(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
     hipLaunchKernelGGL((k_mp_actq<DFMT>), dim3((unsigned)((aw + 3) / 4)), dim3(256), 0, s, p, P);
     if (hipError_t e = hipGetLastError()) return e;
     if (ev) (void)hipEventRecord(ev[2], s);
-    hipLaunchKernelGGL((k_mp_mm<DFMT, 1>), dim3((unsigned)((p.H + kMpCols - 1) / kMpCols), (unsigned)p.max_chunks),
+    hipLaunchKernelGGL((k_mp_mm<DFMT, 1>), dim3((unsigned)((p.H + kMlCols - 1) / kMlCols), (unsigned)p.max_chunks),
                        dim3(256), 0, s, p);
     if (hipError_t e = hipGetLastError()) return e;
     hipLaunchKernelGGL(k_mp_combine, dim3((unsigned)(((int64_t)M * p.H + 255) / 256)), dim3(256), 0, s, p);

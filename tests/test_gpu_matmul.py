@@ -141,6 +141,29 @@ def test_concatenated_rows_match_separate_matrices(gpu):
         assert_bitexact(lead.forward(x).cpu().numpy(), a.forward(x).cpu().numpy(), "leading_rows")
 
 
+@pytest.fixture(scope="module")
+def large_matrices():
+    """Matrices past the size where 2..63-row calls take the exact-order MFMA
+    kernel (iq_dense_mfma.hip): Q6_K [40960 x 2048] (68.8 MB, LM-head-like)
+    and Q4_K [61440 x 2048] (70.8 MB)."""
+    rng = np.random.default_rng(77)
+    return {Q6: (S.random_matrix(Q6, 40960, 2048, rng), 40960), Q4: (S.random_matrix(Q4, 61440, 2048, rng), 61440)}
+
+
+@pytest.mark.parametrize("dtype", [Q6, Q4], ids=["q6k", "q4k"])
+def test_large_matrix_rows_bitexact(gpu, oracle, large_matrices, dtype):
+    """2..63 input rows on a large matrix (one and two 16-row tiles, ragged
+    tails) are bitwise the oracle's, hence bitwise the one-row results."""
+    w, rows = large_matrices[dtype]
+    mat = Q.QuantizedMatrix.upload(w, dtype, rows, 2048)
+    impl = 1 if oracle.have_avx2() else 0
+    for m in (1, 2, 3, 8, 16, 17, 33, 63):
+        x = S.normal((m, 2048), np.random.default_rng(2000 + m))
+        expected = oracle.matmul(dtype, w, rows, 2048, x, impl=impl, nthreads=8)
+        got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+        assert_bitexact(got, expected, f"{S.NAMES[dtype]} [{rows}x2048] m={m}")
+
+
 @pytest.mark.parametrize("m", [1, 8, 16])
 def test_joined_attention_projections_match_separate_calls(gpu, m):
     """q/gate [8192 x 2048], k and v [512 x 2048] joined by rows give bitwise
