@@ -31,6 +31,9 @@ FLAGS = [
     "-fno-fast-math",
     "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: no accumulator-register copies back to VALU
+    # operands (the exact lane-order tiles read every MFMA result at once)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
     "-Wall",
