@@ -515,6 +515,111 @@ hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
     }
 }
 
+// One input row, K-quant weights of 8 or 16 blocks per row: y = x . W^T
+// with the row's K split over the 4 waves of a workgroup (8 weight rows per
+// workgroup), as in the one-token MoE kernels.  Each wave issues its blocks'
+// weight burst, quantises its x blocks into LDS under it and forms the
+// exact per-block lane integers; wave 0 then advances the reference's
+// in-order FMA chains over all blocks and reduces them with the hsum trees.
+// A mid-size matrix at one row is latency-bound, and a quarter of the
+// decode per wave shortens its critical path.
+template <int FMT, int NG>
+__global__ __launch_bounds__(256) void k_gemv1_sk(const uint8_t* __restrict__ w, int64_t n, int64_t row_bytes,
+                                                  const float* __restrict__ x, float* __restrict__ y) {
+    constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
+    static_assert(NG % NW == 0 && (VPL == 8 || VPL == 16), "shape");
+    __shared__ __align__(16) int8_t s_q[NG * 256];
+    __shared__ __align__(16) float s_d[NG * 8];
+    __shared__ __align__(16) int16_t s_s8[NG * 8];
+    __shared__ int s_isum[8][8][NG];  // [row][lane k][block]
+    __shared__ int s_msum[8][4][NG];
+    __shared__ float s_dd[8][NG], s_dm[8][NG];
+    const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int LPB = 256 / VPL;
+    const int g0 = wave * NB;
+    const int gx = g0 + lane / LPB;  // x block this lane quantises
+    float xv[VPL];
+    q8k_vpl_load<VPL>(x + (int64_t)gx * 256, xv);
+    const int64_t i = (int64_t)blockIdx.x * 8 + slot;
+    const int64_t ic = i < n ? i : n - 1;
+    const uint8_t* wrow[1] = {w + ic * row_bytes + (int64_t)g0 * WT<FMT>::kBlockBytes};
+    typename WT<FMT>::T wb[1][NB];
+    lanes_load_exact<FMT, 1, NB>(wrow, k, wb);
+    ActView a;
+    a.ng = NG;
+    a.ldq = NG * 256;
+    a.ldd = NG * 8;
+    a.m = 1;
+    a.q = s_q;
+    a.d = s_d;
+    a.s8 = s_s8;
+    quant_q8k_vpl<VPL>(xv, true, 0, gx, a);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int g = g0 + b;
+        uint32_t av[8];
+        load_act(a, 0, g, k, av);
+        const float yd = a.d[g];
+        if constexpr (FMT == kQ4_K) {
+            const Q4Dec dec = q4_decode(wb[0][b], k);
+            const uint32_t q8s = *(const uint32_t*)(a.s8 + g * 8 + 2 * (k & 3));
+            int32_t isum, msum;
+            float d, dmin;
+            q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
+            s_isum[slot][k][g] = isum;
+            if (k < 4) s_msum[slot][k][g] = msum;
+            if (k == 0) {
+                s_dd[slot][g] = d;
+                s_dm[slot][g] = dmin;
+            }
+        } else {
+            const Q6Dec dec = q6_decode(wb[0][b], k);
+            int32_t isum;
+            float d;
+            q6_dot(dec, av, yd, isum, d);
+            s_isum[slot][k][g] = isum;
+            if (k == 0) s_dd[slot][g] = d;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float acc = 0.f, accm = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        acc = __builtin_fmaf(s_dd[slot][g], (float)s_isum[slot][k][g], acc);
+        if constexpr (FMT == kQ4_K) accm = __builtin_fmaf(s_dm[slot][g], (float)s_msum[slot][k & 3][g], accm);
+    }
+    float v = hsum8(acc);
+    if constexpr (FMT == kQ4_K) v = v + hsum4(accm);
+    if (k == 0 && i < n) y[i] = v;
+}
+
+template <int FMT>
+hipError_t launch_sk(const WeightView& w, const float* x, float* y, hipStream_t s) {
+    const unsigned groups = (unsigned)((w.rows + 7) / 8);
+    if (w.cols == 2048) hipLaunchKernelGGL((k_gemv1_sk<FMT, 8>), dim3(groups), dim3(256), 0, s, w.w, w.rows, w.row_bytes, x, y);
+    else hipLaunchKernelGGL((k_gemv1_sk<FMT, 16>), dim3(groups), dim3(256), 0, s, w.w, w.rows, w.row_bytes, x, y);
+    return hipGetLastError();
+}
+
+// One-row calls on K-quant matrices of width 2048 or 4096 up to
+// IQ_SK_MAX_BYTES (larger ones stream better through k_gemv); Q6_K rows of
+// an even block count keep the burst's dword alignment.
+#ifndef IQ_SK_MAX_BYTES
+#define IQ_SK_MAX_BYTES (64ll << 20)
+#endif
+bool sk_supported(const WeightView& w) {
+    if (w.cols != 2048 && w.cols != 4096) return false;
+    if (w.rows * w.row_bytes > (int64_t)IQ_SK_MAX_BYTES) return false;
+    if (w.dtype == kQ4_K) return ((uintptr_t)w.w & 15) == 0;
+    if (w.dtype == kQ6_K) return ((uintptr_t)w.w & 3) == 0;
+    return false;
+}
+
 }  // namespace
 
 // Up to 8 rows every matrix the MFMA kernel (iq_dense_mfma.hip) leaves
@@ -540,6 +645,7 @@ bool gemv_supported(const WeightView& w, int64_t m) {
 hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                        hipStream_t s) {
     if (!gemv_supported(w, m)) return hipErrorNotSupported;
+    if (m == 1 && sk_supported(w)) return w.dtype == kQ4_K ? launch_sk<kQ4_K>(w, x, y, s) : launch_sk<kQ6_K>(w, x, y, s);
     GemvArgs args;
     args.w = w.w;
     args.n = w.rows;
