@@ -28,7 +28,7 @@ SHAPES = [
     (Q4, 96, 512), (Q6, 96, 512), (Q8, 96, 512),
     (Q4, 1024, 2048), (Q6, 2048, 512), (Q8, 4096, 2048),
     (Q4, 2048, 4096), (Q6, 37, 768), (Q8, 45, 96), (Q4, 13, 256),
-    (Q6, 300, 2048), (Q6, 64, 4096), (Q4, 77, 2048), (Q8, 19, 1024), (Q6, 5, 6144),
+    (Q6, 300, 2048), (Q6, 64, 4096), (Q4, 77, 2048), (Q8, 19, 1024), (Q6, 5, 6144), (Q8, 40, 4096),
 ]
 ROWS = [1, 2, 3, 4, 7, 8, 9, 15, 16, 17, 33, 48, 63]
 
