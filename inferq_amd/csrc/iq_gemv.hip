@@ -598,6 +598,118 @@ __global__ __launch_bounds__(256) void k_gemv1_sk(const uint8_t* __restrict__ w,
     if (k == 0 && i < n) y[i] = v;
 }
 
+// The same split for a tile of MT input rows: each wave quantises its x
+// blocks of every row into LDS and forms the exact per-block integers of its
+// blocks for every row, sharing one decode of its weights; the in-order
+// chains of row r then run on wave r % 4.  Each row's result is the one-row
+// kernel's.  Launched at two rows, where it takes q/gate [8192 x 2048] from
+// 10.7 to 8.4 us and k/v [512 x 2048] from 7.1 to 4.9 us; at 3-8 rows the
+// row-tiled k_gemv is faster (the per-row LDS traffic and chains grow with
+// the rows while the weight bytes do not).
+template <int FMT, int NG, int MT>
+__global__ __launch_bounds__(256) void k_gemv_sk(const uint8_t* __restrict__ w, int64_t n, int64_t row_bytes,
+                                                 const float* __restrict__ x, int64_t ldx, int m, float* __restrict__ y,
+                                                 int64_t ldy) {
+    constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
+    static_assert(NG % NW == 0 && (VPL == 8 || VPL == 16), "shape");
+    __shared__ __align__(16) int8_t s_q[MT * NG * 256];
+    __shared__ __align__(16) float s_d[MT * NG * 8];
+    __shared__ __align__(16) int16_t s_s8[MT * NG * 8];
+    __shared__ int s_isum[MT][8][8][NG];  // [input row][weight row][lane k][block]
+    __shared__ int s_msum[MT][8][4][NG];
+    __shared__ float s_dd[MT][8][NG], s_dm[MT][8][NG];
+    const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m0 = (int)blockIdx.y * MT, mc = min(MT, m - m0);
+    constexpr int LPB = 256 / VPL;
+    const int g0 = wave * NB;
+    const int gx = g0 + lane / LPB;  // x block this lane quantises
+    float xv[MT][VPL];
+#pragma unroll
+    for (int r = 0; r < MT; r++)
+        q8k_vpl_load<VPL>(r < mc ? x + (int64_t)(m0 + r) * ldx + (int64_t)gx * 256 : nullptr, xv[r]);
+    const int64_t i = (int64_t)blockIdx.x * 8 + slot;
+    const int64_t ic = i < n ? i : n - 1;
+    const uint8_t* wrow[1] = {w + ic * row_bytes + (int64_t)g0 * WT<FMT>::kBlockBytes};
+    typename WT<FMT>::T wb[1][NB];
+    lanes_load_exact<FMT, 1, NB>(wrow, k, wb);
+    ActView a;
+    a.ng = NG;
+    a.ldq = NG * 256;
+    a.ldd = NG * 8;
+    a.m = MT;
+    a.q = s_q;
+    a.d = s_d;
+    a.s8 = s_s8;
+#pragma unroll
+    for (int r = 0; r < MT; r++) quant_q8k_vpl<VPL>(xv[r], r < mc, r, gx, a);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int g = g0 + b;
+        if constexpr (FMT == kQ4_K) {
+            const Q4Dec dec = q4_decode(wb[0][b], k);
+#pragma unroll
+            for (int r = 0; r < MT; r++) {
+                if (r < mc) {  // uniform
+                    uint32_t av[8];
+                    load_act(a, r, g, k, av);
+                    const float yd = a.d[r * a.ldd + g];
+                    const uint32_t q8s = *(const uint32_t*)(a.s8 + (r * NG + g) * 8 + 2 * (k & 3));
+                    int32_t isum, msum;
+                    float d, dmin;
+                    q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
+                    s_isum[r][slot][k][g] = isum;
+                    if (k < 4) s_msum[r][slot][k][g] = msum;
+                    if (k == 0) {
+                        s_dd[r][slot][g] = d;
+                        s_dm[r][slot][g] = dmin;
+                    }
+                }
+            }
+        } else {
+            const Q6Dec dec = q6_decode(wb[0][b], k);
+#pragma unroll
+            for (int r = 0; r < MT; r++) {
+                if (r < mc) {  // uniform
+                    uint32_t av[8];
+                    load_act(a, r, g, k, av);
+                    const float yd = a.d[r * a.ldd + g];
+                    int32_t isum;
+                    float d;
+                    q6_dot(dec, av, yd, isum, d);
+                    s_isum[r][slot][k][g] = isum;
+                    if (k == 0) s_dd[r][slot][g] = d;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int r = wave; r < mc; r += NW) {
+        float acc = 0.f, accm = 0.f;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            acc = __builtin_fmaf(s_dd[r][slot][g], (float)s_isum[r][slot][k][g], acc);
+            if constexpr (FMT == kQ4_K) accm = __builtin_fmaf(s_dm[r][slot][g], (float)s_msum[r][slot][k & 3][g], accm);
+        }
+        float v = hsum8(acc);
+        if constexpr (FMT == kQ4_K) v = v + hsum4(accm);
+        if (k == 0 && i < n) y[(int64_t)(m0 + r) * ldy + i] = v;
+    }
+}
+
+template <int FMT>
+hipError_t launch_sk2(const WeightView& w, const float* x, int64_t ldx, float* y, int64_t ldy, hipStream_t s) {
+    const dim3 grid((unsigned)((w.rows + 7) / 8), 1);
+    if (w.cols == 2048)
+        hipLaunchKernelGGL((k_gemv_sk<FMT, 8, 2>), grid, dim3(256), 0, s, w.w, w.rows, w.row_bytes, x, ldx, 2, y, ldy);
+    else
+        hipLaunchKernelGGL((k_gemv_sk<FMT, 16, 2>), grid, dim3(256), 0, s, w.w, w.rows, w.row_bytes, x, ldx, 2, y, ldy);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t launch_sk(const WeightView& w, const float* x, float* y, hipStream_t s) {
     const unsigned groups = (unsigned)((w.rows + 7) / 8);
@@ -646,6 +758,8 @@ hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t
                        hipStream_t s) {
     if (!gemv_supported(w, m)) return hipErrorNotSupported;
     if (m == 1 && sk_supported(w)) return w.dtype == kQ4_K ? launch_sk<kQ4_K>(w, x, y, s) : launch_sk<kQ6_K>(w, x, y, s);
+    if (m == 2 && sk_supported(w))
+        return w.dtype == kQ4_K ? launch_sk2<kQ4_K>(w, x, ldx, y, ldy, s) : launch_sk2<kQ6_K>(w, x, ldx, y, ldy, s);
     GemvArgs args;
     args.w = w.w;
     args.n = w.rows;

@@ -164,7 +164,7 @@ def test_large_matrix_rows_bitexact(gpu, oracle, large_matrices, dtype):
         assert_bitexact(got, expected, f"{S.NAMES[dtype]} [{rows}x2048] m={m}")
 
 
-@pytest.mark.parametrize("m", [1, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 8, 16])
 def test_joined_attention_projections_match_separate_calls(gpu, m):
     """q/gate [8192 x 2048], k and v [512 x 2048] joined by rows give bitwise
     the three separate products at decode and verify widths (the
