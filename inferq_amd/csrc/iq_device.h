@@ -36,6 +36,15 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// Bytes of q (each < 16) times s (< 8) byte by byte, as two 16-bit lanes:
+// every product is below 128, so no lane carries into the next byte.
+__device__ __forceinline__ uint32_t bytes_mul_small(uint32_t q, uint32_t s) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 a = __builtin_bit_cast(u16x2, q);
+    const u16x2 b = {(unsigned short)s, (unsigned short)s};
+    return __builtin_bit_cast(uint32_t, a * b);
+}
+
 __device__ __forceinline__ int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }

@@ -28,7 +28,6 @@ typedef int v4i_ml __attribute__((ext_vector_type(4)));
 typedef float v4f_ml __attribute__((ext_vector_type(4)));
 typedef _Float16 v4h_ml __attribute__((ext_vector_type(4)));
 typedef short s16x2_ml __attribute__((ext_vector_type(2)));
-typedef unsigned short u16x2_ml __attribute__((ext_vector_type(2)));
 
 constexpr int kMlCols = 64;  // weight rows per tile (16 per wave)
 constexpr int kMlAS = 272;   // LDS stride of an activation row (256 + pad)
@@ -62,13 +61,6 @@ struct MlStage {
     static constexpr int END = H + (MlFmt<FMT>::kMins ? R * 32 : 0);
 };
 
-// Bytes of q (each < 16) times s (< 8) byte by byte: every product is below
-// 128, so two 16-bit lanes never carry into each other.
-__device__ __forceinline__ uint32_t ml_bytes_mul_small(uint32_t q, uint32_t s) {
-    const u16x2_ml a = __builtin_bit_cast(u16x2_ml, q);
-    const u16x2_ml b = {(unsigned short)s, (unsigned short)s};
-    return __builtin_bit_cast(uint32_t, a * b);
-}
 
 // Four unsigned six-bit values u (bytes) times a signed scale sc, minus
 // 32 sc: p = sc * (u - 32) in -4064..4096, split p = 64 hi + lo; returns the
@@ -245,10 +237,10 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
             if constexpr (FMT == kQ4_K) {
                 const uint32_t qd = *(const uint32_t*)(bcol + 16 + 32 * q + 4 * k);
                 const uint32_t lo = qd & 0x0f0f0f0fu, hi = (qd >> 4) & 0x0f0f0f0fu;
-                w1[0] = ml_bytes_mul_small(lo, s6a >> 3);
-                w1[1] = ml_bytes_mul_small(hi, s6b >> 3);
-                w2[0] = ml_bytes_mul_small(lo, s6a & 7u);
-                w2[1] = ml_bytes_mul_small(hi, s6b & 7u);
+                w1[0] = bytes_mul_small(lo, s6a >> 3);
+                w1[1] = bytes_mul_small(hi, s6b >> 3);
+                w2[0] = bytes_mul_small(lo, s6a & 7u);
+                w2[1] = bytes_mul_small(hi, s6b & 7u);
                 mul = 8;
             } else {
                 const int hk = k >= 4;

@@ -46,7 +46,7 @@ struct MoeParams {
     // MFMA (prefill) path
     _Float16* xhs = nullptr;        // [M][H/256][16] 16-value sums of quantised x
     _Float16* ahs = nullptr;        // [P][I/256][16] the same of quantised act
-    int32_t* chunk_group = nullptr;  // [max_chunks] group of each 32-row chunk
+    int32_t* chunk_group = nullptr;  // [max_chunks] group of each chunk of rows
     int32_t* chunk_r0 = nullptr;     // [max_chunks] first row of the chunk in its group
     int max_chunks = 0;
 };
@@ -59,7 +59,7 @@ hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStr
 bool moep_supported(const MoeParams& p, int gate_dtype, int down_dtype);
 hipError_t launch_moe_prefill(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
                               hipEvent_t const* events);
-// Upper bound of the 32-row chunks a call of M tokens makes.
+// Upper bound of the row chunks a call of M tokens makes.
 int moep_max_chunks(int64_t M, int64_t K, int64_t E);
 // One launch of a call already made with these parameters (stage 0 routing
 // of the grouped path, 1 gate/up, 2 down).

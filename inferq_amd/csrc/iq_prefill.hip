@@ -1,21 +1,12 @@
 // iq_prefill.hip -- y = x . W^T for Q4_K weights at many input rows
 // (prefill), on int8 MFMA (v_mfma_i32_16x16x64_i8).
 //
-// Arithmetic.  Per block b of 256 weights, the reference's exact integers
-// are isum = sum_j sc_j * sum_{e in sub-block j} q_e a_e and msum =
-// sum_j m_j * bsum32_j (src/qgemm.rs:175-245; sc_j, m_j six-bit, q_e four-bit,
-// a_e the Q8K int8 activations).  A six-bit scale times a four-bit quant
-// does not fit int8, so the scale is split, sc = 8 sc_hi + sc_lo with both
-// parts in 0..7: the MFMA streams w1 = sc_hi q and w2 = sc_lo q (bytes
-// <= 105) give isum = 8 acc1 + acc2 exactly (each weight byte carries its
-// sub-block's scale, so a K step may span sub-blocks).  msum comes from
-// one f16 MFMA per block over the 16 bsums of 16 values (|bsum16| <= 2048 and
-// the mins are exact in f16; products and sums stay below 2^24 in the f32
-// accumulator).  Every per-block integer is therefore the reference's, bit
-// for bit.  The f32 combination y += dx_b (dw_b isum_b - dmin_b msum_b) runs
-// in a different order than the reference's per-lane FMA chains: results
-// agree within the path's 1e-4 normwise tolerance, not bitwise (this kernel
-// serves 64+ input rows; fewer rows keep the bit-exact kernels).
+// Arithmetic (iq_pf_q4k.h).  Every per-block integer is the reference's
+// (src/qgemm.rs:175-245), bit for bit; the f32 combination
+// y += dx_b (dw_b isum_b - dmin_b msum_b) runs in a different order than the
+// reference's per-lane FMA chains: results agree within the path's 1e-4
+// normwise tolerance, not bitwise (this kernel serves 64+ input rows; fewer
+// rows keep the bit-exact kernels).
 //
 // Tiling.  A workgroup (8 waves, two per SIMD) owns 64 input rows and 128
 // output columns; each wave all 64 rows of 16 columns as four 16 x 16 tiles
@@ -27,25 +18,16 @@
 // multiply per dword and stream).  Narrow outputs are split over K, with
 // partial tiles summed in a fixed order by a second pass.
 #include "iq_lanes.h"
+#include "iq_pf_q4k.h"
 #include "iq_quant.h"
 
 namespace iq {
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kPfRows = 64;   // input rows per workgroup
-constexpr int kPfCols = 128;  // output columns per workgroup (32 per wave)
-
-// Bytes of q (each < 16) times s (< 8) byte by byte: every product is below
-// 128, so two 16-bit lanes never carry into each other.
-__device__ __forceinline__ uint32_t bytes_mul_small(uint32_t q, uint32_t s) {
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    const u16x2 a = __builtin_bit_cast(u16x2, q);
-    const u16x2 b = {(unsigned short)s, (unsigned short)s};
-    return __builtin_bit_cast(uint32_t, a * b);
-}
+constexpr int kPfCols = 128;  // output columns per workgroup (16 per wave)
 
 // ---- activation quantisation --------------------------------------------------
 // Q8K (bit-exact from_float) into the layouts the MFMA kernel reads:
@@ -83,8 +65,6 @@ struct PrefillArgs {
     int32_t* dbg_msum;
 };
 
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int kPfThreads = 512;  // 8 waves of 16 columns each
 
@@ -190,57 +170,16 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
         // itself the scheduler sinks them next to the stores that wait on them)
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* bcol = S + kStB + (16 * wave + jj) * kBS;
-        const u32x4a16 hdr = *(const u32x4a16*)bcol;
-        const float dw = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
-        const Q4Scales sc = q4_scales(hdr.y, hdr.z, hdr.w);
-        v4i acc1[4], acc2[4];
-#pragma unroll
-        for (int st4 = 0; st4 < 4; st4++) {  // K step: values 64 st4 .. +63
-            const int shn = (g >> 1) * 4;
-            // sub-block 2 st4 + (g >> 1): byte (2 st4 + (g >> 1)) & 3 of the low or high scale word
-            const uint32_t s6 = byte_of(st4 < 2 ? sc.sc_lo : sc.sc_hi, (2 * st4 + (g >> 1)) & 3);
-            const uint32_t hi = s6 >> 3, lo = s6 & 7u;
-            const u32x4a16 raw = *(const u32x4a16*)(bcol + 16 + 32 * st4 + 16 * (g & 1));
-            const uint32_t qv[4] = {(raw.x >> shn) & 0x0f0f0f0fu, (raw.y >> shn) & 0x0f0f0f0fu,
-                                    (raw.z >> shn) & 0x0f0f0f0fu, (raw.w >> shn) & 0x0f0f0f0fu};
-            const v4i w1 = {(int)bytes_mul_small(qv[0], hi), (int)bytes_mul_small(qv[1], hi),
-                            (int)bytes_mul_small(qv[2], hi), (int)bytes_mul_small(qv[3], hi)};
-            const v4i w2 = {(int)bytes_mul_small(qv[0], lo), (int)bytes_mul_small(qv[1], lo),
-                            (int)bytes_mul_small(qv[2], lo), (int)bytes_mul_small(qv[3], lo)};
-#pragma unroll
-            for (int rt = 0; rt < 4; rt++) {
-                const v4i a = *(const v4i*)(S + kStA + (16 * rt + jj) * kAS + 64 * st4 + 16 * g);
-                const v4i z = {};
-                acc1[rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w1, st4 == 0 ? z : acc1[rt], 0, 0, 0);
-                acc2[rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w2, st4 == 0 ? z : acc2[rt], 0, 0, 0);
-            }
-        }
-
-        // mins: msum = sum_t m_{t/2} bsum16_t (K = 16; lane group g: t = 4g..4g+3)
-        const uint32_t mw = g < 2 ? sc.mn_lo : sc.mn_hi;  // m_{2g}, m_{2g+1}: bytes 2 (g & 1) + 0, 1
-        const _Float16 mA = (_Float16)(float)byte_of(mw, 2 * (g & 1));
-        const _Float16 mB = (_Float16)(float)byte_of(mw, 2 * (g & 1) + 1);
-        const v4h bm = {mA, mA, mB, mB};
-#pragma unroll
-        for (int rt = 0; rt < 4; rt++) {
-            const v4h am = *(const v4h*)(S + kStH + (16 * rt + jj) * 32 + 8 * g);
-            const f32x4 dx = *(const f32x4*)(S + kStD + 4 * (16 * rt + 4 * g));
-            const v4f z = {};
-            const v4f msum = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int32_t isum = 8 * acc1[rt][r] + acc2[rt][r];
-                const float t = __builtin_fmaf(-dmin, msum[r], dw * (float)isum);
-                out[rt][r] = __builtin_fmaf(dx[r], t, out[rt][r]);
-                if constexpr (DBG) {
-                    const int64_t row = row0 + 16 * rt + 4 * g + r, gc = n0 + 16 * wave + jj;
-                    if (row < p.m && gc < p.n) {
-                        p.dbg_isum[(row * p.n + gc) * p.nb + b] = isum;
-                        p.dbg_msum[(row * p.n + gc) * p.nb + b] = (int32_t)msum[r];
-                    }
-                }
-            }
-        }
+        pf_q4k_block<4, kAS>(S + kStA, bcol, S + kStH, (const float*)(S + kStD), g, jj, out,
+                             [&](int rt, int r, int32_t isum, float msum) {
+                                 if constexpr (DBG) {
+                                     const int64_t row = row0 + 16 * rt + 4 * g + r, gc = n0 + 16 * wave + jj;
+                                     if (row < p.m && gc < p.n) {
+                                         p.dbg_isum[(row * p.n + gc) * p.nb + b] = isum;
+                                         p.dbg_msum[(row * p.n + gc) * p.nb + b] = (int32_t)msum;
+                                     }
+                                 }
+                             });
         // the next block's loads have had this whole block to land
         __builtin_amdgcn_sched_barrier(0);
         park(st[(b - b0 + 1) & 1]);
