@@ -1,7 +1,10 @@
 // iq_pf_q4k.h -- one Q4_K block of a wave's prefill tile on int8 MFMA:
-// per-block integers exact, f32 combination in tile order.  Shared by the
-// dense prefill (iq_prefill.hip) and the grouped MoE prefill
-// (iq_moe_prefill.hip).
+// per-block integers exact, f32 combination in tile order (the dense
+// prefill, iq_prefill.hip).  Not for products whose outputs are quantised
+// again (the MoE gate/up, whose SwiGLU rows become Q8K for down): a last-ulp
+// difference there can move a value across a rounding boundary of the
+// quantiser, and one changed int8 activation shifts the down output by
+// about 1e-4 of its norm.
 //
 // Per block of 256 weights the reference's integers are isum = sum_j sc_j *
 // sum_{e in sub-block j} q_e a_e and msum = sum_j m_j * bsum32_j
