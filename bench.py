@@ -349,62 +349,65 @@ def prefill(args, hip, stream, device):
 
 
 def decode_sweep(args, hip, device, layers):
-    """the quantized matmuls of one decode step over the
-    resident layers -- per layer the attention projections q/gate
-    [8192 x 2048], k and v [512 x 2048], o [2048 x 4096] (Q4_K) and the MoE
-    layer -- then the LM head [248320 x 2048] Q6_K, at M = 1 and M = 8 rows.
-    Every call of a step is launched in order on one stream (graph replay);
-    reported: matmul time per step, tokens per second of matmul time, and
-    the step's algorithmic HBM bytes over that time.  The *_qkv_rows lines
-    run the same step with q/gate, k and v of each layer joined into one
-    [9216 x 2048] matrix (QuantizedMatrix::concatenate_rows,
-    src/gguf.rs:379-404, as the reference joins DeltaNet's qkvz): one launch
-    instead of three, the same bytes and bitwise the same outputs."""
+    """the quantized matmuls of one decode step of the
+    40-layer Qwen3.6-35B-A3B shape (src/config.rs:235-246): layers l with
+    (l + 1) % 4 == 0 are full attention -- q/gate [8192 x 2048], k and v
+    [512 x 2048], o [2048 x 4096] (src/qwen/quantized_attention.rs:428-442,
+    503) -- and the other 30 are DeltaNet -- qkvz [12288 x 2048] (qkv and z
+    joined by rows, as the reference loads them), ba [64 x 2048], out
+    [2048 x 4096] (src/qwen/quantized_deltanet.rs:419-434, 537-563, 699) --
+    all Q4_K, each followed by its MoE layer; then the LM head [248320 x
+    2048] Q6_K; at M = 1 and M = 8 rows.  Every call of a step is launched
+    in order on one stream (graph replay); reported: matmul time per step,
+    tokens per second of matmul time, and the step's algorithmic HBM bytes
+    over that time.  The *_qkv_rows lines also join the attention layers'
+    q/gate, k and v into one [9216 x 2048] matrix (QuantizedMatrix::
+    concatenate_rows, src/gguf.rs:379-404): one launch instead of three, the
+    same bytes and bitwise the same outputs."""
     import torch
 
     from inferq_amd import qgemm, synth
 
     n = len(layers)
-    shapes = ((8192, 2048), (512, 2048), (512, 2048), (2048, 4096))
-    dense = [[qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, r, c, device, 5000 + 10 * li + j),
-                                         synth.Q4_K, r, c) for j, (r, c) in enumerate(shapes)] for li in range(n)]
+    attn = ((8192, 2048), (512, 2048), (512, 2048), (2048, 4096))
+    delta = ((12288, 2048), (64, 2048), (2048, 4096))
+    is_attn = [(li + 1) % 4 == 0 for li in range(n)]
+
+    def mat(r, c, seed):
+        return qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, r, c, device, seed), synth.Q4_K, r, c)
+
+    dense = [[mat(r, c, 5000 + 10 * li + j) for j, (r, c) in enumerate(attn if is_attn[li] else delta)]
+             for li in range(n)]
+    qkv = [d[0].concatenate_rows(d[1]).concatenate_rows(d[2]) if is_attn[li] else None for li, d in enumerate(dense)]
     lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 6000), synth.Q6_K,
                                     248320, 2048)
-    dense_bytes = n * sum(m_.storage_bytes() for m_ in dense[0])
-    qkv = [d[0].concatenate_rows(d[1]).concatenate_rows(d[2]) for d in dense]
+    dense_bytes = sum(m_.storage_bytes() for d in dense for m_ in d)
     gu, dn = expert_bytes()
     g = torch.Generator(device=device)
     g.manual_seed(args.seed + 9)
-    res = {"layers": n}
+    res = {"layers": n, "attention_layers": sum(is_attn), "deltanet_layers": n - sum(is_attn)}
     for m in (1, 8):
-        x2 = torch.randn(m, 2048, device=device, generator=g)
-        x4 = torch.randn(m, 4096, device=device, generator=g)
+        xin = {c: torch.randn(m, c, device=device, generator=g) for c in (2048, 4096)}
         lg = torch.randn(n, m, E, device=device, generator=g)
-        ys = [torch.empty(m, r, device=device) for r, _ in shapes]
-        yqkv = torch.empty(m, 9216, device=device)
+        ys = {r: torch.empty(m, r, device=device) for r in {r for r, _ in attn + delta} | {9216}}
         out = torch.empty(m, H, device=device)
         ylm = torch.empty(m, 248320, device=device)
 
-        def step(i):
+        def step(i, joined=False):
             for li in range(n):
                 mats = dense[li]
-                mats[0].forward_into(x2, ys[0])
-                mats[1].forward_into(x2, ys[1])
-                mats[2].forward_into(x2, ys[2])
-                mats[3].forward_into(x4, ys[3])
-                layers[li][0].forward_into(x2, lg[li], out)
-            lm.forward_into(x2, ylm)
-
-        def step_qkv(i):
-            for li in range(n):
-                qkv[li].forward_into(x2, yqkv)
-                dense[li][3].forward_into(x4, ys[3])
-                layers[li][0].forward_into(x2, lg[li], out)
-            lm.forward_into(x2, ylm)
+                if is_attn[li] and joined:
+                    qkv[li].forward_into(xin[2048], ys[9216])
+                    mats[3].forward_into(xin[4096], ys[2048])
+                else:
+                    for mt in mats:
+                        mt.forward_into(xin[mt.shape()[1]], ys[mt.shape()[0]])
+                layers[li][0].forward_into(xin[2048], lg[li], out)
+            lm.forward_into(xin[2048], ylm)
 
         uniq = float(np.mean([len(torch.unique(torch.topk(lg[li], TOPK, dim=1).indices)) for li in range(n)]))
         total = n * (uniq + 1) * (gu + dn) + dense_bytes + lm.storage_bytes()
-        for name, fn in ((f"m{m}", step), (f"m{m}_qkv_rows", step_qkv)):
+        for name, fn in ((f"m{m}", step), (f"m{m}_qkv_rows", lambda i: step(i, True))):
             ms = time_graph(fn, 2, hip, warmup=1)
             res[name] = {"us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(m / (ms * 1e-3), 1),
                          "unique_experts_per_layer": round(uniq, 1), "GB_per_step": round(total / 1e9, 3),
