@@ -710,6 +710,20 @@ hipError_t launch_sk2(const WeightView& w, const float* x, int64_t ldx, float* y
     return hipGetLastError();
 }
 
+// m single-row tiles of the split kernel, one per grid row.
+template <int FMT>
+hipError_t launch_sk_rows(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                          hipStream_t s) {
+    const dim3 grid((unsigned)((w.rows + 7) / 8), (unsigned)m);
+    if (w.cols == 2048)
+        hipLaunchKernelGGL((k_gemv_sk<FMT, 8, 1>), grid, dim3(256), 0, s, w.w, w.rows, w.row_bytes, x, ldx, (int)m, y,
+                           ldy);
+    else
+        hipLaunchKernelGGL((k_gemv_sk<FMT, 16, 1>), grid, dim3(256), 0, s, w.w, w.rows, w.row_bytes, x, ldx, (int)m,
+                           y, ldy);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t launch_sk(const WeightView& w, const float* x, float* y, hipStream_t s) {
     const unsigned groups = (unsigned)((w.rows + 7) / 8);
@@ -760,6 +774,18 @@ hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t
     if (m == 1 && sk_supported(w)) return w.dtype == kQ4_K ? launch_sk<kQ4_K>(w, x, y, s) : launch_sk<kQ6_K>(w, x, y, s);
     if (m == 2 && sk_supported(w))
         return w.dtype == kQ4_K ? launch_sk2<kQ4_K>(w, x, ldx, y, ldy, s) : launch_sk2<kQ6_K>(w, x, ldx, y, ldy, s);
+    // Three to eight rows as single-row tiles of the split kernel while the
+    // tiles total at most 4096 workgroups at width 2048 (768 at width 4096,
+    // whose tiles quantise and chain twice the blocks); past that the
+    // row-tiled kernel, which decodes each weight once per tile of rows,
+    // is faster.  k/v [512 x 2048] at 4 rows 6.1 -> 3.8 us, at 8 rows 6.1 ->
+    // 4.1 us; q/gate [8192 x 2048] at 4 rows 13.4 -> 11.7 us (at 5 rows 13.1
+    // against 15.6); [4096 x 2048] at 6 rows 11.3 -> 9.6 us; o [2048 x 4096]
+    // at 3 rows 7.7 -> 7.1 us.
+    const int64_t sk_tiles = (w.rows + 7) / 8 * m;
+    if (m <= 8 && sk_supported(w) && sk_tiles <= (w.cols == 2048 ? 4096 : 768))
+        return w.dtype == kQ4_K ? launch_sk_rows<kQ4_K>(w, x, ldx, m, y, ldy, s)
+                                : launch_sk_rows<kQ6_K>(w, x, ldx, m, y, ldy, s);
     GemvArgs args;
     args.w = w.w;
     args.n = w.rows;
