@@ -421,6 +421,114 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
     if (k == 0 && ok) p.act[((int64_t)t * nslots + sidx) * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
 }
 
+// The one-token form on eight waves: gate on waves 0-3 and up on waves 4-7,
+// each wave a quarter of the blocks of one matrix, so each wave forms half
+// the per-block integers of the four-wave kernel.  Wave 0 alone runs the
+// top-k and hands the expert id over in LDS (eight waves each repeating it
+// were slower than four); waves 0-3 quantise x for all eight.  Grid as
+// k_moe1_gate_up<GFMT, NG, false>.
+template <int GFMT, int NG>
+__global__ __launch_bounds__(512) void k_moe1_gate_up8(MoeParams p) {
+    constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
+    static_assert(NG % NW == 0 && (VPL == 8 || VPL == 16 || VPL == 32), "shape");
+    __shared__ __align__(16) int8_t s_q[NG * 256];
+    __shared__ __align__(16) float s_d[NG * 8];
+    __shared__ __align__(16) int16_t s_s8[NG * 8];
+    __shared__ int s_isum[2][8][8][NG];  // [gate/up][row][lane k][block]
+    __shared__ int s_msum[2][8][4][NG];
+    __shared__ float s_dd[2][8][NG], s_dm[2][8][NG];
+    __shared__ int s_e;
+    const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int quarter = wave & 3, r = wave >> 2;  // r: 0 gate, 1 up
+    const int K = (int)p.K, t = blockIdx.z;
+    const int nslots = K + (p.sdown_w ? 1 : 0);
+    if (blockIdx.y == 0) {
+        if (blockIdx.x == 0) moe1_route(p, wave, t);
+        return;
+    }
+    const int sidx = (int)blockIdx.y - 1;
+    constexpr int LPB = 256 / VPL;
+    const int g0 = quarter * NB;
+    const int gx = g0 + lane / LPB;  // x block this lane quantises (waves 0-3)
+    float xv[VPL];
+    if (r == 0) q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
+    int e = (int)p.E;
+    if (wave == 0 && sidx < K) {
+        float lv[kRoutePer];
+        route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
+        int sel[kMoe1MaxSlots];
+        route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
+        if (lane == 0) s_e = sel[sidx];
+    }
+    lds_barrier();
+    if (sidx < K) e = __builtin_amdgcn_readfirstlane(s_e);
+    const bool shared = sidx >= K;
+    const uint8_t* mb = r == 0 ? (shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes)
+                               : (shared ? p.sup_w : p.up + (int64_t)e * p.g_exp_bytes);
+    const int64_t i = (int64_t)blockIdx.x * 8 + slot;
+    const bool ok = i < p.I;
+    const int64_t ic = ok ? i : p.I - 1;
+    const uint8_t* wrow[1] = {mb + ic * p.g_row_bytes + (int64_t)g0 * WT<GFMT>::kBlockBytes};
+    typename WT<GFMT>::T w[1][NB];
+    lanes_load_exact<GFMT, 1, NB>(wrow, k, w);
+    ActView a;
+    a.ng = NG;
+    a.ldq = NG * 256;
+    a.ldd = NG * 8;
+    a.m = 1;
+    a.q = s_q;
+    a.d = s_d;
+    a.s8 = s_s8;
+    if (r == 0) quant_q8k_vpl<VPL>(xv, true, 0, gx, a);
+    lds_barrier();  // the quantised x, from waves 0-3, for all eight
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int g = g0 + b;
+        uint32_t av[8];
+        load_act(a, 0, g, k, av);
+        const float yd = a.d[g];
+        if constexpr (GFMT == kQ4_K) {
+            const Q4Dec dec = q4_decode(w[0][b], k);
+            const uint32_t q8s = *(const uint32_t*)(a.s8 + g * 8 + 2 * (k & 3));
+            int32_t isum, msum;
+            float d, dmin;
+            q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
+            s_isum[r][slot][k][g] = isum;
+            if (k < 4) s_msum[r][slot][k][g] = msum;
+            if (k == 0) {
+                s_dd[r][slot][g] = d;
+                s_dm[r][slot][g] = dmin;
+            }
+        } else {
+            const Q6Dec dec = q6_decode(w[0][b], k);
+            int32_t isum;
+            float d;
+            q6_dot(dec, av, yd, isum, d);
+            s_isum[r][slot][k][g] = isum;
+            if (k == 0) s_dd[r][slot][g] = d;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float o[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; rr++) {
+        float acc = 0.f, accm = 0.f;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            acc = __builtin_fmaf(s_dd[rr][slot][g], (float)s_isum[rr][slot][k][g], acc);
+            if constexpr (GFMT == kQ4_K)
+                accm = __builtin_fmaf(s_dm[rr][slot][g], (float)s_msum[rr][slot][k & 3][g], accm);
+        }
+        float v = hsum8(acc);
+        if constexpr (GFMT == kQ4_K) v = v + hsum4(accm);
+        o[rr] = v;
+    }
+    // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
+    if (k == 0 && ok) p.act[((int64_t)t * nslots + sidx) * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
+}
+
 // Routing of every token of a call (grid M, two waves each).
 __global__ __launch_bounds__(128) void k_moe1_route(MoeParams p) { moe1_route(p, (int)(threadIdx.x >> 6), blockIdx.x); }
 
@@ -505,6 +613,11 @@ hipError_t launch_moe1_stage(const MoeParams& p, int stage, hipStream_t s) {
         if (p.M >= kMoeRouteLaunchMin) {
             hipLaunchKernelGGL(k_moe1_route, dim3(m), dim3(128), 0, s, p);
             hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8, true>), dim3(rows_i, nslots, m), dim3(256), 0, s, p);
+        } else if (m == 1) {
+            // one token: eight waves per workgroup halve each wave's block
+            // products (layer 13.1 -> 12.8 us); wider calls fill the GPU
+            // with workgroups and keep four waves (8 tokens: 49 against 58 us)
+            hipLaunchKernelGGL((k_moe1_gate_up8<GFMT, 8>), dim3(rows_i, nslots + 1, m), dim3(512), 0, s, p);
         } else {
             hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8, false>), dim3(rows_i, nslots + 1, m), dim3(256), 0, s, p);
         }
