@@ -341,14 +341,19 @@ __global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
         if (sidx < K) e = __builtin_amdgcn_readfirstlane(p.experts[t * K + sidx]);
         q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
     } else {
-        float lv[kRoutePer];
-        route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
+        // wave 0 routes and hands the id over in LDS: the other waves keep
+        // their SIMDs free for the workgroups around them
+        __shared__ int s_e4;
         q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
-        if (sidx < K) {
+        if (wave == 0 && sidx < K) {
+            float lv[kRoutePer];
+            route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
             int sel[kMoe1MaxSlots];
             route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
-            e = sel[sidx];
+            if (lane == 0) s_e4 = sel[sidx];
         }
+        lds_barrier();
+        if (sidx < K) e = __builtin_amdgcn_readfirstlane(s_e4);
     }
     const bool shared = sidx >= K;
     const uint8_t* gb = shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes;
