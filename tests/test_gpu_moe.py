@@ -145,6 +145,35 @@ def test_prefill_width_moe_matches_oracle(gpu, oracle, qwen_layer, m):
     assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, f"prefill-width MoE m={m}")
 
 
+@pytest.fixture(scope="module")
+def qwen_layer_routed_only():
+    """The config-2 shape without a shared expert (32 experts)."""
+    return S.random_moe_layer(2048, 512, 32, Q4, Q6, np.random.default_rng(2025), shared=False)
+
+
+@pytest.mark.parametrize("top_k", [1, 8])
+@pytest.mark.parametrize("m", [1, 4, 64])
+def test_routed_only_layer_matches_oracle(gpu, oracle, qwen_layer_routed_only, top_k, m):
+    """No shared expert (no shared slot in the token-major grids, no shared
+    rows in the grouped path) at top-1 and top-8: routes equal, outputs
+    within the bar, multi-token calls equal one-token calls."""
+    layer = qwen_layer_routed_only
+    moe, _ = _device_layer(layer, top_k, gpu)
+    rng = np.random.default_rng(900 + 10 * m + top_k)
+    x = S.normal((m, 2048), rng)
+    logits = S.normal((m, 32), rng)
+    xg, lg = torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu)
+    out = moe.forward(xg, lg)
+    ref, ref_e, _ = oracle.moe_forward(_oracle_layer(layer, top_k), x, logits, mode=1, impl=_impl(oracle),
+                                       nthreads=8)
+    assert [r.experts for r in out.routes] == ref_e.tolist()
+    got = out.hidden.cpu().numpy()
+    assert_close_normwise(got, ref, 1e-4, f"routed-only MoE top-{top_k} m={m}")
+    if m > 1:
+        singles = np.concatenate([moe.forward(xg[i:i + 1], lg[i:i + 1]).hidden.cpu().numpy() for i in range(m)])
+        assert_bitexact(got, singles, f"routed-only grouped vs per-token m={m}")
+
+
 @pytest.mark.parametrize("m", [32, 64])
 def test_skewed_grouped_call_equals_single_token_calls(gpu, qwen_layer, m):
     """m rows with skewed routing in one call (token-major at 32, grouped by
