@@ -732,15 +732,13 @@ hipError_t launch_sk(const WeightView& w, const float* x, float* y, hipStream_t 
     return hipGetLastError();
 }
 
-// One-row calls on K-quant matrices of width 2048 or 4096 up to
-// IQ_SK_MAX_BYTES (larger ones stream better through k_gemv); Q6_K rows of
-// an even block count keep the burst's dword alignment.
-#ifndef IQ_SK_MAX_BYTES
-#define IQ_SK_MAX_BYTES (64ll << 20)
-#endif
+// The split kernels take K-quant matrices of width 2048 or 4096 up to
+// kSkMaxBytes (larger ones stream better through k_gemv); Q6_K rows of 8 or
+// 16 blocks keep the burst's dword alignment.
+constexpr int64_t kSkMaxBytes = (int64_t)64 << 20;
 bool sk_supported(const WeightView& w) {
     if (w.cols != 2048 && w.cols != 4096) return false;
-    if (w.rows * w.row_bytes > (int64_t)IQ_SK_MAX_BYTES) return false;
+    if (w.rows * w.row_bytes > kSkMaxBytes) return false;
     if (w.dtype == kQ4_K) return ((uintptr_t)w.w & 15) == 0;
     if (w.dtype == kQ6_K) return ((uintptr_t)w.w & 3) == 0;
     return false;
