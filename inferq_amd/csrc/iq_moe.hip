@@ -277,7 +277,10 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeParams p) {
 // pass and have far less weight traffic in flight per CU.
 
 constexpr int kMoe1MaxSlots = 12;  // top-k routes plus the shared expert
-constexpr int kMoeTokenMajorMax = 48;  // widest call served token-major
+// widest call served token-major: since the grouped MFMA path took 16-row
+// chunks it is faster from about 32 tokens (32: 125 against 137 us, 48: 148
+// against 195 us in graph replays; 24: 105-108 either way)
+constexpr int kMoeTokenMajorMax = 28;
 constexpr int kMoeRouteLaunchMin = 12;  // calls this wide route in a launch of their own
 
 // Routing workgroup of token t's gate/up slice: wave 0 routes the token

@@ -100,7 +100,7 @@ def format_layers():
 @pytest.mark.parametrize("fmts", _FORMAT_PAIRS, ids=lambda f: f"{_NAMES[f[0]]}-{_NAMES[f[1]]}")
 def test_format_pairs_match_oracle(gpu, oracle, format_layers, fmts, m):
     """Every gate/down format pair at one row, a verify width and a prefill
-    width (K-quant pairs take the token-major kernels up to 48 rows and the
+    width (K-quant pairs take the token-major kernels up to 28 rows and the
     grouped MFMA kernels past that; Q8_0 the generic grouped path); a
     multi-row call equals one-row calls, bitwise."""
     layer = format_layers[fmts]
@@ -128,11 +128,11 @@ def _dirichlet_logits(m, n_experts, rng, alpha=0.3):
     return (S.normal((m, n_experts), rng) + np.log(np.maximum(p, 1e-30))).astype(np.float32)
 
 
-@pytest.mark.parametrize("m", [17, 48, 49, 256])
+@pytest.mark.parametrize("m", [17, 28, 29, 48, 256])
 def test_prefill_width_moe_matches_oracle(gpu, oracle, qwen_layer, m):
     """Wide calls with skewed routing (large groups on a few experts, most
-    experts idle): the widest token-major calls (17, 48 rows), the narrowest
-    grouped MFMA call (49) and the prefill width of 256."""
+    experts idle): token-major calls (17, and 28, the widest), the narrowest
+    grouped MFMA call (29), 48 and the prefill width of 256."""
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     rng = np.random.default_rng(300 + m)
     x = S.normal((m, 2048), rng)
@@ -174,9 +174,9 @@ def test_routed_only_layer_matches_oracle(gpu, oracle, qwen_layer_routed_only, t
         assert_bitexact(got, singles, f"routed-only grouped vs per-token m={m}")
 
 
-@pytest.mark.parametrize("m", [32, 64])
+@pytest.mark.parametrize("m", [24, 64])
 def test_skewed_grouped_call_equals_single_token_calls(gpu, qwen_layer, m):
-    """m rows with skewed routing in one call (token-major at 32, grouped by
+    """m rows with skewed routing in one call (token-major at 24, grouped by
     expert at 64) equal m one-row calls."""
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     rng = np.random.default_rng(98)
