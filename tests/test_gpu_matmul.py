@@ -185,6 +185,19 @@ def test_host_entry_matches_device_entry(gpu, oracle):
     assert_bitexact(mat.forward_host(x), oracle.matmul(Q4, w, 128, 1024, x), "host entry")
 
 
+def test_empty_inputs_give_empty_outputs(gpu):
+    """Zero input rows (src/gguf.rs:433-456 with input_rows == 0): an empty
+    result of the right shape, and no launch."""
+    rng = np.random.default_rng(8)
+    mat = Q.QuantizedMatrix.upload(S.random_matrix(Q4, 24, 512, rng), Q4, 24, 512)
+    assert mat.forward(torch.zeros(0, 512, device=gpu)).shape == (0, 24)
+    assert mat.forward(torch.zeros(3, 0, 512, device=gpu)).shape == (3, 0, 24)
+    assert mat.forward_rows(torch.zeros(0, device=gpu), 0).numel() == 0
+    x = S.normal((2, 512), rng)
+    y = mat.forward(torch.from_numpy(x).to(gpu))  # the library still works after the empty calls
+    assert_bitexact(y.cpu().numpy(), mat.forward_host(x), "after empty calls")
+
+
 def test_call_time_errors(gpu):
     mat = Q.QuantizedMatrix.upload(np.zeros(144, np.uint8), Q4, 1, 256)
     with pytest.raises(Q.QgemmError, match="final dimension 128, expected 256"):

@@ -221,6 +221,20 @@ def test_reference_routing_case(gpu, oracle):
     assert_bitexact(grouped.hidden.cpu().numpy(), np.repeat(h, 3, axis=0), "grouped vs token-major")
 
 
+def test_empty_token_batch(gpu, oracle):
+    """Zero tokens: an empty output with no routes, and the next call is
+    unaffected."""
+    rng = np.random.default_rng(2)
+    layer = S.random_moe_layer(256, 256, 8, Q4, Q6, rng, shared=True)
+    moe, _ = _device_layer(layer, 2, gpu)
+    out = moe.forward(torch.zeros(0, 256, device=gpu), torch.zeros(0, 8, device=gpu))
+    assert out.hidden.shape == (0, 256) and out.routes == []
+    x, logits = S.normal((2, 256), rng), S.normal((2, 8), rng)
+    got = moe.forward(torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu))
+    ref, _, _ = oracle.moe_forward(_oracle_layer(layer, 2), x, logits, mode=0, impl=_impl(oracle))
+    assert_close_normwise(got.hidden.cpu().numpy(), ref, 1e-4, "MoE after an empty call")
+
+
 def test_moe_load_time_errors(gpu):
     from inferq_amd import QgemmError
 
