@@ -455,7 +455,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         log(f"bench.py: --gpus {args.gpus} is not supported: this build measures the hot path on one GPU "
-            "(the multi-GPU split is a design in DESIGN.md, not implemented).")
+            "(splitting experts and LM-head rows across GPUs is designed, not implemented).")
         sys.exit(2)
 
     import torch
