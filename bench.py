@@ -326,12 +326,15 @@ def secondary(args, hip, stream, device, layers):
 
 def prefill(args, hip, stream, device):
     """BASELINE configs[3], dense part: Q4_K [256 x 2048] -> 8192 and
-    [256 x 4096] -> 2048 on the int8-MFMA path (activation quantisation,
-    MFMA kernel and, for the narrow output, the split-K reduction all inside
-    the timed call).  TOPS = 2 M N K / time; peak = 5.0 POPS dense int8."""
+    [256 x 4096] -> 2048 on int8 MFMA (activation quantisation, MFMA kernel
+    and, for the narrow output, the split-K reduction all inside the timed
+    call), on both MFMA paths: the dispatch's exact lane order (bitwise the
+    reference) and the prefill tiles a caller requests explicitly (tile
+    order, within 1e-4).  TOPS = 2 M N K / time; peak = 5.0 POPS dense
+    int8."""
     import torch
 
-    from inferq_amd import qgemm, synth
+    from inferq_amd import _lib, qgemm, synth
 
     res = {}
     for n, k in ((8192, 2048), (2048, 4096)):
@@ -340,10 +343,11 @@ def prefill(args, hip, stream, device):
                                            n, k) for c in range(copies)]
         x = torch.randn(256, k, device=device)
         y = torch.empty(256, n, device=device)
-        ms = time_graph(lambda i: mats[i % copies].forward_into(x, y), max(20, args.steps // 4), hip)
-        tops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
-        res[f"q4k_256x{k}_to_{n}"] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
-                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        for label, path in (("tiles", _lib.PATH_PREFILL_TILES), ("exact", _lib.PATH_AUTO)):
+            ms = time_graph(lambda i: mats[i % copies].forward_into(x, y, path), max(20, args.steps // 4), hip)
+            tops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
+            res[f"q4k_256x{k}_to_{n}_{label}"] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
+                                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         del mats
     return res
 

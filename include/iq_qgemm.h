@@ -15,7 +15,9 @@
  *   - Every function returns IQ_OK (0) or a negative IQ_ERR_* code;
  *     iq_last_error() returns this thread's message for the last failure.
  *   - Results are deterministic and bit-identical to the reference's CPU
- *     kernels for the same inputs, whatever the row count.
+ *     kernels for the same inputs, whatever the row count, on every entry
+ *     except iq_matmul_via(..., IQ_PATH_PREFILL_TILES, ...), which a caller
+ *     must request explicitly (its f32 order differs; within 1e-4).
  *   - stream is a hipStream_t (NULL = the default stream).
  */
 #ifndef IQ_QGEMM_H
@@ -39,6 +41,23 @@ enum iq_status {
     IQ_ERR_OOM = -4,     /* device allocation failed */
     IQ_ERR_HIP = -5,     /* HIP runtime error (launch, copy, no device) */
     IQ_ERR_RANGE = -6    /* index out of range (expert, rows) */
+};
+
+/* Kernel choice of iq_matmul_via (the reference's MultiRowPath,
+ * src/gguf.rs:43-62): IQ_PATH_AUTO is iq_matmul's dispatch.  The fixed paths
+ * run one kernel at any row count it covers, so a benchmark or a parity
+ * test can hold everything but the kernel constant.  All give the
+ * reference's bits except IQ_PATH_PREFILL_TILES: int8-MFMA prefill tiles
+ * (Q4_K, 64 or more input rows) whose block integers are exact but whose
+ * f32 combination runs in tile order, within 1e-4 normwise of the
+ * reference -- faster at prefill widths, and not output-preserving across
+ * row counts, so never chosen by the dispatch. */
+enum iq_path {
+    IQ_PATH_AUTO = 0,
+    IQ_PATH_LANES = 1,        /* generic lane kernel (any dtype, any m) */
+    IQ_PATH_GEMV = 2,         /* LDS-staged GEMV (1..63 rows, K-quant and Q8_0) */
+    IQ_PATH_LANE_MFMA = 3,    /* exact lane order on int8 MFMA (Q4_K / Q6_K) */
+    IQ_PATH_PREFILL_TILES = 4 /* tile-order int8 MFMA (Q4_K, m >= 64): NOT bitwise */
 };
 
 typedef struct iq_weight *iq_weight_t;
@@ -92,16 +111,26 @@ int iq_weights_leading_rows(iq_weight_t a, int64_t rows, iq_weight_t *out);
 /* y[m x rows] = x[m x cols] . W^T for device f32 x and y (row-major).  The
  * input rows are quantised on the GPU exactly as the reference's
  * from_float does (Q8K for K-quants, Q8_0 for Q8_0) and the product follows
- * the reference's per-lane f32 order, for any m >= 1.  Uses a library
- * workspace on the device: calls on one device must not overlap (use
- * iq_matmul_ws with distinct workspaces for concurrent streams).
+ * the reference's per-lane f32 order, for any m >= 1: each output row is
+ * bitwise what a one-row call gives.  Uses a library workspace per (device,
+ * stream): calls on different streams or threads never share memory, and
+ * the library lock is held while a call enqueues its launches.  A workspace
+ * grows on the first call that needs more (synchronising that stream); such
+ * a call fails during graph capture, so capture after one eager call of the
+ * same size, or use iq_matmul_ws.
  * Replaces: QuantizedMatrix::forward / forward_spread / forward_rows /
  * multi_row_forward / fused_forward (src/gguf.rs:406-456, :558-690) and the
  * per-row kernels q4k_q8k_row / q6k_q8k_row / q80_q80_row they call
  * (src/qgemm.rs:447-468). */
 int iq_matmul(iq_weight_t w, const float *x, int64_t m, float *y, iq_stream_t stream);
 
-/* Device workspace bytes iq_matmul_ws needs for m input rows of W. */
+/* iq_matmul on one chosen kernel (enum iq_path); IQ_ERR_DTYPE when that
+ * kernel does not cover the dtype, shape or row count.
+ * Replaces: QuantizedMatrix::forward_via (src/gguf.rs:522-556). */
+int iq_matmul_via(iq_weight_t w, const float *x, int64_t m, float *y, int path, iq_stream_t stream);
+
+/* Device workspace bytes iq_matmul_ws needs for m input rows of W (any
+ * path). */
 size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m);
 
 /* iq_matmul with a caller-provided device workspace (>= the size above). */
@@ -132,10 +161,10 @@ int iq_quantize_q80(const float *x, int64_t m, int64_t k, void *blocks_out, iq_s
 int iq_block_sums(iq_weight_t w, const float *x, int64_t m, float *y, int32_t *isum, int32_t *msum,
                   iq_stream_t stream);
 
-/* Per-block integer totals of the int8-MFMA (prefill) path: for Q4_K
- * matrices at 64 or more input rows, iq_matmul runs this path, whose f32
- * combination order differs from the reference's (results agree within the
- * path's 1e-4 normwise tolerance) while each block's integers are exact.
+/* Per-block integer totals of the prefill-tile path (IQ_PATH_PREFILL_TILES,
+ * Q4_K matrices at 64 or more input rows), whose f32 combination order
+ * differs from the reference's (results agree within the path's 1e-4
+ * normwise tolerance) while each block's integers are exact.
  * isum and msum are [m][rows][cols / 256]: isum the block's total integer
  * dot (the sum of the reference's eight `sumi` lanes), msum its mins term
  * (the sum of the four `prod` lanes).  y receives the product.
@@ -175,6 +204,12 @@ int iq_moe_destroy(iq_moe_t moe);
  * down, ordered combine, then routed + shared * sigmoid(x . selector)
  * (:266-273).  experts_out [m x top_k] i32 and weights_out [m x top_k] f32
  * (device, may be NULL) receive the routes.  m * top_k <= 4096.
+ * The handle owns a workspace sized by the widest call so far; a wider call
+ * regrows it (synchronising the device), which is refused during graph
+ * capture.  A captured graph keeps the workspace address it was captured
+ * with, so after capturing a call, make no wider call on the same handle
+ * while the graph may still be replayed.  Calls on one handle must not
+ * overlap in time (they share the workspace); use one handle per stream.
  * Replaces: QuantizedMoeLayer::forward (src/qwen/quantized_moe.rs:227-281)
  * minus the router matmul, whose logits are the input here. */
 int iq_moe_forward(iq_moe_t moe, const float *x, const float *router_logits, int64_t m, float *out,

@@ -12,6 +12,8 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libiq_qgemm.so")
 
 IQ_Q8_0, IQ_Q4_K, IQ_Q6_K = 8, 12, 14
+# enum iq_path (the reference's MultiRowPath, src/gguf.rs:43-62)
+PATH_AUTO, PATH_LANES, PATH_GEMV, PATH_LANE_MFMA, PATH_PREFILL_TILES = 0, 1, 2, 3, 4
 IQ_OK = 0
 IQ_ERR_INVALID, IQ_ERR_SHAPE, IQ_ERR_DTYPE, IQ_ERR_OOM, IQ_ERR_HIP, IQ_ERR_RANGE = -1, -2, -3, -4, -5, -6
 STATUS_NAMES = {
@@ -43,6 +45,7 @@ _SIGNATURES = {
     "iq_weights_concat_rows": ([P, P, ctypes.POINTER(P)], INT),
     "iq_weights_leading_rows": ([P, I64, ctypes.POINTER(P)], INT),
     "iq_matmul": ([P, P, I64, P, P], INT),
+    "iq_matmul_via": ([P, P, I64, P, INT, P], INT),
     "iq_matmul_workspace_size": ([P, I64], SZ),
     "iq_matmul_ws": ([P, P, I64, P, P, SZ, P], INT),
     "iq_matmul_host": ([P, P, I64, P], INT),

@@ -51,6 +51,8 @@ namespace {
 
 std::mutex g_ws_mu;
 struct Workspace {
+    int device = -1;
+    hipStream_t stream = nullptr;
     void* p = nullptr;
     size_t bytes = 0;
 };
@@ -64,30 +66,44 @@ int current_device(int* dev) {
 
 }  // namespace
 
-// Library-owned growable workspace of the current device.
-int workspace(size_t bytes, void** out) {
+int WsLease::acquire(size_t bytes, hipStream_t stream) {
     int dev;
     if (int rc = current_device(&dev)) return rc;
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
-    Workspace& w = g_ws[dev];
-    if (w.bytes < bytes) {
-        if (w.p) {
-            hipError_t e = hipDeviceSynchronize();  // the old buffer may still be in use
-            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-            (void)hipFree(w.p);
-            w.p = nullptr;
-            w.bytes = 0;
+    lock_ = std::unique_lock<std::mutex>(g_ws_mu);
+    Workspace* w = nullptr;
+    for (Workspace& c : g_ws)
+        if (c.device == dev && c.stream == stream) w = &c;
+    if (!w) {
+        g_ws.push_back(Workspace{dev, stream, nullptr, 0});
+        w = &g_ws.back();
+    }
+    if (w->bytes < bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(IQ_ERR_INVALID,
+                        "the library workspace of this stream must grow to %zu bytes, which cannot happen during "
+                        "graph capture: make one eager call of the same size on the stream first, or pass a "
+                        "workspace (iq_matmul_ws)",
+                        bytes);
+        if (w->p) {
+            e = hipStreamSynchronize(stream);  // earlier work on the stream may still read the old buffer
+            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+            (void)hipFree(w->p);
+            w->p = nullptr;
+            w->bytes = 0;
         }
         size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-        hipError_t e = hipMalloc(&w.p, want);
+        e = hipMalloc(&w->p, want);
         if (e != hipSuccess) {
             (void)hipGetLastError();
+            w->p = nullptr;
             return fail(IQ_ERR_OOM, "workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
         }
-        w.bytes = want;
+        w->bytes = want;
     }
-    *out = w.p;
+    p_ = w->p;
     return IQ_OK;
 }
 
@@ -166,35 +182,66 @@ int quantize_for(const iq_weight* w, const float* x, int64_t m, const ActView& a
 // for the int8-MFMA path its layouts and split-K partial tiles).
 size_t matmul_ws_bytes(const iq_weight* w, int64_t m) {
     const size_t a = act_bytes(m, w->cols), p = prefill_workspace_size(view_of(w), m);
-    const size_t d = dense_mfma_workspace_size(view_of(w), m);
+    const size_t d = dense_mfma_workspace_any(view_of(w), m);
     const size_t ap = a > p ? a : p;
     return ap > d ? ap : d;
 }
 
-int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* ws, size_t ws_bytes, int32_t* isum,
-                int32_t* msum, hipStream_t s) {
+// Kernel choice of a product (iq_matmul_via's path argument).  Every path
+// but IQ_PATH_PREFILL_TILES gives the reference's result bit for bit.
+hipError_t launch_path(const iq_weight* w, const float* x, int64_t m, float* y, void* ws, int path, int32_t* isum,
+                       int32_t* msum, hipStream_t s) {
+    const WeightView v = view_of(w);
+    hipError_t e = hipErrorNotSupported;
+    if (path == IQ_PATH_AUTO) {
+        if (!isum && dense_mfma_supported(v, m)) e = launch_dense_mfma(v, x, w->cols, m, y, w->rows, ws, s);
+        if (e == hipErrorNotSupported && !isum && gemv_supported(v, m)) e = launch_gemv(v, x, w->cols, m, y, w->rows, s);
+    } else if (path == IQ_PATH_GEMV) {
+        e = launch_gemv(v, x, w->cols, m, y, w->rows, s);
+    } else if (path == IQ_PATH_LANE_MFMA) {
+        e = launch_dense_mfma_any(v, x, w->cols, m, y, w->rows, ws, s);
+    } else if (path == IQ_PATH_PREFILL_TILES) {
+        e = launch_prefill(v, x, w->cols, m, y, w->rows, ws, nullptr, nullptr, s);
+    }
+    if (e == hipErrorNotSupported && (path == IQ_PATH_AUTO || path == IQ_PATH_LANES)) {
+        ActView a = act_carve(ws, m, w->cols);
+        e = w->dtype == kQ8_0 ? launch_quant_q80(x, w->cols, m, w->cols, a, nullptr, s)
+                              : launch_quant_q8k(x, w->cols, m, w->cols, a, nullptr, s);
+        if (e == hipSuccess) e = launch_matmul_lanes(v, a, y, w->rows, isum, msum, s);
+    }
+    return e;
+}
+
+const char* path_name(int path) {
+    switch (path) {
+    case IQ_PATH_AUTO: return "auto";
+    case IQ_PATH_LANES: return "lanes";
+    case IQ_PATH_GEMV: return "gemv";
+    case IQ_PATH_LANE_MFMA: return "lane-order MFMA";
+    case IQ_PATH_PREFILL_TILES: return "prefill tiles";
+    default: return "unknown";
+    }
+}
+
+int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* ws, size_t ws_bytes, int path,
+                int32_t* isum, int32_t* msum, hipStream_t s) {
     if (int rc = check_weight(w)) return rc;
     if (m < 0) return fail(IQ_ERR_SHAPE, "negative input row count %lld", (long long)m);
+    if (path < IQ_PATH_AUTO || path > IQ_PATH_PREFILL_TILES) return fail(IQ_ERR_INVALID, "unknown matmul path %d", path);
     if (m == 0) return IQ_OK;
     if (!x || !y) return fail(IQ_ERR_INVALID, "null input or output pointer");
     const size_t need = matmul_ws_bytes(w, m);
+    WsLease lease;  // held until the launches below are enqueued
     if (!ws) {
-        if (int rc = workspace(need, &ws)) return rc;
+        if (int rc = lease.acquire(need, s)) return rc;
+        ws = lease.ptr();
     } else if (ws_bytes < need) {
         return fail(IQ_ERR_SHAPE, "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
     }
-    hipError_t e = hipErrorNotSupported;
-    if (!isum && dense_mfma_supported(view_of(w), m))
-        e = launch_dense_mfma(view_of(w), x, w->cols, m, y, w->rows, ws, s);
-    if (e == hipErrorNotSupported && !isum && gemv_supported(view_of(w), m))
-        e = launch_gemv(view_of(w), x, w->cols, m, y, w->rows, s);
-    if (e == hipErrorNotSupported && !isum && prefill_supported(view_of(w), m))
-        e = launch_prefill(view_of(w), x, w->cols, m, y, w->rows, ws, nullptr, nullptr, s);
-    if (e == hipErrorNotSupported) {
-        ActView a = act_carve(ws, m, w->cols);
-        if (int rc = quantize_for(w, x, m, a, nullptr, s)) return rc;
-        e = launch_matmul_lanes(view_of(w), a, y, w->rows, isum, msum, s);
-    }
+    const hipError_t e = launch_path(w, x, m, y, ws, path, isum, msum, s);
+    if (e == hipErrorNotSupported)
+        return fail(IQ_ERR_DTYPE, "%s has no %s kernel for %lld input rows of a [%lld, %lld] matrix", dtype_name(w->dtype),
+                    path_name(path), (long long)m, (long long)w->rows, (long long)w->cols);
     if (e != hipSuccess) return hip_fail(e, "matmul launch");
     return IQ_OK;
 }
@@ -319,7 +366,11 @@ IQ_API int iq_weights_leading_rows(iq_weight_t a, int64_t rows, iq_weight_t* out
 }
 
 IQ_API int iq_matmul(iq_weight_t w, const float* x, int64_t m, float* y, iq_stream_t stream) {
-    return matmul_impl(w, x, m, y, nullptr, 0, nullptr, nullptr, (hipStream_t)stream);
+    return matmul_impl(w, x, m, y, nullptr, 0, IQ_PATH_AUTO, nullptr, nullptr, (hipStream_t)stream);
+}
+
+IQ_API int iq_matmul_via(iq_weight_t w, const float* x, int64_t m, float* y, int path, iq_stream_t stream) {
+    return matmul_impl(w, x, m, y, nullptr, 0, path, nullptr, nullptr, (hipStream_t)stream);
 }
 
 IQ_API size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m) {
@@ -330,7 +381,8 @@ IQ_API size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m) {
 IQ_API int iq_matmul_ws(iq_weight_t w, const float* x, int64_t m, float* y, void* workspace_ptr,
                         size_t workspace_bytes, iq_stream_t stream) {
     if (!workspace_ptr) return fail(IQ_ERR_INVALID, "null workspace");
-    return matmul_impl(w, x, m, y, workspace_ptr, workspace_bytes, nullptr, nullptr, (hipStream_t)stream);
+    return matmul_impl(w, x, m, y, workspace_ptr, workspace_bytes, IQ_PATH_AUTO, nullptr, nullptr,
+                       (hipStream_t)stream);
 }
 
 IQ_API int iq_matmul_host(iq_weight_t w, const float* x_host, int64_t m, float* y_host) {
@@ -340,13 +392,13 @@ IQ_API int iq_matmul_host(iq_weight_t w, const float* x_host, int64_t m, float* 
     const size_t xb = (size_t)(m * w->cols) * 4, yb = (size_t)(m * w->rows) * 4;
     const size_t xo = 0, yo = (xb + 255) & ~(size_t)255, ao = yo + ((yb + 255) & ~(size_t)255);
     const size_t need = ao + matmul_ws_bytes(w, m);
-    void* ws;
-    if (int rc = workspace(need, &ws)) return rc;
-    uint8_t* base = (uint8_t*)ws;
+    WsLease lease;
+    if (int rc = lease.acquire(need, nullptr)) return rc;
+    uint8_t* base = (uint8_t*)lease.ptr();
     hipError_t e = hipMemcpy(base + xo, x_host, xb, hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy (input)");
-    if (int rc = matmul_impl(w, (const float*)(base + xo), m, (float*)(base + yo), base + ao, need - ao, nullptr,
-                             nullptr, nullptr))
+    if (int rc = matmul_impl(w, (const float*)(base + xo), m, (float*)(base + yo), base + ao, need - ao, IQ_PATH_AUTO,
+                             nullptr, nullptr, nullptr))
         return rc;
     e = hipMemcpy(y_host, base + yo, yb, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy (output)");
@@ -360,9 +412,9 @@ static int quantize_entry(int dtype, const float* x, int64_t m, int64_t k, void*
         return fail(IQ_ERR_SHAPE, "quantize_row_%s: %lld is not divisible by %lld", dtype == kQ8_0 ? "q8_0" : "q8k",
                     (long long)k, (long long)be);
     if (m == 0) return IQ_OK;
-    void* ws;
-    if (int rc = workspace(act_bytes(m, k), &ws)) return rc;
-    ActView a = act_carve(ws, m, k);
+    WsLease lease;
+    if (int rc = lease.acquire(act_bytes(m, k), s)) return rc;
+    ActView a = act_carve(lease.ptr(), m, k);
     hipError_t e = dtype == kQ8_0 ? launch_quant_q80(x, k, m, k, a, (uint8_t*)blocks_out, s)
                                   : launch_quant_q8k(x, k, m, k, a, (uint8_t*)blocks_out, s);
     if (e != hipSuccess) return hip_fail(e, "quantisation launch");
@@ -384,9 +436,9 @@ IQ_API int iq_prefill_block_sums(iq_weight_t w, const float* x, int64_t m, float
     if (!prefill_supported(view_of(w), m))
         return fail(IQ_ERR_SHAPE, "the int8-MFMA path covers Q4_K matrices at %lld or more input rows (got %s, %lld)",
                     (long long)kPrefillMinRows, dtype_name(w->dtype), (long long)m);
-    void* ws;
-    if (int rc = workspace(prefill_workspace_size(view_of(w), m), &ws)) return rc;
-    hipError_t e = launch_prefill(view_of(w), x, w->cols, m, y, w->rows, ws, isum, msum, (hipStream_t)stream);
+    WsLease lease;
+    if (int rc = lease.acquire(prefill_workspace_size(view_of(w), m), (hipStream_t)stream)) return rc;
+    hipError_t e = launch_prefill(view_of(w), x, w->cols, m, y, w->rows, lease.ptr(), isum, msum, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
     return IQ_OK;
 }
@@ -395,5 +447,5 @@ IQ_API int iq_block_sums(iq_weight_t w, const float* x, int64_t m, float* y, int
                          iq_stream_t stream) {
     if (!isum) return fail(IQ_ERR_INVALID, "null isum buffer");
     if (w && w->dtype == kQ4_K && !msum) return fail(IQ_ERR_INVALID, "Q4_K needs an msum buffer");
-    return matmul_impl(w, x, m, y, nullptr, 0, isum, msum, (hipStream_t)stream);
+    return matmul_impl(w, x, m, y, nullptr, 0, IQ_PATH_LANES, isum, msum, (hipStream_t)stream);
 }

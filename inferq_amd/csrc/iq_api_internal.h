@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "iq_internal.h"
 
 struct iq_weight {
@@ -23,7 +25,27 @@ const char* dtype_name(int dtype);
 int64_t block_elems(int dtype);
 int64_t block_bytes(int dtype);
 bool dtype_ok(int dtype);
-int workspace(size_t bytes, void** out);
+// Library-owned device workspace of one (device, stream) pair.  A lease
+// holds the library's workspace lock until it is destroyed, so a caller
+// keeps it across every launch that uses the memory: another thread can
+// neither grow (free) the buffer under those launches nor interleave its own
+// launches on the same memory.  Workspaces of different streams are
+// distinct, so calls on different streams never share memory.  Growing a
+// workspace synchronises its stream (its earlier work may still read the old
+// buffer) and is refused while the stream is being captured into a graph.
+class WsLease {
+  public:
+    WsLease() = default;
+    WsLease(const WsLease&) = delete;
+    WsLease& operator=(const WsLease&) = delete;
+    // Acquire at least `bytes` for `stream` on the current device.
+    int acquire(size_t bytes, hipStream_t stream);
+    void* ptr() const { return p_; }
+
+  private:
+    std::unique_lock<std::mutex> lock_;
+    void* p_ = nullptr;
+};
 int check_weight(const iq_weight* w);
 WeightView view_of(const iq_weight* w);
 

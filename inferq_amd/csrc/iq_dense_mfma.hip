@@ -103,34 +103,52 @@ hipError_t launch_t(const DmArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Large K-quant matrices at 2..63 rows: from 64 MiB of weights (an LM head:
-// 2.2x-4.5x over the GEMV at 8-48 rows); from 8 MiB at 16 rows or more
-// (q/gate [8192 x 2048]: 1.8x-2.4x); and from 8 MiB at 8 rows with 8192
-// weight rows or more (q/gate at 8 rows 16.7 -> 15.9 us, q/gate + k + v
-// joined [9216 x 2048] 23.1 -> 15.6 us, q/gate at 12 rows 23.4 -> 15.9 us).
-// Smaller or narrower matrices keep the GEMV, whose latency is lower there
-// (64 weight rows per workgroup leave a [512 x 2048] matrix 8 workgroups and
-// o [2048 x 4096] 32, which ran 2.5x slower).  Staging reads 16-byte chunks
-// of Q4_K rows and 4-byte-aligned windows of Q6_K blocks, so rows must keep
-// that alignment (Q6_K: an even block count per row).
-bool dense_mfma_supported(const WeightView& w, int64_t m) {
-    if (m < 2 || m >= kPrefillMinRows || w.cols % 256 != 0 || w.rows < 1) return false;
-    const int64_t bytes = w.rows * w.row_bytes;
-    const bool large = bytes >= ((int64_t)64 << 20);
-    const bool mid = bytes >= ((int64_t)8 << 20) && (m >= 16 || (m >= 8 && w.rows >= 8192));
-    if (!large && !mid) return false;
+// Whether the tile can read W at all: staging reads 16-byte chunks of Q4_K
+// rows and 4-byte-aligned windows of Q6_K blocks, so rows must keep that
+// alignment (Q6_K: an even block count per row).
+bool dm_layout_ok(const WeightView& w) {
+    if (w.cols % 256 != 0 || w.rows < 1) return false;
     if (w.dtype == kQ4_K) return ((uintptr_t)w.w & 15) == 0;
     if (w.dtype == kQ6_K) return ((uintptr_t)w.w & 3) == 0 && w.row_bytes % 4 == 0;
     return false;
 }
 
-size_t dense_mfma_workspace_size(const WeightView& w, int64_t m) {
-    return dense_mfma_supported(w, m) ? dm_plan(w, m).total() : 0;
+// Where the dispatch uses this kernel.  At 2..63 rows: from 64 MiB of
+// weights (an LM head: 2.2x-4.5x over the GEMV at 8-48 rows); from 8 MiB at
+// 16 rows or more (q/gate [8192 x 2048]: 1.8x-2.4x); and from 8 MiB at 8 rows
+// with 8192 weight rows or more (q/gate at 8 rows 16.7 -> 15.9 us, q/gate + k
+// + v joined [9216 x 2048] 23.1 -> 15.6 us, q/gate at 12 rows 23.4 -> 15.9
+// us).  Smaller or narrower matrices keep the GEMV, whose latency is lower
+// there (64 weight rows per workgroup leave a [512 x 2048] matrix 8
+// workgroups and o [2048 x 4096] 32, which ran 2.5x slower).  From 64 rows
+// (prefill widths) every K-quant matrix the tile can read takes it: the
+// result stays bitwise the one-row result, which speculative decoding needs
+// (src/gguf.rs:493-520 tiles prefill rows under the same guarantee).
+bool dense_mfma_supported(const WeightView& w, int64_t m) {
+    if (m < 2 || !dm_layout_ok(w)) return false;
+    if (m >= kPrefillMinRows) return true;
+    const int64_t bytes = w.rows * w.row_bytes;
+    const bool large = bytes >= ((int64_t)64 << 20);
+    const bool mid = bytes >= ((int64_t)8 << 20) && (m >= 16 || (m >= 8 && w.rows >= 8192));
+    return large || mid;
 }
+
+size_t dense_mfma_workspace_any(const WeightView& w, int64_t m) {
+    return m >= 1 && dm_layout_ok(w) ? dm_plan(w, m).total() : 0;
+}
+
+hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                                 void* ws, hipStream_t s);
 
 hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                              void* ws, hipStream_t s) {
     if (!dense_mfma_supported(w, m)) return hipErrorNotSupported;
+    return launch_dense_mfma_any(w, x, ldx, m, y, ldy, ws, s);
+}
+
+hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                                 void* ws, hipStream_t s) {
+    if (m < 1 || !dm_layout_ok(w) || m > (int64_t)1 << 20) return hipErrorNotSupported;
     const DmPlan P = dm_plan(w, m);
     uint8_t* base = (uint8_t*)ws;
     DmArgs a;

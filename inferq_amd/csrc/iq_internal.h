@@ -57,9 +57,9 @@ bool gemv_supported(const WeightView& w, int64_t m);
 hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                        hipStream_t s);
 
-// The int8-MFMA kernel for Q4_K weights at kPrefillMinRows or more input
-// rows (iq_prefill.hip): per-block integers exact, f32 combination in its own
-// order.  launch_prefill quantises x itself into `ws` (at least
+// The int8-MFMA prefill-tile kernel for Q4_K weights at kPrefillMinRows or
+// more input rows (iq_prefill.hip): per-block integers exact, f32
+// combination in its own order, so only an explicit request runs it.  launch_prefill quantises x itself into `ws` (at least
 // prefill_workspace_size bytes); dbg_isum / dbg_msum, when not null, receive
 // the per-block integer totals [m][rows][cols / 256].
 constexpr int64_t kPrefillMinRows = 64;
@@ -68,13 +68,17 @@ size_t prefill_workspace_size(const WeightView& w, int64_t m);
 hipError_t launch_prefill(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                           void* ws, int32_t* dbg_isum, int32_t* dbg_msum, hipStream_t s);
 
-// The exact lane-order int8-MFMA kernel for large Q4_K / Q6_K matrices at
-// 2..63 input rows (iq_dense_mfma.hip): bitwise the one-row results.
-// launch_dense_mfma quantises x itself into `ws` (at least
-// dense_mfma_workspace_size bytes).
+// The exact lane-order int8-MFMA kernel for Q4_K / Q6_K matrices
+// (iq_dense_mfma.hip): bitwise the one-row results.  dense_mfma_supported
+// says where the dispatch uses it (large matrices at 2..63 input rows, every
+// readable matrix from kPrefillMinRows rows); launch_dense_mfma_any runs it
+// at any row count on any matrix whose layout it can read.  Both quantise x
+// themselves into `ws` (at least dense_mfma_workspace_any bytes).
 bool dense_mfma_supported(const WeightView& w, int64_t m);
-size_t dense_mfma_workspace_size(const WeightView& w, int64_t m);
+size_t dense_mfma_workspace_any(const WeightView& w, int64_t m);
 hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                              void* ws, hipStream_t s);
+hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                                 void* ws, hipStream_t s);
 
 }  // namespace iq

@@ -170,7 +170,17 @@ static int moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t 
     std::lock_guard<std::mutex> lock(L->mu);
     if (L->ws_m < m) {
         const size_t bytes = carve(L, (int)m, nullptr, nullptr);
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t ce = hipStreamIsCapturing(s, &cs);
+        if (ce != hipSuccess) return hip_fail(ce, "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(IQ_ERR_INVALID,
+                        "the MoE workspace must grow to %lld tokens, which cannot happen during graph capture: make "
+                        "one eager call of at least this many tokens on the handle first",
+                        (long long)m);
         if (L->ws) {
+            // the old buffer goes away: the stage hooks must not launch on it
+            L->has_last = false;
             hipError_t e = hipDeviceSynchronize();
             if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
             (void)hipFree(L->ws);
@@ -196,6 +206,7 @@ static int moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t 
     p.logits = logits;
     p.M = (int)m;
     p.out = out;
+    L->has_last = false;
     hipError_t e = launch_moe(p, L->gfmt, L->dfmt, s, (hipEvent_t const*)events);
     if (e != hipSuccess) return hip_fail(e, "MoE launch");
     L->last = p;

@@ -42,8 +42,17 @@ class QuantizedMoeLayer:
                  gate, up, down, shared_gate=None, shared_up=None, shared_down=None, selector=None,
                  normalize: bool = True, shared_gate_dtype: int | None = None,
                  shared_down_dtype: int | None = None):
+        import torch
+
+        named = (("gate", gate), ("up", up), ("down", down), ("shared_gate", shared_gate),
+                 ("shared_up", shared_up), ("shared_down", shared_down), ("selector", selector))
+        for name, t in named:  # before any device call: a host tensor is a caller error, not a missing GPU
+            if t is not None and not t.is_cuda:
+                raise QgemmError(_lib.IQ_ERR_INVALID, f"MoE {name} tensor must be resident in HBM (got {t.device})")
         _ensure_init()
         self.hidden, self.inter, self.n_experts, self.top_k = hidden, inter, n_experts, top_k
+        self.device = torch.cuda.current_device()
+        self._check_device(**dict(named))
         self._keep = [t for t in (gate, up, down, shared_gate, shared_up, shared_down, selector) if t is not None]
 
         def ptr(t):
@@ -69,8 +78,19 @@ class QuantizedMoeLayer:
             _lib._lib.iq_moe_destroy(h)
             self._h = None
 
+    def _check_device(self, **tensors) -> None:
+        """Every tensor handed to the C ABI must live in this layer's HBM:
+        a host pointer would reach the kernels as a device address."""
+        for name, t in tensors.items():
+            if t is None:
+                continue
+            if not t.is_cuda or t.device.index != self.device:
+                raise QgemmError(_lib.IQ_ERR_INVALID, f"MoE {name} must be a tensor on cuda:{self.device} "
+                                                      f"(got {t.device})")
+
     def forward_into(self, xs, router_logits, out, experts=None, weights=None) -> None:
         """Raw call: device f32 xs [m, hidden], logits [m, n_experts], out [m, hidden]."""
+        self._check_device(xs=xs, router_logits=router_logits, out=out, experts=experts, weights=weights)
         m = xs.numel() // self.hidden
         check(lib().iq_moe_forward(self._h, xs.data_ptr(), router_logits.data_ptr(), m, out.data_ptr(),
                                    None if experts is None else experts.data_ptr(),
@@ -79,6 +99,7 @@ class QuantizedMoeLayer:
     def forward_timed(self, xs, router_logits, out, events) -> None:
         """forward_into recording 4 hipEvent_t handles around the routing,
         gate/up and down launches (iq_moe_forward_timed)."""
+        self._check_device(xs=xs, router_logits=router_logits, out=out)
         m = xs.numel() // self.hidden
         ev = (ctypes.c_void_p * 4)(*events)
         check(lib().iq_moe_forward_timed(self._h, xs.data_ptr(), router_logits.data_ptr(), m, out.data_ptr(),
@@ -95,6 +116,7 @@ class QuantizedMoeLayer:
         if xs.numel() % self.hidden:
             raise QgemmError(_lib.IQ_ERR_SHAPE,
                              f"MoE input element count is not divisible by hidden size {self.hidden}")
+        self._check_device(xs=xs, router_logits=router_logits)
         flat = xs.to(torch.float32).reshape(-1, self.hidden).contiguous()
         m = flat.shape[0]
         logits = router_logits.to(torch.float32).reshape(m, self.n_experts).contiguous()

@@ -145,10 +145,22 @@ class QuantizedMatrix:
         check(lib().iq_matmul(self._h, xs.data_ptr(), m, y.data_ptr(), _stream()))
         return y
 
-    def forward_into(self, x, y) -> None:
-        """Raw call: contiguous device f32 x [m, cols] into y [m, rows]."""
+    def forward_via(self, xs, path: int):
+        """src/gguf.rs:522-556: run one chosen kernel (an `iq_path` value,
+        e.g. `_lib.PATH_PREFILL_TILES`), bypassing the dispatch."""
+        import torch
+
+        xs = self._validated_input(xs)
+        m = xs.numel() // self._cols
+        y = torch.empty(*xs.shape[:-1], self._rows, dtype=torch.float32, device=xs.device)
+        check(lib().iq_matmul_via(self._h, xs.data_ptr(), m, y.data_ptr(), path, _stream()))
+        return y
+
+    def forward_into(self, x, y, path: int = 0) -> None:
+        """Raw call: contiguous device f32 x [m, cols] into y [m, rows]
+        (`path` as forward_via; 0 = the dispatch)."""
         m = x.numel() // self._cols
-        check(lib().iq_matmul(self._h, x.data_ptr(), m, y.data_ptr(), _stream()))
+        check(lib().iq_matmul_via(self._h, x.data_ptr(), m, y.data_ptr(), path, _stream()))
 
     # Where the output rows are computed never changes the result
     # (RowSpread, src/gguf.rs:64-80); on the GPU there is one spread.

@@ -1,5 +1,6 @@
-"""GPU parity of the int8-MFMA prefill path (Q4_K, 64 or more input rows)
-through the C ABI.
+"""GPU parity of the int8-MFMA prefill-tile path (Q4_K, 64 or more input
+rows), which a caller requests explicitly (iq_matmul_via with
+IQ_PATH_PREFILL_TILES; the dispatch never picks it), through the C ABI.
 
 Tolerance: per-block integers (the block's total integer dot and its mins
 term) are compared bit for bit with the oracle; outputs within a normwise
@@ -12,6 +13,7 @@ import pytest
 import torch
 
 from conftest import assert_bitexact, assert_close_normwise
+from inferq_amd import _lib
 from inferq_amd import qgemm as Q
 from inferq_amd import synth as S
 
@@ -54,7 +56,7 @@ def test_prefill_matches_oracle(gpu, oracle, rows, cols, m):
     w = S.random_matrix(Q4, rows, cols, rng)
     x = S.normal((m, cols), rng)
     mat = Q.QuantizedMatrix.upload(w, Q4, rows, cols)
-    got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    got = mat.forward_via(torch.from_numpy(x).to(gpu), _lib.PATH_PREFILL_TILES).cpu().numpy()
     ref = oracle.matmul(Q4, w, rows, cols, x, nthreads=8)
     _rowwise_close(got, ref, 1e-4, f"prefill [{rows}x{cols}] m={m}")
 
@@ -64,16 +66,24 @@ def test_prefill_is_deterministic(gpu):
     w = S.random_matrix(Q4, 2048, 4096, rng)
     mat = Q.QuantizedMatrix.upload(w, Q4, 2048, 4096)
     x = torch.from_numpy(S.normal((256, 4096), rng)).to(gpu)
-    a = mat.forward(x).cpu().numpy()
-    b = mat.forward(x).cpu().numpy()
+    a = mat.forward_via(x, _lib.PATH_PREFILL_TILES).cpu().numpy()
+    b = mat.forward_via(x, _lib.PATH_PREFILL_TILES).cpu().numpy()
     assert_bitexact(a, b, "run to run")
 
 
-def test_below_prefill_threshold_stays_bitexact(gpu, oracle):
-    """63 rows run the bit-exact kernels, 64 the MFMA path."""
+def test_prefill_tiles_only_on_request(gpu, oracle):
+    """The dispatch keeps the reference's bits at 64+ rows; the tile path
+    runs only when asked for, and refuses what it does not cover."""
     rng = np.random.default_rng(63)
     w = S.random_matrix(Q4, 256, 2048, rng)
-    x = S.normal((63, 2048), rng)
+    x = S.normal((64, 2048), rng)
     mat = Q.QuantizedMatrix.upload(w, Q4, 256, 2048)
-    assert_bitexact(mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy(),
-                    oracle.matmul(Q4, w, 256, 2048, x), "63 rows")
+    xt = torch.from_numpy(x).to(gpu)
+    assert_bitexact(mat.forward(xt).cpu().numpy(), oracle.matmul(Q4, w, 256, 2048, x, nthreads=8), "dispatch, 64 rows")
+    _rowwise_close(mat.forward_via(xt, _lib.PATH_PREFILL_TILES).cpu().numpy(),
+                   oracle.matmul(Q4, w, 256, 2048, x, nthreads=8), 1e-4, "tiles, 64 rows")
+    with pytest.raises(Q.QgemmError, match="prefill tiles kernel for 63 input rows"):
+        mat.forward_via(xt[:63], _lib.PATH_PREFILL_TILES)
+    q6 = Q.QuantizedMatrix.upload(S.random_matrix(S.Q6_K, 64, 2048, rng), S.Q6_K, 64, 2048)
+    with pytest.raises(Q.QgemmError, match="Q6K has no prefill tiles kernel"):
+        q6.forward_via(xt, _lib.PATH_PREFILL_TILES)

@@ -116,3 +116,23 @@ def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libiq_qgemm.so"))
     with pytest.raises(OSError, match="missing"):
         _lib.lib()
+
+
+def test_moe_rejects_host_tensors():
+    """Host (CPU) tensors never reach the C ABI: their addresses would be
+    dereferenced by the kernels as device addresses."""
+    import torch
+
+    from inferq_amd import moe
+
+    cpu = torch.zeros(4, dtype=torch.uint8)
+    with pytest.raises(_lib.QgemmError, match="resident in HBM"):
+        moe.QuantizedMoeLayer(256, 256, 4, 2, S.Q4_K, S.Q6_K, cpu, cpu, cpu)
+    layer = object.__new__(moe.QuantizedMoeLayer)
+    layer.hidden, layer.n_experts, layer.top_k, layer.device = 256, 4, 2, 0
+    x = torch.zeros(1, 256)
+    for call in (lambda: layer.forward_into(x, torch.zeros(1, 4), torch.zeros(1, 256)),
+                 lambda: layer.forward(x, torch.zeros(1, 4)),
+                 lambda: layer.forward_timed(x, torch.zeros(1, 4), torch.zeros(1, 256), [None] * 4)):
+        with pytest.raises(_lib.QgemmError, match="must be a tensor on cuda:0"):
+            call()
