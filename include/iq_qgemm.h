@@ -31,13 +31,15 @@ extern "C" {
 #endif
 
 /* GGML type ids as carried by GGUF (the reference's GgmlDType). */
-enum iq_dtype { IQ_Q8_0 = 8, IQ_Q4_K = 12, IQ_Q6_K = 14 };
+/* Q5_K runs on the lane kernel in ggml's published vec_dot_q5_K_q8_K order
+ * (the reference hands it to candle's per-row vec_dot, src/gguf.rs:593). */
+enum iq_dtype { IQ_Q8_0 = 8, IQ_Q4_K = 12, IQ_Q5_K = 13, IQ_Q6_K = 14 };
 
 enum iq_status {
     IQ_OK = 0,
     IQ_ERR_INVALID = -1, /* null handle / pointer, bad argument */
     IQ_ERR_SHAPE = -2,   /* width not a whole number of blocks, wrong input width, size mismatch */
-    IQ_ERR_DTYPE = -3,   /* dtype outside {Q8_0, Q4_K, Q6_K}, or mismatched dtypes */
+    IQ_ERR_DTYPE = -3,   /* dtype outside {Q8_0, Q4_K, Q5_K, Q6_K}, mismatched dtypes, or no kernel */
     IQ_ERR_OOM = -4,     /* device allocation failed */
     IQ_ERR_HIP = -5,     /* HIP runtime error (launch, copy, no device) */
     IQ_ERR_RANGE = -6    /* index out of range (expert, rows) */
@@ -192,6 +194,8 @@ typedef struct {
     int shared_gate_dtype, shared_down_dtype;
     const void *shared_gate, *shared_up, *shared_down; /* device or all NULL */
     const float *selector;                              /* device; required with a shared expert */
+    const float *router; /* device f32 [n_experts x hidden] (blk.N.ffn_gate_inp.weight), or NULL:
+                            required by iq_moe_forward_x */
 } iq_moe_desc;
 
 int iq_moe_create(const iq_moe_desc *desc, iq_moe_t *out);
@@ -214,6 +218,18 @@ int iq_moe_destroy(iq_moe_t moe);
  * minus the router matmul, whose logits are the input here. */
 int iq_moe_forward(iq_moe_t moe, const float *x, const float *router_logits, int64_t m, float *out,
                    int32_t *experts_out, float *weights_out, iq_stream_t stream);
+
+/* The whole sublayer from x: router logits = x . router^T on the GPU (f32,
+ * a fixed order per (token, expert): per lane over h = lane + 64 j, then a
+ * butterfly -- the reference's candle gemm order is not visible), then as
+ * iq_moe_forward; when `residual` (device [m x hidden], 16-byte aligned) is
+ * not NULL, out = residual + MoE(x), the residual add of the decoder layer.
+ * Needs a layer created with a router.
+ * Replaces: QuantizedMoeLayer::forward (src/qwen/quantized_moe.rs:227-281,
+ * router matmul at :253) and the residual add that follows it
+ * (src/qwen/quantized_layer.rs:212). */
+int iq_moe_forward_x(iq_moe_t moe, const float *x, int64_t m, const float *residual, float *out,
+                     int32_t *experts_out, float *weights_out, iq_stream_t stream);
 
 /* iq_moe_forward, also recording events[0..3] (hipEvent_t handles created by
  * the caller) on `stream`: before the routing launch, then after the

@@ -11,7 +11,7 @@ import os
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libiq_qgemm.so")
 
-IQ_Q8_0, IQ_Q4_K, IQ_Q6_K = 8, 12, 14
+IQ_Q8_0, IQ_Q4_K, IQ_Q5_K, IQ_Q6_K = 8, 12, 13, 14
 # enum iq_path (the reference's MultiRowPath, src/gguf.rs:43-62)
 PATH_AUTO, PATH_LANES, PATH_GEMV, PATH_LANE_MFMA, PATH_PREFILL_TILES = 0, 1, 2, 3, 4
 IQ_OK = 0
@@ -56,6 +56,7 @@ _SIGNATURES = {
     "iq_moe_create": ([P, ctypes.POINTER(P)], INT),
     "iq_moe_destroy": ([P], INT),
     "iq_moe_forward": ([P, P, P, I64, P, P, P, P], INT),
+    "iq_moe_forward_x": ([P, P, I64, P, P, P, P, P], INT),
     "iq_moe_forward_timed": ([P, P, P, I64, P, P, P, ctypes.POINTER(P), P], INT),
     "iq_moe_forward_stage": ([P, INT, P], INT),
 }
@@ -72,7 +73,7 @@ class MoeDesc(ctypes.Structure):
         ("gate_bytes", ctypes.c_size_t), ("up_bytes", ctypes.c_size_t), ("down_bytes", ctypes.c_size_t),
         ("shared_gate_dtype", ctypes.c_int), ("shared_down_dtype", ctypes.c_int),
         ("shared_gate", ctypes.c_void_p), ("shared_up", ctypes.c_void_p), ("shared_down", ctypes.c_void_p),
-        ("selector", ctypes.c_void_p),
+        ("selector", ctypes.c_void_p), ("router", ctypes.c_void_p),
     ]
 
 

@@ -37,6 +37,7 @@ int hip_fail(hipError_t e, const char* what) {
 const char* dtype_name(int dtype) {
     switch (dtype) {
     case kQ4_K: return "Q4K";
+    case kQ5_K: return "Q5K";
     case kQ6_K: return "Q6K";
     case kQ8_0: return "Q8_0";
     default: return "unknown";
@@ -44,8 +45,9 @@ const char* dtype_name(int dtype) {
 }
 
 int64_t block_elems(int dtype) { return dtype == kQ8_0 ? 32 : 256; }
-int64_t block_bytes(int dtype) { return dtype == kQ4_K ? 144 : dtype == kQ6_K ? 210 : 34; }
-bool dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ6_K || dtype == kQ8_0; }
+int64_t block_bytes(int dtype) { return dtype == kQ4_K ? 144 : dtype == kQ5_K ? 176 : dtype == kQ6_K ? 210 : 34; }
+bool dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0; }
+bool moe_dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ6_K || dtype == kQ8_0; }
 
 namespace {
 
@@ -127,7 +129,8 @@ WeightView view_of(const iq_weight* w) {
 // src/gguf.rs:627-646).
 int check_matrix(int dtype, int64_t rows, int64_t cols, size_t nbytes, int64_t* row_bytes) {
     if (!dtype_ok(dtype))
-        return fail(IQ_ERR_DTYPE, "unsupported executable GGUF matrix dtype %d; expected Q4_K, Q6_K or Q8_0", dtype);
+        return fail(IQ_ERR_DTYPE, "unsupported executable GGUF matrix dtype %d; expected Q4_K, Q5_K, Q6_K or Q8_0",
+                    dtype);
     if (rows <= 0 || cols <= 0) return fail(IQ_ERR_SHAPE, "invalid matrix shape [%lld, %lld]", (long long)rows,
                                              (long long)cols);
     if (cols % block_elems(dtype))
@@ -446,6 +449,7 @@ IQ_API int iq_prefill_block_sums(iq_weight_t w, const float* x, int64_t m, float
 IQ_API int iq_block_sums(iq_weight_t w, const float* x, int64_t m, float* y, int32_t* isum, int32_t* msum,
                          iq_stream_t stream) {
     if (!isum) return fail(IQ_ERR_INVALID, "null isum buffer");
-    if (w && w->dtype == kQ4_K && !msum) return fail(IQ_ERR_INVALID, "Q4_K needs an msum buffer");
+    if (w && (w->dtype == kQ4_K || w->dtype == kQ5_K) && !msum)
+        return fail(IQ_ERR_INVALID, "%s needs an msum buffer", dtype_name(w->dtype));
     return matmul_impl(w, x, m, y, nullptr, 0, IQ_PATH_LANES, isum, msum, (hipStream_t)stream);
 }

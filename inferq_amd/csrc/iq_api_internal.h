@@ -25,6 +25,7 @@ const char* dtype_name(int dtype);
 int64_t block_elems(int dtype);
 int64_t block_bytes(int dtype);
 bool dtype_ok(int dtype);
+bool moe_dtype_ok(int dtype);  // expert formats of the MoE kernels (no Q5_K)
 // Library-owned device workspace of one (device, stream) pair.  A lease
 // holds the library's workspace lock until it is destroyed, so a caller
 // keeps it across every launch that uses the memory: another thread can

@@ -10,6 +10,7 @@ namespace iq {
 // GGML type ids (GGUF dtype codes).
 constexpr int kQ8_0 = 8;
 constexpr int kQ4_K = 12;
+constexpr int kQ5_K = 13;
 constexpr int kQ6_K = 14;
 
 // Quantised activations in the internal (lane-transposed) layout.

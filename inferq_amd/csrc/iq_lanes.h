@@ -39,6 +39,13 @@ struct Q4W {
     u32x4a16 hdr;   // d, dmin, scales[12]
     uint32_t q[4];  // qs dwords 32j + 4k
 };
+// Q5_K: the Q4_K header and nibbles plus the lane's dword of qh (bit 2j of
+// byte l is the fifth bit of weight 64j + l, bit 2j + 1 that of 64j + 32 + l).
+struct Q5W {
+    u32x4a16 hdr;   // d, dmin, scales[12]
+    uint32_t qh;    // qh dword 4k
+    uint32_t q[4];  // qs dwords 32j + 4k
+};
 // Q6_K lane data.  A block at 2 (mod 4) is loaded as aligned dword pairs
 // whose byte funnel shift (by `sh` bytes) is applied at use, so that a burst
 // of loads is never interrupted by waits for earlier ones.
@@ -63,6 +70,11 @@ struct WT<kQ4_K> {
     static constexpr int kBlockBytes = 144;
 };
 template <>
+struct WT<kQ5_K> {
+    using T = Q5W;
+    static constexpr int kBlockBytes = 176;
+};
+template <>
 struct WT<kQ6_K> {
     using T = Q6W;
     static constexpr int kBlockBytes = 210;
@@ -77,6 +89,14 @@ __device__ __forceinline__ void load_q4(const uint8_t* blk, int k, Q4W& w) {
     w.hdr = *(const u32x4a16*)blk;
 #pragma unroll
     for (int j = 0; j < 4; j++) w.q[j] = ld32(blk + 16 + 32 * j + 4 * k);
+}
+
+// 176-byte blocks keep the 16-byte alignment of the row.
+__device__ __forceinline__ void load_q5(const uint8_t* blk, int k, Q5W& w) {
+    w.hdr = *(const u32x4a16*)blk;
+    w.qh = ld32(blk + 16 + 4 * k);
+#pragma unroll
+    for (int j = 0; j < 4; j++) w.q[j] = ld32(blk + 48 + 32 * j + 4 * k);
 }
 
 // Q6_K block known to start at 0 (mod 4): exact dword loads.
@@ -165,6 +185,31 @@ __device__ __forceinline__ Q4Dec q4_decode(const Q4W& wb, int k) {
     }
     return r;
 }
+// Q5_K decodes into the Q4_K form: the 5-bit weights (0..31) go where the
+// nibbles were, so q4_dot gives the lane integers of ggml's
+// vec_dot_q5_K_q8_K (the same maddubs/madd lane structure as Q4_K).
+__device__ __forceinline__ Q4Dec q5_decode(const Q5W& wb, int k) {
+    Q4W as4;
+    as4.hdr = wb.hdr;
+#pragma unroll
+    for (int j = 0; j < 4; j++) as4.q[j] = wb.q[j];
+    Q4Dec r = q4_decode(as4, k);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        r.lo[j] |= ((wb.qh >> (2 * j)) & 0x01010101u) << 4;
+        r.hi[j] |= ((wb.qh >> (2 * j + 1)) & 0x01010101u) << 4;
+    }
+    return r;
+}
+
+// Sum of an int over lanes 0..3 of each group of 8 (lanes 4..7 hold copies
+// of lanes 0..3), in every lane: (l0 + l1) + (l2 + l3), exact.
+__device__ __forceinline__ int32_t isum_quad(int32_t v) {
+    v = v + __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    v = v + __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    return v;
+}
+
 __device__ __forceinline__ void q4_dot(const Q4Dec& r, const uint32_t (&av)[8], float yd, uint32_t q8s, int32_t& isum,
                                        int32_t& msum, float& d, float& dmin) {
     isum = 0;
@@ -231,6 +276,7 @@ __device__ __forceinline__ void lanes_load(const uint8_t* const (&wrow)[R], int 
             const int g = g0 + bi;
             if (g < ng && wrow[r] != nullptr) {
                 if constexpr (FMT == kQ4_K) load_q4(wrow[r] + (int64_t)g * 144, k, w[r][bi]);
+                else if constexpr (FMT == kQ5_K) load_q5(wrow[r] + (int64_t)g * 176, k, w[r][bi]);
                 else if constexpr (FMT == kQ6_K) load_q6(wrow[r] + (int64_t)g * 210, k, w[r][bi]);
                 else load_q8(wrow[r], (int64_t)g * 8, nbw, k, w[r][bi]);
             } else {
@@ -308,6 +354,33 @@ __device__ __forceinline__ void lanes_accumulate(const typename WT<FMT>::T (&w)[
                         }
                     }
                 }
+            } else if constexpr (FMT == kQ5_K) {
+                // lanes as Q4_K; the mins join one f32 scalar per row,
+                // summs = summs + dmin * (m . q8s), multiply then add
+                const Q4Dec dec = q5_decode(wb, k);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    if (mi < mc[r]) {
+                        const int64_t ar = arow[r][mi];
+                        uint32_t av[8];
+                        load_act(a, ar, g, k, av);
+                        const float yd = a.d[ar * a.ldd + g];
+                        const uint32_t q8s = *(const uint32_t*)(a.s8 + (ar * a.ng + g) * 8 + 2 * (k & 3));
+                        int32_t isum, msum;
+                        float d, dmin;
+                        q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
+                        acc[r][mi] = __builtin_fmaf(d, (float)isum, acc[r][mi]);
+                        const int32_t mtot = isum_quad(msum);
+                        accm[r][mi] = accm[r][mi] + dmin * (float)mtot;
+                        if constexpr (DBG) {
+                            if (wrow[r]) {
+                                const int64_t base = ((ar * dbg.n + dbg.row) * dbg.nbw + g);
+                                dbg.isum[base * 8 + k] = isum;
+                                if (k < 4) dbg.msum[base * 4 + k] = msum;
+                            }
+                        }
+                    }
+                }
             } else if constexpr (FMT == kQ6_K) {
                 const Q6Dec dec = q6_decode(wb, k);
 #pragma unroll
@@ -355,7 +428,7 @@ __device__ __forceinline__ void lanes_accumulate(const typename WT<FMT>::T (&w)[
 }
 
 // The 8 lanes of each row combine: hsum_f32_8 (+ hsum_f32_4 of the Q4_K
-// mins).  out[r][i] is valid in lane k == 0 of each group.
+// mins, + the Q5_K mins scalar).  out[r][i] is valid in lane k == 0 of each group.
 template <int FMT, int MT, int R>
 __device__ __forceinline__ void lanes_finish(const float (&acc)[R][MT], const float (&accm)[R][MT],
                                              float (&out)[R][MT]) {
@@ -365,6 +438,7 @@ __device__ __forceinline__ void lanes_finish(const float (&acc)[R][MT], const fl
         for (int mi = 0; mi < MT; mi++) {
             float v = hsum8(acc[r][mi]);
             if constexpr (FMT == kQ4_K) v = v + hsum4(accm[r][mi]);
+            if constexpr (FMT == kQ5_K) v = v + accm[r][mi];  // every lane holds summs
             out[r][mi] = v;
         }
     }

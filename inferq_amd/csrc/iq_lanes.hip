@@ -88,6 +88,7 @@ hipError_t launch_matmul_lanes(const WeightView& w, const ActView& a, float* y, 
     const bool dbg = isum != nullptr;
     switch (w.dtype) {
     case kQ4_K: return launch_fmt<kQ4_K>(args, dbg, s);
+    case kQ5_K: return launch_fmt<kQ5_K>(args, dbg, s);
     case kQ6_K: return launch_fmt<kQ6_K>(args, dbg, s);
     case kQ8_0: return launch_fmt<kQ8_0>(args, dbg, s);
     default: return hipErrorInvalidValue;

@@ -23,9 +23,12 @@ struct MoeParams {
     const float* selector = nullptr;   // [H]
     int64_t g_row_bytes = 0, d_row_bytes = 0, g_exp_bytes = 0, d_exp_bytes = 0;
     int g_nbw = 0, d_nbw = 0;  // weight blocks per row of gate/up and of down
+    const float* router = nullptr;  // f32 [E][H] (blk.N.ffn_gate_inp.weight), or null
     // call
     const float* x = nullptr;       // [M][H]
-    const float* logits = nullptr;  // [M][E]
+    const float* logits = nullptr;  // [M][E] (given, or computed from router into logits_ws)
+    float* logits_ws = nullptr;     // [M][E] workspace for the router's logits
+    const float* residual = nullptr;  // [M][H] added to the output, or null
     int M = 0;
     float* out = nullptr;  // [M][H]
     // workspace
@@ -50,6 +53,12 @@ struct MoeParams {
     int32_t* chunk_r0 = nullptr;     // [max_chunks] first row of the chunk in its group
     int max_chunks = 0;
 };
+
+// logits_ws[t][e] = x[t] . router[e] (the router matmul of
+// src/qwen/quantized_moe.rs:253) in a fixed order: lane l of a wave sums
+// x[h] * r[h] for h = l, l + 64, ... in order, then the lanes meet in a
+// butterfly; every (token, expert) pair is formed the same way at any M.
+hipError_t launch_moe_router(const MoeParams& p, hipStream_t s);
 
 // Launch prep, gate_up and down for one layer call.
 // events (may be null): 4 hipEvent_t recorded before and between the launches.

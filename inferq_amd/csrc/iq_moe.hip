@@ -261,6 +261,7 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeParams p) {
             acc = acc + p.vals[(int64_t)pos * p.H + nn] * p.weights[t * K + j];
         }
         if (p.sgate_w) acc = acc + p.vals[(int64_t)(p.M * K + t) * p.H + nn] * p.sgate[t];
+        if (p.residual) acc = p.residual[(int64_t)t * p.H + nn] + acc;  // src/qwen/quantized_layer.rs:212
         p.out[(int64_t)t * p.H + nn] = acc;
     }
 }
@@ -597,6 +598,7 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
             float v = 0.f;
             for (int j = 0; j < K; j++) v = v + s_vals[j][threadIdx.x] * p.weights[t * K + j];
             if (has_shared) v = v + s_vals[K][threadIdx.x] * p.sgate[t];
+            if (p.residual) v = p.residual[(int64_t)t * p.H + nn] + v;  // src/qwen/quantized_layer.rs:212
             p.out[(int64_t)t * p.H + nn] = v;
         }
     }
@@ -653,6 +655,52 @@ hipError_t launch_moe1_g(const MoeParams& p, int dfmt, hipStream_t s, hipEvent_t
     case kQ4_K: return launch_moe1<GFMT, kQ4_K>(p, s, ev);
     case kQ6_K: return launch_moe1<GFMT, kQ6_K>(p, s, ev);
     default: return hipErrorInvalidValue;
+    }
+}
+
+// ---------------------------------------------------------------- router
+// Grid (E, ceil(M / TT)), one wave per workgroup: expert e = blockIdx.x
+// against tokens blockIdx.y * TT ..; each lane keeps one partial sum per
+// token over h = lane + 64 j (the router row is read once per TT tokens).
+template <int TT>
+__global__ __launch_bounds__(64) void k_moe_router(MoeParams p) {
+    const int lane = threadIdx.x;
+    const int e = blockIdx.x, t0 = blockIdx.y * TT;
+    const int nt = min(TT, p.M - t0);
+    const int64_t H = p.H;
+    const float* r = p.router + (int64_t)e * H;
+    float part[TT];
+#pragma unroll
+    for (int i = 0; i < TT; i++) part[i] = 0.f;
+    int64_t h = lane;
+    for (; h + 64 * 7 < H; h += 64 * 8) {
+        float rv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) rv[j] = r[h + 64 * j];
+#pragma unroll
+        for (int i = 0; i < TT; i++) {
+            if (i < nt) {
+                const float* xr = p.x + (int64_t)(t0 + i) * H + h;
+                float xv[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) xv[j] = xr[64 * j];
+#pragma unroll
+                for (int j = 0; j < 8; j++) part[i] = part[i] + xv[j] * rv[j];
+            }
+        }
+    }
+    for (; h < H; h += 64) {
+        const float rv = r[h];
+#pragma unroll
+        for (int i = 0; i < TT; i++)
+            if (i < nt) part[i] = part[i] + p.x[(int64_t)(t0 + i) * H + h] * rv;
+    }
+#pragma unroll
+    for (int i = 0; i < TT; i++) {
+        float v = part[i];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+        if (lane == 0 && i < nt) p.logits_ws[(int64_t)(t0 + i) * p.E + e] = v;
     }
 }
 
@@ -716,6 +764,13 @@ hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hip
     case kQ8_0: return launch_g<kQ8_0>(p, dfmt, s, ev);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_moe_router(const MoeParams& p, hipStream_t s) {
+    if (!p.router || !p.logits_ws || p.M < 1) return hipErrorInvalidValue;
+    if (p.M <= 2) hipLaunchKernelGGL((k_moe_router<1>), dim3((unsigned)p.E, (unsigned)p.M), dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((k_moe_router<8>), dim3((unsigned)p.E, (unsigned)((p.M + 7) / 8)), dim3(64), 0, s, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_moe_stage(const MoeParams& p, int gfmt, int dfmt, int stage, hipStream_t s) {

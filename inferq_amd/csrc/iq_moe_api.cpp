@@ -59,7 +59,9 @@ size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
     uint8_t* ahs = take(P * ngI * 32);
     uint8_t* chg = take((size_t)maxch * 4);
     uint8_t* chr = take((size_t)maxch * 4);
+    uint8_t* lgw = L->layer.router ? take((size_t)m * L->layer.E * 4) : nullptr;
     if (p) {
+        p->logits_ws = (float*)lgw;
         p->experts = (int32_t*)experts;
         p->weights = (float*)weights;
         p->sgate = (float*)sgate;
@@ -93,7 +95,7 @@ IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
     if (E > kMoeMaxExperts || K > kMoeMaxTopK)
         return fail(IQ_ERR_RANGE, "this build supports at most %d experts and top-%d (got %lld, %lld)", kMoeMaxExperts,
                     kMoeMaxTopK, (long long)E, (long long)K);
-    if (!dtype_ok(d->gate_dtype) || !dtype_ok(d->down_dtype))
+    if (!moe_dtype_ok(d->gate_dtype) || !moe_dtype_ok(d->down_dtype))
         return fail(IQ_ERR_DTYPE, "unsupported expert dtypes %d / %d; expected Q4_K, Q6_K or Q8_0", d->gate_dtype,
                     d->down_dtype);
     if (H <= 0 || I <= 0 || H % block_elems(d->gate_dtype) || I % block_elems(d->down_dtype) || I % 32)
@@ -111,7 +113,7 @@ IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
         return fail(IQ_ERR_SHAPE, "invalid down expert shape: %zu bytes for [%lld, %lld, %lld] %s", d->down_bytes,
                     (long long)E, (long long)H, (long long)I, dtype_name(d->down_dtype));
     for (const void* ptr : {d->gate, d->up, d->down, (const void*)d->shared_gate, (const void*)d->shared_up,
-                            (const void*)d->shared_down, (const void*)d->selector})
+                            (const void*)d->shared_down, (const void*)d->selector, (const void*)d->router})
         if ((uintptr_t)ptr & 15u) return fail(IQ_ERR_INVALID, "device tensors must be 16-byte aligned");
     const int nshared = (d->shared_gate != nullptr) + (d->shared_up != nullptr) + (d->shared_down != nullptr);
     if (nshared != 0 && nshared != 3) return fail(IQ_ERR_INVALID, "shared expert needs gate, up and down matrices");
@@ -138,6 +140,7 @@ IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
         p.sdown_w = (const uint8_t*)d->shared_down;
         p.selector = d->selector;
     }
+    p.router = d->router;
     p.g_row_bytes = grb;
     p.d_row_bytes = drb;
     p.g_exp_bytes = I * grb;
@@ -157,12 +160,18 @@ IQ_API int iq_moe_destroy(iq_moe_t L) {
     return IQ_OK;
 }
 
-static int moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
-                       int32_t* experts_out, float* weights_out, void* const* events, iq_stream_t stream) {
+// logits == nullptr: the layer's router computes them from x.
+static int moe_forward(iq_moe_t L, const float* x, const float* logits, const float* residual, int64_t m,
+                       float* out, int32_t* experts_out, float* weights_out, void* const* events,
+                       iq_stream_t stream) {
     if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
     if (m < 0) return fail(IQ_ERR_SHAPE, "negative token count");
     if (m == 0) return IQ_OK;
-    if (!x || !logits || !out) return fail(IQ_ERR_INVALID, "null input or output pointer");
+    if (!logits && !L->layer.router)
+        return fail(IQ_ERR_INVALID, "this MoE layer has no router: pass router logits (iq_moe_forward)");
+    if (!x || !out) return fail(IQ_ERR_INVALID, "null input or output pointer");
+    if (residual && ((uintptr_t)residual & 15u))
+        return fail(IQ_ERR_INVALID, "the residual must be 16-byte aligned");
     if (m * L->layer.K > kMoeMaxAssign)
         return fail(IQ_ERR_RANGE, "%lld tokens x top-%lld exceeds %d assignments per call", (long long)m,
                     (long long)L->layer.K, kMoeMaxAssign);
@@ -203,11 +212,19 @@ static int moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t 
     // carve() sized the views for ws_m tokens; the call uses m
     p.xq.m = (int)m;
     p.x = x;
-    p.logits = logits;
     p.M = (int)m;
     p.out = out;
+    p.residual = residual;
     L->has_last = false;
-    hipError_t e = launch_moe(p, L->gfmt, L->dfmt, s, (hipEvent_t const*)events);
+    hipError_t e = hipSuccess;
+    if (logits) {
+        p.logits = logits;
+    } else {
+        p.logits = p.logits_ws;
+        e = launch_moe_router(p, s);
+        if (e != hipSuccess) return hip_fail(e, "MoE router launch");
+    }
+    e = launch_moe(p, L->gfmt, L->dfmt, s, (hipEvent_t const*)events);
     if (e != hipSuccess) return hip_fail(e, "MoE launch");
     L->last = p;
     L->has_last = true;
@@ -221,7 +238,13 @@ static int moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t 
 
 IQ_API int iq_moe_forward(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
                           int32_t* experts_out, float* weights_out, iq_stream_t stream) {
-    return moe_forward(L, x, logits, m, out, experts_out, weights_out, nullptr, stream);
+    if (m > 0 && !logits) return fail(IQ_ERR_INVALID, "null router logits");
+    return moe_forward(L, x, logits, nullptr, m, out, experts_out, weights_out, nullptr, stream);
+}
+
+IQ_API int iq_moe_forward_x(iq_moe_t L, const float* x, int64_t m, const float* residual, float* out,
+                            int32_t* experts_out, float* weights_out, iq_stream_t stream) {
+    return moe_forward(L, x, nullptr, residual, m, out, experts_out, weights_out, nullptr, stream);
 }
 
 IQ_API int iq_moe_forward_timed(iq_moe_t L, const float* x, const float* logits, int64_t m, float* out,
@@ -229,7 +252,8 @@ IQ_API int iq_moe_forward_timed(iq_moe_t L, const float* x, const float* logits,
                                 iq_stream_t stream) {
     if (!events || !events[0] || !events[1] || !events[2] || !events[3])
         return fail(IQ_ERR_INVALID, "iq_moe_forward_timed needs four events");
-    return moe_forward(L, x, logits, m, out, experts_out, weights_out, events, stream);
+    if (m > 0 && !logits) return fail(IQ_ERR_INVALID, "null router logits");
+    return moe_forward(L, x, logits, nullptr, m, out, experts_out, weights_out, events, stream);
 }
 
 IQ_API int iq_moe_forward_stage(iq_moe_t L, int stage, iq_stream_t stream) {

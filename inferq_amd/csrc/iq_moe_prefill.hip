@@ -321,6 +321,13 @@ __global__ __launch_bounds__(256) void k_mp_combine(MoeParams p) {
         acc.z = acc.z + sv.z * gt;
         acc.w = acc.w + sv.w * gt;
     }
+    if (p.residual) {  // src/qwen/quantized_layer.rs:212
+        const f32x4 rv = *(const f32x4*)(p.residual + (int64_t)t * p.H + nn);
+        acc.x = rv.x + acc.x;
+        acc.y = rv.y + acc.y;
+        acc.z = rv.z + acc.z;
+        acc.w = rv.w + acc.w;
+    }
     *(f32x4*)(p.out + (int64_t)t * p.H + nn) = acc;
 }
 
@@ -365,7 +372,8 @@ bool moep_supported(const MoeParams& p, int gfmt, int dfmt) {
     auto al = [](const void* q, uintptr_t a) { return q == nullptr || ((uintptr_t)q & (a - 1)) == 0; };
     const uintptr_t ga = gfmt == kQ4_K ? 16 : 4, da = dfmt == kQ4_K ? 16 : 4;
     const bool aligned = al(p.gate, ga) && al(p.up, ga) && al(p.sgate_w, ga) && al(p.sup_w, ga) && al(p.down, da) &&
-                         al(p.sdown_w, da) && al(p.out, 16);  // k_mp_combine stores four floats at a time
+                         al(p.sdown_w, da) && al(p.out, 16) &&
+                         al(p.residual, 16);  // k_mp_combine moves four floats at a time
     return kq && aligned && p.M >= kMoePrefillMinTokens && p.H % 256 == 0 && p.I % 256 == 0 && p.E <= kMoeMaxExperts &&
            p.K <= kMoeMaxTopK && p.g_row_bytes % 4 == 0 && p.d_row_bytes % 4 == 0 &&
            (int64_t)p.E * ((p.M + 31) / 32) * 4 <= 32768 && p.xhs != nullptr && p.chunk_group != nullptr &&

@@ -2,10 +2,10 @@
 
 `QuantizedMoeLayer` keeps the interface of inferq's QuantizedMoeLayer
 (src/qwen/quantized_moe.rs:105-460) with the routed experts resident in HBM
-as the GGUF expert tensors and the whole layer (routing, grouped experts,
-SwiGLU, ordered combine, shared expert) run by the gfx950 kernels through
-the C ABI.  The router's logits are an input: the router matmul is not part
-of this path.
+as the GGUF expert tensors and the whole layer (router matmul when the
+layer has a router, routing, grouped experts, SwiGLU, ordered combine,
+shared expert, optionally the decoder layer's residual add) run by the
+gfx950 kernels through the C ABI.  Router logits may also be given.
 """
 from __future__ import annotations
 
@@ -41,11 +41,12 @@ class QuantizedMoeLayer:
     def __init__(self, hidden: int, inter: int, n_experts: int, top_k: int, gate_dtype: int, down_dtype: int,
                  gate, up, down, shared_gate=None, shared_up=None, shared_down=None, selector=None,
                  normalize: bool = True, shared_gate_dtype: int | None = None,
-                 shared_down_dtype: int | None = None):
+                 shared_down_dtype: int | None = None, router=None):
         import torch
 
         named = (("gate", gate), ("up", up), ("down", down), ("shared_gate", shared_gate),
-                 ("shared_up", shared_up), ("shared_down", shared_down), ("selector", selector))
+                 ("shared_up", shared_up), ("shared_down", shared_down), ("selector", selector),
+                 ("router", router))
         for name, t in named:  # before any device call: a host tensor is a caller error, not a missing GPU
             if t is not None and not t.is_cuda:
                 raise QgemmError(_lib.IQ_ERR_INVALID, f"MoE {name} tensor must be resident in HBM (got {t.device})")
@@ -53,7 +54,9 @@ class QuantizedMoeLayer:
         self.hidden, self.inter, self.n_experts, self.top_k = hidden, inter, n_experts, top_k
         self.device = torch.cuda.current_device()
         self._check_device(**dict(named))
-        self._keep = [t for t in (gate, up, down, shared_gate, shared_up, shared_down, selector) if t is not None]
+        self._keep = [t for t in (gate, up, down, shared_gate, shared_up, shared_down, selector, router)
+                      if t is not None]
+        self.has_router = router is not None
 
         def ptr(t):
             return None if t is None else t.data_ptr()
@@ -66,7 +69,7 @@ class QuantizedMoeLayer:
             ptr(gate), ptr(up), ptr(down), nbytes(gate), nbytes(up), nbytes(down),
             shared_gate_dtype if shared_gate_dtype is not None else gate_dtype,
             shared_down_dtype if shared_down_dtype is not None else down_dtype,
-            ptr(shared_gate), ptr(shared_up), ptr(shared_down), ptr(selector),
+            ptr(shared_gate), ptr(shared_up), ptr(shared_down), ptr(selector), ptr(router),
         )
         h = ctypes.c_void_p()
         check(lib().iq_moe_create(ctypes.byref(desc), ctypes.byref(h)))
@@ -96,6 +99,16 @@ class QuantizedMoeLayer:
                                    None if experts is None else experts.data_ptr(),
                                    None if weights is None else weights.data_ptr(), _stream()))
 
+    def forward_x_into(self, xs, out, residual=None, experts=None, weights=None) -> None:
+        """Raw call of the whole sublayer from x (iq_moe_forward_x): the
+        layer's router gives the logits; out = residual + MoE(xs) when a
+        residual is given."""
+        self._check_device(xs=xs, out=out, residual=residual, experts=experts, weights=weights)
+        m = xs.numel() // self.hidden
+        check(lib().iq_moe_forward_x(self._h, xs.data_ptr(), m, None if residual is None else residual.data_ptr(),
+                                     out.data_ptr(), None if experts is None else experts.data_ptr(),
+                                     None if weights is None else weights.data_ptr(), _stream()))
+
     def forward_timed(self, xs, router_logits, out, events) -> None:
         """forward_into recording 4 hipEvent_t handles around the routing,
         gate/up and down launches (iq_moe_forward_timed)."""
@@ -109,20 +122,29 @@ class QuantizedMoeLayer:
         """Re-launch one stage of the last call (iq_moe_forward_stage)."""
         check(lib().iq_moe_forward_stage(self._h, stage, _stream()))
 
-    def forward(self, xs, router_logits) -> QuantizedMoeOutput:
-        """src/qwen/quantized_moe.rs:227: the layer output and the routes."""
+    def forward(self, xs, router_logits=None, residual=None) -> QuantizedMoeOutput:
+        """src/qwen/quantized_moe.rs:227: the layer output and the routes.
+        Without router_logits the layer's router computes them
+        (src/qwen/quantized_moe.rs:253); with a residual the output is
+        residual + MoE(xs) (src/qwen/quantized_layer.rs:212)."""
         import torch
 
         if xs.numel() % self.hidden:
             raise QgemmError(_lib.IQ_ERR_SHAPE,
                              f"MoE input element count is not divisible by hidden size {self.hidden}")
-        self._check_device(xs=xs, router_logits=router_logits)
+        self._check_device(xs=xs, router_logits=router_logits, residual=residual)
         flat = xs.to(torch.float32).reshape(-1, self.hidden).contiguous()
         m = flat.shape[0]
-        logits = router_logits.to(torch.float32).reshape(m, self.n_experts).contiguous()
         out = torch.empty_like(flat)
         experts = torch.empty(m, self.top_k, dtype=torch.int32, device=flat.device)
         weights = torch.empty(m, self.top_k, dtype=torch.float32, device=flat.device)
-        self.forward_into(flat, logits, out, experts, weights)
+        if router_logits is None:
+            res = None if residual is None else residual.to(torch.float32).reshape(m, self.hidden).contiguous()
+            self.forward_x_into(flat, out, res, experts, weights)
+        else:
+            if residual is not None:
+                raise QgemmError(_lib.IQ_ERR_INVALID, "a residual goes with the layer's own router (forward_x)")
+            logits = router_logits.to(torch.float32).reshape(m, self.n_experts).contiguous()
+            self.forward_into(flat, logits, out, experts, weights)
         e, w = experts.cpu().tolist(), weights.cpu().tolist()
         return QuantizedMoeOutput(out.reshape(xs.shape), [Route(a, b) for a, b in zip(e, w)])

@@ -13,11 +13,11 @@ import ctypes
 import numpy as np
 
 from . import _lib
-from ._lib import IQ_Q4_K, IQ_Q6_K, IQ_Q8_0, QgemmError, check, lib
+from ._lib import IQ_Q4_K, IQ_Q5_K, IQ_Q6_K, IQ_Q8_0, QgemmError, check, lib
 
-DTYPE_NAMES = {IQ_Q4_K: "Q4K", IQ_Q6_K: "Q6K", IQ_Q8_0: "Q8_0"}
-BLOCK_ELEMS = {IQ_Q4_K: 256, IQ_Q6_K: 256, IQ_Q8_0: 32}
-BLOCK_BYTES = {IQ_Q4_K: 144, IQ_Q6_K: 210, IQ_Q8_0: 34}
+DTYPE_NAMES = {IQ_Q4_K: "Q4K", IQ_Q5_K: "Q5K", IQ_Q6_K: "Q6K", IQ_Q8_0: "Q8_0"}
+BLOCK_ELEMS = {IQ_Q4_K: 256, IQ_Q5_K: 256, IQ_Q6_K: 256, IQ_Q8_0: 32}
+BLOCK_BYTES = {IQ_Q4_K: 144, IQ_Q5_K: 176, IQ_Q6_K: 210, IQ_Q8_0: 34}
 
 _initialised = set()
 
@@ -202,7 +202,7 @@ class QuantizedMatrix:
         msum = torch.empty(m, self._rows, nb, 4, dtype=torch.int32, device=xs.device)
         check(lib().iq_block_sums(self._h, xs.data_ptr(), m, y.data_ptr(), isum.data_ptr(), msum.data_ptr(),
                                   _stream()))
-        return y, isum, (msum if self._dtype == IQ_Q4_K else None)
+        return y, isum, (msum if self._dtype in (IQ_Q4_K, IQ_Q5_K) else None)
 
     def prefill_block_sums(self, xs):
         """Product and per-block integer totals of the int8-MFMA path (Q4_K,

@@ -4,6 +4,7 @@ Weights are random bytes in the native GGUF block layouts, drawn so that
 every block is a valid, finite block:
   * Q4_K (144 B): fp16 d and dmin ~ U[0, 2^-6); 12 scale bytes and 128 quant
     bytes uniform u8.
+  * Q5_K (176 B): as Q4_K, plus 32 high-bit bytes uniform u8.
   * Q6_K (210 B): ql, qh uniform u8; 16 scales uniform i8; fp16 d ~ U[0, 2^-6).
   * Q8_0 (34 B): fp16 d = |N(0,1)| * 0.02; 32 quants uniform in [-127, 127].
 Activations and router logits are f32 ~ N(0, 1).
@@ -12,10 +13,10 @@ from __future__ import annotations
 
 import numpy as np
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_0: 34}
-BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32}
-NAMES = {Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_0: "Q8_0"}
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34}
+BLOCK_ELEMS = {Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32}
+NAMES = {Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q8_0: "Q8_0"}
 
 
 def row_bytes(dtype: int, cols: int) -> int:
@@ -36,7 +37,7 @@ def random_blocks(dtype: int, n_blocks: int, rng: np.random.Generator) -> np.nda
     """n_blocks random blocks as a flat uint8 array."""
     bb = BLOCK_BYTES[dtype]
     raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
-    if dtype == Q4_K:
+    if dtype in (Q4_K, Q5_K):
         d = _f16_bits(rng.random(n_blocks, dtype=np.float32) * np.float32(2.0 ** -6))
         dmin = _f16_bits(rng.random(n_blocks, dtype=np.float32) * np.float32(2.0 ** -6))
         raw[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
@@ -99,7 +100,7 @@ def random_blocks_device(dtype: int, n_blocks: int, device, seed: int):
     def f16_bytes(values):
         return values.to(torch.float16).view(torch.uint8).reshape(n_blocks, 2)
 
-    if dtype == Q4_K:
+    if dtype in (Q4_K, Q5_K):
         raw[:, 0:2] = f16_bytes(torch.rand(n_blocks, device=device, generator=gen) * 2.0 ** -6)
         raw[:, 2:4] = f16_bytes(torch.rand(n_blocks, device=device, generator=gen) * 2.0 ** -6)
     elif dtype == Q6_K:

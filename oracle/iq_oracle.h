@@ -37,10 +37,11 @@ extern "C" {
 #endif
 
 /* GGML type ids, the values GGUF files carry. */
-enum { OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q6_K = 14 };
+enum { OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14 };
 
 /* GGUF block layouts (src/qgemm.rs:46-65). */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } or_q4k_block; /* 144 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } or_q5k_block; /* 176 B */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } or_q6k_block; /* 210 B */
 typedef struct { uint16_t d; int8_t qs[32]; } or_q80_block;                                 /* 34 B */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } or_q8k_block;              /* 292 B */
@@ -66,6 +67,12 @@ void or_unpack_k_scales(const uint8_t packed[12], uint8_t sc[8], uint8_t mn[8]);
  * of `sumi` after one block; msum[k] (Q4_K only) is lane k of the mins
  * `prod` vector.  These are the "per-block integer dot products". */
 void or_q4k_block_lanes(const or_q4k_block *w, const or_q8k_block *x, int32_t isum[8], int32_t msum[4]);
+/* Q5_K (src/qgemm.rs:50-53; executed by candle's BlockQ5K::vec_dot at
+ * src/gguf.rs:593, a port of ggml's AVX2 vec_dot_q5_K_q8_K -- candle-core
+ * 0.11.0, not vendored here): the Q4_K lane structure with the fifth bit of
+ * weight 64j + l (+32) from bit 2j (2j+1) of qh[l]; msum[k] are the four
+ * lanes of madd(mins, pairwise bsums). */
+void or_q5k_block_lanes(const or_q5k_block *w, const or_q8k_block *x, int32_t isum[8], int32_t msum[4]);
 void or_q6k_block_lanes(const or_q6k_block *w, const or_q8k_block *x, int32_t isum[8]);
 void or_q80_block_lanes(const or_q80_block *w, const or_q80_block *x, int32_t isum[8]);
 
@@ -73,6 +80,7 @@ void or_q80_block_lanes(const or_q80_block *w, const or_q80_block *x, int32_t is
  * the dequantisation formula (no lanes).  sum_k isum[k] must equal `isum`
  * here, and sum_k msum[k] must equal `msum`. */
 void or_q4k_block_textbook(const or_q4k_block *w, const or_q8k_block *x, int64_t *isum, int64_t *msum);
+void or_q5k_block_textbook(const or_q5k_block *w, const or_q8k_block *x, int64_t *isum, int64_t *msum);
 void or_q6k_block_textbook(const or_q6k_block *w, const or_q8k_block *x, int64_t *isum);
 void or_q80_block_textbook(const or_q80_block *w, const or_q80_block *x, int64_t *isum);
 
@@ -82,6 +90,12 @@ void or_q80_block_textbook(const or_q80_block *w, const or_q80_block *x, int64_t
  * `_lanes` is a scalar emulation of the AVX2 lane arithmetic; `_avx2` is the
  * intrinsic form (only when built with AVX2+FMA; returns -1 otherwise). */
 void or_q4k_q8k_row_lanes(const or_q4k_block *w, size_t nb, const or_q8k_block *in, size_t rows, float *out);
+/* Q5_K per (row, input): eight f32 lanes advanced by fma(d, isum_k) per
+ * block, the mins as one f32 scalar summs = summs + dmin * (m . q8s) per
+ * block (multiply, then add), result hsum_f32_8(acc) + summs -- ggml's
+ * published vec_dot_q5_K_q8_K order.  PARITY UNPINNED against candle's
+ * AVX2 code itself, which is absent here. */
+void or_q5k_q8k_row_lanes(const or_q5k_block *w, size_t nb, const or_q8k_block *in, size_t rows, float *out);
 void or_q6k_q8k_row_lanes(const or_q6k_block *w, size_t nb, const or_q8k_block *in, size_t rows, float *out);
 void or_q80_q80_row_lanes(const or_q80_block *w, size_t nb, const or_q80_block *in, size_t rows, float *out);
 int or_q4k_q8k_row_avx2(const or_q4k_block *w, size_t nb, const or_q8k_block *in, size_t rows, float *out);
@@ -133,6 +147,13 @@ typedef struct {
 
 int or_moe_forward(const or_moe_layer *layer, const float *x, const float *logits, size_t m,
                    float *out, int32_t *experts, float *weights, int mode, int impl, int nthreads);
+
+/* The router matmul, logits[t][e] = x[t] . router[e] for f32 x [m x h]
+ * and router [e x h] (src/qwen/quantized_moe.rs:253, a candle f32 Linear
+ * whose summation order is not visible here).  order 0: summed in double
+ * and rounded once (the exact product to within one rounding); order 1:
+ * summed sequentially in f32 over h. */
+void or_router_logits(const float *x, size_t m, size_t h, const float *router, size_t e, float *logits, int order);
 
 /* Pieces of the MoE exposed for tests. */
 float or_silu_mul(float gate, float up);  /* (g / (1 + exp(-g))) * u */

@@ -30,6 +30,8 @@ static void run_rows(const row_job *j) {
         if (j->dtype == OR_Q4_K) {
             if (j->impl == 1) or_q4k_q8k_row_avx2(wrow, j->nb, j->packed, j->rows, o);
             else or_q4k_q8k_row_lanes(wrow, j->nb, j->packed, j->rows, o);
+        } else if (j->dtype == OR_Q5_K) {
+            or_q5k_q8k_row_lanes(wrow, j->nb, j->packed, j->rows, o);  /* one order: no AVX2 twin */
         } else if (j->dtype == OR_Q6_K) {
             if (j->impl == 1) or_q6k_q8k_row_avx2(wrow, j->nb, j->packed, j->rows, o);
             else or_q6k_q8k_row_lanes(wrow, j->nb, j->packed, j->rows, o);

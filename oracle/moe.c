@@ -19,6 +19,23 @@ float or_silu_mul(float gate, float up) {
     return (gate / (1.f + expf(-gate))) * up;
 }
 
+void or_router_logits(const float *x, size_t m, size_t h, const float *router, size_t e, float *logits, int order) {
+    for (size_t t = 0; t < m; t++) {
+        for (size_t j = 0; j < e; j++) {
+            const float *xr = x + t * h, *r = router + j * h;
+            if (order == 0) {
+                double s = 0.0;
+                for (size_t i = 0; i < h; i++) s += (double)xr[i] * (double)r[i];
+                logits[t * e + j] = (float)s;
+            } else {
+                float s = 0.f;
+                for (size_t i = 0; i < h; i++) s = s + xr[i] * r[i];
+                logits[t * e + j] = s;
+            }
+        }
+    }
+}
+
 float or_sigmoid(float v) {
     /* candle-nn sigmoid: recip(exp(-v) + 1) */
     return 1.f / (expf(-v) + 1.f);

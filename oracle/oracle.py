@@ -15,16 +15,18 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 
 Q4K_BLOCK = np.dtype([("d", "<u2"), ("dmin", "<u2"), ("scales", "u1", 12), ("qs", "u1", 128)])
+Q5K_BLOCK = np.dtype([("d", "<u2"), ("dmin", "<u2"), ("scales", "u1", 12), ("qh", "u1", 32), ("qs", "u1", 128)])
 Q6K_BLOCK = np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("scales", "i1", 16), ("d", "<u2")])
 Q80_BLOCK = np.dtype([("d", "<u2"), ("qs", "i1", 32)])
 Q8K_BLOCK = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)])
-assert (Q4K_BLOCK.itemsize, Q6K_BLOCK.itemsize, Q80_BLOCK.itemsize, Q8K_BLOCK.itemsize) == (144, 210, 34, 292)
+assert (Q4K_BLOCK.itemsize, Q5K_BLOCK.itemsize, Q6K_BLOCK.itemsize, Q80_BLOCK.itemsize,
+        Q8K_BLOCK.itemsize) == (144, 176, 210, 34, 292)
 
-BLOCK = {Q4_K: Q4K_BLOCK, Q6_K: Q6K_BLOCK, Q8_0: Q80_BLOCK}
-BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32}
+BLOCK = {Q4_K: Q4K_BLOCK, Q5_K: Q5K_BLOCK, Q6_K: Q6K_BLOCK, Q8_0: Q80_BLOCK}
+BLOCK_ELEMS = {Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32}
 
 _lib = None
 
@@ -50,13 +52,16 @@ def _declare(L: ctypes.CDLL) -> None:
     L.or_f32_to_f16.argtypes, L.or_f32_to_f16.restype = [F], ctypes.c_uint16
     for name in ("or_quantize_q8k", "or_quantize_q80"):
         getattr(L, name).argtypes, getattr(L, name).restype = [P, S, P], I
+    L.or_router_logits.argtypes, L.or_router_logits.restype = [P, S, S, P, S, P, I], None
     L.or_q4k_block_lanes.argtypes = [P, P, P, P]
+    L.or_q5k_block_lanes.argtypes = [P, P, P, P]
+    L.or_q5k_block_textbook.argtypes = [P, P, P, P]
     L.or_q6k_block_lanes.argtypes = [P, P, P]
     L.or_q80_block_lanes.argtypes = [P, P, P]
     L.or_q4k_block_textbook.argtypes = [P, P, P, P]
     L.or_q6k_block_textbook.argtypes = [P, P, P]
     L.or_q80_block_textbook.argtypes = [P, P, P]
-    for name in ("or_q4k_q8k_row_lanes", "or_q6k_q8k_row_lanes", "or_q80_q80_row_lanes"):
+    for name in ("or_q4k_q8k_row_lanes", "or_q5k_q8k_row_lanes", "or_q6k_q8k_row_lanes", "or_q80_q80_row_lanes"):
         getattr(L, name).argtypes, getattr(L, name).restype = [P, S, P, S, P], None
     for name in ("or_q4k_q8k_row_avx2", "or_q6k_q8k_row_avx2", "or_q80_q80_row_avx2"):
         getattr(L, name).argtypes, getattr(L, name).restype = [P, S, P, S, P], I
@@ -104,13 +109,14 @@ def quantize_q80(x: np.ndarray) -> np.ndarray:
 
 
 def block_lanes(dtype: int, wblock: np.ndarray, xblock: np.ndarray):
-    """Per-block lane integers (isum[8], msum[4] for Q4_K)."""
+    """Per-block lane integers (isum[8], msum[4] for Q4_K and Q5_K)."""
     isum = np.zeros(8, np.int32)
     msum = np.zeros(4, np.int32)
     w = np.ascontiguousarray(wblock)
     x = np.ascontiguousarray(xblock)
-    if dtype == Q4_K:
-        lib().or_q4k_block_lanes(_p(w), _p(x), _p(isum), _p(msum))
+    if dtype in (Q4_K, Q5_K):
+        fn = lib().or_q4k_block_lanes if dtype == Q4_K else lib().or_q5k_block_lanes
+        fn(_p(w), _p(x), _p(isum), _p(msum))
         return isum, msum
     if dtype == Q6_K:
         lib().or_q6k_block_lanes(_p(w), _p(x), _p(isum))
@@ -124,8 +130,9 @@ def block_textbook(dtype: int, wblock: np.ndarray, xblock: np.ndarray):
     msum = np.zeros(1, np.int64)
     w = np.ascontiguousarray(wblock)
     x = np.ascontiguousarray(xblock)
-    if dtype == Q4_K:
-        lib().or_q4k_block_textbook(_p(w), _p(x), _p(isum), _p(msum))
+    if dtype in (Q4_K, Q5_K):
+        fn = lib().or_q4k_block_textbook if dtype == Q4_K else lib().or_q5k_block_textbook
+        fn(_p(w), _p(x), _p(isum), _p(msum))
         return int(isum[0]), int(msum[0])
     if dtype == Q6_K:
         lib().or_q6k_block_textbook(_p(w), _p(x), _p(isum))
@@ -139,7 +146,7 @@ def row_kernel(dtype: int, wrow: np.ndarray, inputs_block_major: np.ndarray, row
     out = np.zeros(rows, np.float32)
     w = np.ascontiguousarray(wrow)
     x = np.ascontiguousarray(inputs_block_major)
-    name = {Q4_K: "q4k_q8k", Q6_K: "q6k_q8k", Q8_0: "q80_q80"}[dtype]
+    name = {Q4_K: "q4k_q8k", Q5_K: "q5k_q8k", Q6_K: "q6k_q8k", Q8_0: "q80_q80"}[dtype]
     fn = getattr(lib(), f"or_{name}_row_{impl}")
     rc = fn(_p(w), w.size, _p(x), rows, _p(out))
     if impl == "avx2" and rc:
@@ -220,6 +227,19 @@ def moe_forward(layer: dict, x: np.ndarray, logits: np.ndarray, mode: int = 0, i
     if rc:
         raise RuntimeError(f"or_moe_forward failed ({rc})")
     return out, experts, weights
+
+
+def router_logits(x: np.ndarray, router: np.ndarray, order: int = 0) -> np.ndarray:
+    """or_router_logits: x [m x h] . router [e x h]^T (order 0: double, 1:
+    sequential f32)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    router = np.ascontiguousarray(router, dtype=np.float32)
+    h = router.shape[-1]
+    x = x.reshape(-1, h)
+    e = router.size // h
+    out = np.zeros((x.shape[0], e), np.float32)
+    lib().or_router_logits(_p(x), x.shape[0], h, _p(router), e, _p(out), order)
+    return out
 
 
 def silu_mul(g: float, u: float) -> float:

@@ -39,6 +39,24 @@ void or_q4k_q8k_row_lanes(const or_q4k_block *w, size_t nb, const or_q8k_block *
     }
 }
 
+void or_q5k_q8k_row_lanes(const or_q5k_block *w, size_t nb, const or_q8k_block *in, size_t rows, float *out) {
+    for (size_t r = 0; r < rows; r++) {
+        float acc[8] = {0}, summs = 0.f;
+        for (size_t b = 0; b < nb; b++) {
+            const or_q8k_block *y = &in[b * rows + r];
+            int32_t isum[8], msum[4];
+            or_q5k_block_lanes(&w[b], y, isum, msum);
+            float d = y->d * or_f16_to_f32(w[b].d);
+            float dmin = -y->d * or_f16_to_f32(w[b].dmin);
+            for (int k = 0; k < 8; k++) acc[k] = fmaf(d, (float)isum[k], acc[k]);
+            /* hadd(hadd(prod, 0), 0): (l0 + l1) + (l2 + l3), exact in i32 */
+            int32_t m = (msum[0] + msum[1]) + (msum[2] + msum[3]);
+            summs = summs + dmin * (float)m;
+        }
+        out[r] = hsum8(acc) + summs;
+    }
+}
+
 void or_q6k_q8k_row_lanes(const or_q6k_block *w, size_t nb, const or_q8k_block *in, size_t rows, float *out) {
     for (size_t r = 0; r < rows; r++) {
         float acc[8] = {0};

@@ -11,6 +11,7 @@
 #include "iq_oracle.h"
 
 _Static_assert(sizeof(or_q4k_block) == 144, "Q4_K block is 144 bytes");
+_Static_assert(sizeof(or_q5k_block) == 176, "Q5_K block is 176 bytes");
 _Static_assert(sizeof(or_q6k_block) == 210, "Q6_K block is 210 bytes");
 _Static_assert(sizeof(or_q80_block) == 34, "Q8_0 block is 34 bytes");
 _Static_assert(sizeof(or_q8k_block) == 292, "Q8K block is 292 bytes");
@@ -73,6 +74,7 @@ uint16_t or_f32_to_f16(float f) {
 size_t or_block_bytes(int dtype) {
     switch (dtype) {
     case OR_Q4_K: return 144;
+    case OR_Q5_K: return 176;
     case OR_Q6_K: return 210;
     case OR_Q8_0: return 34;
     default: return 0;
@@ -82,6 +84,7 @@ size_t or_block_bytes(int dtype) {
 size_t or_block_elems(int dtype) {
     switch (dtype) {
     case OR_Q4_K:
+    case OR_Q5_K:
     case OR_Q6_K: return 256;
     case OR_Q8_0: return 32;
     default: return 0;
@@ -184,6 +187,29 @@ void or_q4k_block_lanes(const or_q4k_block *w, const or_q8k_block *x, int32_t is
         msum[k] = (int32_t)mn[2 * k] * q8s[2 * k] + (int32_t)mn[2 * k + 1] * q8s[2 * k + 1];
 }
 
+void or_q5k_block_lanes(const or_q5k_block *w, const or_q8k_block *x, int32_t isum[8], int32_t msum[4]) {
+    uint8_t sc[8], mn[8];
+    or_unpack_k_scales(w->scales, sc, mn);
+    for (int k = 0; k < 8; k++) {
+        int32_t s = 0;
+        for (int j = 0; j < 4; j++) {
+            int32_t lo = 0, hi = 0;
+            for (int b = 4 * k; b < 4 * k + 4; b++) {
+                uint8_t q = w->qs[32 * j + b];
+                int32_t h0 = (w->qh[b] >> (2 * j)) & 1, h1 = (w->qh[b] >> (2 * j + 1)) & 1;
+                lo += ((int32_t)(q & 15) + 16 * h0) * x->qs[64 * j + b];
+                hi += ((int32_t)(q >> 4) + 16 * h1) * x->qs[64 * j + 32 + b];
+            }
+            s += (int32_t)sc[2 * j] * lo + (int32_t)sc[2 * j + 1] * hi;
+        }
+        isum[k] = s;
+    }
+    int16_t q8s[8];
+    for (int i = 0; i < 8; i++) q8s[i] = (int16_t)(x->bsums[2 * i] + x->bsums[2 * i + 1]);
+    for (int k = 0; k < 4; k++)
+        msum[k] = (int32_t)mn[2 * k] * q8s[2 * k] + (int32_t)mn[2 * k + 1] * q8s[2 * k + 1];
+}
+
 void or_q6k_block_lanes(const or_q6k_block *w, const or_q8k_block *x, int32_t isum[8]) {
     for (int k = 0; k < 8; k++) {
         int32_t s = 0;
@@ -222,6 +248,18 @@ static int q4k_elem(const or_q4k_block *w, int e, int *sub) {
     return r < 32 ? (q & 15) : (q >> 4);
 }
 
+/* ggml dequantize_row_q5_K: weight 64j + l takes the low nibble of
+ * qs[32j + l] and bit 2j of qh[l]; weight 64j + 32 + l the high nibble and
+ * bit 2j + 1. */
+static int q5k_elem(const or_q5k_block *w, int e, int *sub) {
+    int j = e / 64, r = e % 64, l = r % 32;
+    *sub = 2 * j + (r >= 32);
+    uint8_t q = w->qs[32 * j + l];
+    int lo = r < 32 ? (q & 15) : (q >> 4);
+    int hi = (w->qh[l] >> (2 * j + (r >= 32))) & 1;
+    return lo + 16 * hi;
+}
+
 static int q6k_elem(const or_q6k_block *w, int e) {
     int h = e / 128, r = e % 128, quarter = r / 32, l = r % 32;
     uint8_t lq = w->ql[64 * h + 32 * (quarter & 1) + l];
@@ -237,6 +275,20 @@ void or_q4k_block_textbook(const or_q4k_block *w, const or_q8k_block *x, int64_t
     for (int e = 0; e < 256; e++) {
         int sub;
         int q = q4k_elem(w, e, &sub);
+        is += (int64_t)sc[sub] * q * x->qs[e];
+        ms += (int64_t)mn[sub] * x->qs[e];
+    }
+    *isum = is;
+    *msum = ms;
+}
+
+void or_q5k_block_textbook(const or_q5k_block *w, const or_q8k_block *x, int64_t *isum, int64_t *msum) {
+    uint8_t sc[8], mn[8];
+    or_unpack_k_scales(w->scales, sc, mn);
+    int64_t is = 0, ms = 0;
+    for (int e = 0; e < 256; e++) {
+        int sub;
+        int q = q5k_elem(w, e, &sub);
         is += (int64_t)sc[sub] * q * x->qs[e];
         ms += (int64_t)mn[sub] * x->qs[e];
     }
@@ -270,6 +322,16 @@ int or_dequantize(int dtype, const void *blocks, size_t n_rows, size_t cols, flo
             for (int e = 0; e < 256; e++) {
                 int sub;
                 int q = q4k_elem(w, e, &sub);
+                y[e] = d * sc[sub] * q - dmin * mn[sub];
+            }
+        } else if (dtype == OR_Q5_K) {
+            const or_q5k_block *w = (const or_q5k_block *)blocks + i;
+            uint8_t sc[8], mn[8];
+            or_unpack_k_scales(w->scales, sc, mn);
+            float d = or_f16_to_f32(w->d), dmin = or_f16_to_f32(w->dmin);
+            for (int e = 0; e < 256; e++) {
+                int sub;
+                int q = q5k_elem(w, e, &sub);
                 y[e] = d * sc[sub] * q - dmin * mn[sub];
             }
         } else if (dtype == OR_Q6_K) {

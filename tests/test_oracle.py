@@ -109,7 +109,7 @@ def test_q80_quantisation_cases(oracle):
 
 
 # ------------------------------------------------- per-block integers
-@pytest.mark.parametrize("dtype", [Q4, Q6, Q8])
+@pytest.mark.parametrize("dtype", [Q4, S.Q5_K, Q6, Q8])
 def test_lane_integers_sum_to_textbook_integers(oracle, dtype):
     rng = np.random.default_rng(2 + dtype)
     nb = 24
@@ -121,7 +121,7 @@ def test_lane_integers_sum_to_textbook_integers(oracle, dtype):
         isum, msum = oracle.block_lanes(dtype, w[b], q[b])
         ti, tm = oracle.block_textbook(dtype, w[b], q[b])
         assert int(isum.astype(np.int64).sum()) == ti
-        if dtype == Q4:
+        if dtype in (Q4, S.Q5_K):
             assert int(msum.astype(np.int64).sum()) == tm
 
 
@@ -139,7 +139,7 @@ def test_lane_emulation_equals_the_avx2_sequence(oracle, dtype):
                         f"{S.NAMES[dtype]} m={m}")
 
 
-@pytest.mark.parametrize("dtype", [Q4, Q6, Q8])
+@pytest.mark.parametrize("dtype", [Q4, S.Q5_K, Q6, Q8])
 def test_product_matches_f64_dequantised_dot(oracle, dtype):
     """Closed form: the f32 result equals dequant(W) . dequant(quant(x)) up
     to f32 accumulation (~1e-6 normwise); a dropped term, a wrong sign or a
@@ -387,3 +387,107 @@ def test_golden_fixtures_reproduce(oracle, golden):
     e, w = oracle.top_k_routes(golden["route_logits"], 2, True)
     assert np.array_equal(e, golden["route_experts"]) and np.array_equal(w, golden["route_weights"])
     assert golden["route_experts"][0].tolist() == [1, 3]
+
+
+def test_router_logits_pins(oracle):
+    """The router product (src/qwen/quantized_moe.rs:253): one-hot router
+    rows pick x's columns exactly; small-integer operands give the integer
+    dot exactly in both orders; double and sequential f32 sums agree within
+    the f32 summation bound n * eps * sum |x r|."""
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((5, 512), dtype=np.float32)
+    cols = np.array([0, 7, 511, 100])
+    onehot = np.zeros((4, 512), np.float32)
+    onehot[np.arange(4), cols] = 1.0
+    for order in (0, 1):
+        assert np.array_equal(oracle.router_logits(x, onehot, order), x[:, cols])
+    xi = rng.integers(-8, 9, (3, 512)).astype(np.float32)
+    ri = rng.integers(-8, 9, (6, 512)).astype(np.float32)
+    exact = xi.astype(np.int64) @ ri.astype(np.int64).T
+    for order in (0, 1):
+        assert np.array_equal(oracle.router_logits(xi, ri, order), exact.astype(np.float32))
+    r = rng.standard_normal((256, 512), dtype=np.float32) / np.float32(np.sqrt(512))
+    a, b = oracle.router_logits(x, r, 0), oracle.router_logits(x, r, 1)
+    bound = 512 * np.finfo(np.float32).eps * (np.abs(x).astype(np.float64) @ np.abs(r).astype(np.float64).T)
+    assert np.all(np.abs(a.astype(np.float64) - b) <= bound + np.abs(a) * np.finfo(np.float32).eps)
+    ref = (x.astype(np.float64) @ r.astype(np.float64).T)
+    assert np.all(np.abs(a - ref) <= np.abs(ref) * np.finfo(np.float32).eps / 2 + 1e-30)
+
+
+# --------------------------------------------------------------- Q5_K
+def _q5_from_q4(q4, qh):
+    """Q5_K blocks with Q4_K blocks' d, dmin, scales and nibbles, plus qh."""
+    q5 = np.zeros(len(q4), oracle_mod().Q5K_BLOCK)
+    for f in ("d", "dmin", "scales", "qs"):
+        q5[f] = q4[f]
+    q5["qh"] = qh
+    return q5
+
+
+def oracle_mod():
+    from oracle import oracle as O
+
+    return O
+
+
+def test_q5k_without_high_bits_is_q4k(oracle):
+    """qh = 0 makes a Q5_K block the Q4_K block with the same other fields
+    (the Q4_K decoding is pinned above): identical dequantised weights and
+    block integers, and the product within f32 rounding (the mins are
+    accumulated as one scalar instead of four lanes)."""
+    rng = np.random.default_rng(44)
+    n, nb = 6, 4
+    q4 = S.random_blocks(Q4, n * nb, rng).view(oracle.Q4K_BLOCK)
+    q5 = _q5_from_q4(q4, 0)
+    k = 256 * nb
+    assert np.array_equal(oracle.dequantize(S.Q5_K, q5.view(np.uint8), n, k),
+                          oracle.dequantize(Q4, q4.view(np.uint8), n, k))
+    x = S.normal((3, k), rng)
+    q = oracle.quantize_q8k(x[0])
+    for b in range(nb):
+        assert oracle.block_textbook(S.Q5_K, q5[b], q[b]) == oracle.block_textbook(Q4, q4[b], q[b])
+        l5, m5 = oracle.block_lanes(S.Q5_K, q5[b], q[b])
+        l4, m4 = oracle.block_lanes(Q4, q4[b], q[b])
+        assert np.array_equal(l5, l4) and np.array_equal(m5, m4)
+    assert_close_normwise(oracle.matmul(S.Q5_K, q5.view(np.uint8), n, k, x),
+                          oracle.matmul(Q4, q4.view(np.uint8), n, k, x), 1e-6, "Q5_K(qh=0) vs Q4_K")
+
+
+def test_q5k_high_bit_placement(oracle):
+    """Bit b of qh[l] adds 16 * d * scale to weight 64 (b // 2) + 32 (b % 2)
+    + l and to no other weight (ggml's Q5_K layout)."""
+    rng = np.random.default_rng(45)
+    q4 = S.random_blocks(Q4, 1, rng).view(oracle.Q4K_BLOCK)
+    base = oracle.dequantize(S.Q5_K, _q5_from_q4(q4, 0).view(np.uint8), 1, 256)[0].astype(np.float64)
+    d = oracle.f16_to_f32(int(q4["d"][0]))
+    sc = np.zeros(8, np.int64)
+    b12 = q4["scales"][0].astype(np.int64)
+    for s_ in range(4):
+        sc[s_] = b12[s_] & 63
+        sc[s_ + 4] = (b12[s_ + 8] & 15) | ((b12[s_] >> 6) << 4)
+    for bit in range(8):
+        for l in (0, 13, 31):
+            qh = np.zeros(32, np.uint8)
+            qh[l] = 1 << bit
+            got = oracle.dequantize(S.Q5_K, _q5_from_q4(q4, qh).view(np.uint8), 1, 256)[0].astype(np.float64)
+            e = 64 * (bit // 2) + 32 * (bit % 2) + l
+            delta = got - base
+            assert np.count_nonzero(delta) == (1 if sc[bit] else 0)
+            assert abs(delta[e] - 16 * d * sc[bit]) <= 1e-6 * max(1.0, abs(got[e]))
+
+
+def test_q5k_with_unit_scales_is_a_plain_integer_dot(oracle):
+    rng = np.random.default_rng(46)
+    nb, n = 3, 5
+    blocks = np.zeros(n * nb, oracle.Q5K_BLOCK)
+    blocks["d"] = 0x3C00
+    blocks["scales"][:, 0:4] = 1
+    blocks["scales"][:, 8:12] = 0x01
+    blocks["qs"] = rng.integers(0, 256, (n * nb, 128))
+    blocks["qh"] = rng.integers(0, 256, (n * nb, 32))
+    w = blocks.view(np.uint8)
+    x = _integer_row(256 * nb, rng)
+    W = oracle.dequantize(S.Q5_K, w, n, 256 * nb).astype(np.int64)
+    assert W.max() == 31 and W.min() == 0
+    y = oracle.matmul(S.Q5_K, w, n, 256 * nb, x[None, :])[0]
+    assert np.array_equal(y, (W @ x.astype(np.int64)).astype(np.float32))
