@@ -144,6 +144,27 @@ int iq_matmul_ws(iq_weight_t w, const float *x, int64_t m, float *y, void *works
  * (QuantizedMatrix::forward_rows, src/gguf.rs:433-456). */
 int iq_matmul_host(iq_weight_t w, const float *x_host, int64_t m, float *y_host);
 
+/* ---- Greedy selection ----------------------------------------------------- */
+
+/* idx[r] = the index of the largest finite value of logit row r of device
+ * y [m x n] (row-major): among equal values the LAST index (Rust's max_by),
+ * -0 equal to +0, NaN and +-inf skipped; -1 when row r has no finite value
+ * (the reference's "all logits are non-finite" error).  val[r] (device, may
+ * be NULL) receives that logit (NaN when idx is -1).  m <= 65535.
+ * Replaces: sampling::argmax (src/sampling.rs:104-110), the greedy sampler
+ * over the LM head's logits. */
+int iq_argmax_rows(const float *y, int64_t m, int64_t n, int32_t *idx, float *val, iq_stream_t stream);
+
+/* The LM head with greedy selection: idx/val as iq_argmax_rows over
+ * x . W^T, whose logits (bitwise iq_matmul's) stay in the library workspace
+ * and are never handed back -- a greedy decode step reads m indices
+ * instead of m x rows floats.  With a leading_rows matrix it is the
+ * vocab-prefix draft head's selection.
+ * Replaces: lm_head.forward followed by sampling::argmax
+ * (src/qwen/quantized_model.rs:737-743, src/sampling.rs:104-110;
+ * draft head src/qwen/quantized_mtp.rs:142-143). */
+int iq_matmul_argmax(iq_weight_t w, const float *x, int64_t m, int32_t *idx, float *val, iq_stream_t stream);
+
 /* ---- Parity hooks ------------------------------------------------------- */
 
 /* Quantise device x[m x k] into the reference block layouts on the device:

@@ -49,6 +49,8 @@ _SIGNATURES = {
     "iq_matmul_workspace_size": ([P, I64], SZ),
     "iq_matmul_ws": ([P, P, I64, P, P, SZ, P], INT),
     "iq_matmul_host": ([P, P, I64, P], INT),
+    "iq_argmax_rows": ([P, I64, I64, P, P, P], INT),
+    "iq_matmul_argmax": ([P, P, I64, P, P, P], INT),
     "iq_quantize_q8k": ([P, I64, I64, P, P], INT),
     "iq_quantize_q80": ([P, I64, I64, P, P], INT),
     "iq_block_sums": ([P, P, I64, P, P, P, P], INT),

@@ -3,6 +3,7 @@
 // dispatch to the kernels.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -443,6 +444,41 @@ IQ_API int iq_prefill_block_sums(iq_weight_t w, const float* x, int64_t m, float
     if (int rc = lease.acquire(prefill_workspace_size(view_of(w), m), (hipStream_t)stream)) return rc;
     hipError_t e = launch_prefill(view_of(w), x, w->cols, m, y, w->rows, lease.ptr(), isum, msum, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return IQ_OK;
+}
+
+IQ_API int iq_argmax_rows(const float* y, int64_t m, int64_t n, int32_t* idx, float* val, iq_stream_t stream) {
+    if (m < 0 || n < 0) return fail(IQ_ERR_SHAPE, "negative logit shape [%lld, %lld]", (long long)m, (long long)n);
+    if (m == 0) return IQ_OK;
+    if (!y || !idx) return fail(IQ_ERR_INVALID, "null logits or index buffer");
+    if (n == 0 || n > INT32_MAX || m > 65535)
+        return fail(IQ_ERR_SHAPE, "argmax covers 1..%d logits per row and up to 65535 rows (got [%lld, %lld])",
+                    INT32_MAX, (long long)m, (long long)n);
+    hipStream_t s = (hipStream_t)stream;
+    WsLease lease;
+    if (int rc = lease.acquire(argmax_workspace_size(m, n), s)) return rc;
+    hipError_t e = launch_argmax(y, m, n, n, idx, val, lease.ptr(), s);
+    if (e != hipSuccess) return hip_fail(e, "argmax launch");
+    return IQ_OK;
+}
+
+IQ_API int iq_matmul_argmax(iq_weight_t w, const float* x, int64_t m, int32_t* idx, float* val, iq_stream_t stream) {
+    if (int rc = check_weight(w)) return rc;
+    if (m < 0) return fail(IQ_ERR_SHAPE, "negative input row count %lld", (long long)m);
+    if (m == 0) return IQ_OK;
+    if (!x || !idx) return fail(IQ_ERR_INVALID, "null input or index buffer");
+    if (m > 65535) return fail(IQ_ERR_SHAPE, "argmax covers up to 65535 rows (got %lld)", (long long)m);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t yb = ((size_t)(m * w->rows) * 4 + 255) & ~(size_t)255;
+    const size_t ab = (argmax_workspace_size(m, w->rows) + 255) & ~(size_t)255;
+    WsLease lease;
+    if (int rc = lease.acquire(yb + ab + matmul_ws_bytes(w, m), s)) return rc;
+    uint8_t* base = (uint8_t*)lease.ptr();
+    float* y = (float*)base;
+    hipError_t e = launch_path(w, x, m, y, base + yb + ab, IQ_PATH_AUTO, nullptr, nullptr, s);
+    if (e != hipSuccess) return hip_fail(e, "matmul launch");
+    e = launch_argmax(y, m, w->rows, w->rows, idx, val, base + yb, s);
+    if (e != hipSuccess) return hip_fail(e, "argmax launch");
     return IQ_OK;
 }
 

@@ -82,4 +82,11 @@ hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, i
 hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                                  void* ws, hipStream_t s);
 
+// Greedy selection over logit rows y [m][ldy] (iq_argmax.hip): idx[r] the
+// last index of the largest finite value of row r (-1 when none is finite),
+// val[r] (may be null) that value.  `ws` holds argmax_workspace_size bytes.
+size_t argmax_workspace_size(int64_t m, int64_t n);
+hipError_t launch_argmax(const float* y, int64_t m, int64_t n, int64_t ldy, int32_t* idx, float* val, void* ws,
+                         hipStream_t s);
+
 }  // namespace iq

@@ -156,6 +156,21 @@ class QuantizedMatrix:
         check(lib().iq_matmul_via(self._h, xs.data_ptr(), m, y.data_ptr(), path, _stream()))
         return y
 
+    def forward_argmax(self, xs):
+        """Greedy token selection on the product (iq_matmul_argmax): per
+        input row the last index of the largest finite logit and that
+        logit (src/qwen/quantized_model.rs:737-743 + src/sampling.rs:
+        104-110), without materialising the logits.  Index -1: the row had
+        no finite logit."""
+        import torch
+
+        xs = self._validated_input(xs)
+        m = xs.numel() // self._cols
+        idx = torch.empty(*xs.shape[:-1], dtype=torch.int32, device=xs.device)
+        val = torch.empty(*xs.shape[:-1], dtype=torch.float32, device=xs.device)
+        check(lib().iq_matmul_argmax(self._h, xs.data_ptr(), m, idx.data_ptr(), val.data_ptr(), _stream()))
+        return idx, val
+
     def forward_into(self, x, y, path: int = 0) -> None:
         """Raw call: contiguous device f32 x [m, cols] into y [m, rows]
         (`path` as forward_via; 0 = the dispatch)."""
@@ -218,6 +233,24 @@ class QuantizedMatrix:
         check(lib().iq_prefill_block_sums(self._h, xs.data_ptr(), m, y.data_ptr(), isum.data_ptr(), msum.data_ptr(),
                                           _stream()))
         return y, isum, msum
+
+
+def argmax(logits):
+    """sampling::argmax (src/sampling.rs:104-110) over the last dimension of
+    device f32 logits: (index, value) per row, index -1 when a row has no
+    finite value."""
+    import torch
+
+    _ensure_init()
+    if not logits.is_cuda:
+        raise QgemmError(_lib.IQ_ERR_INVALID, "argmax logits must be a device (HBM) tensor")
+    y = logits.to(torch.float32).contiguous()
+    n = y.shape[-1]
+    m = y.numel() // n if n else 0
+    idx = torch.empty(y.shape[:-1], dtype=torch.int32, device=y.device)
+    val = torch.empty(y.shape[:-1], dtype=torch.float32, device=y.device)
+    check(lib().iq_argmax_rows(y.data_ptr(), m, n, idx.data_ptr(), val.data_ptr(), _stream()))
+    return idx, val
 
 
 def quantize_q8k(xs):
