@@ -64,6 +64,8 @@ enum iq_path {
 
 typedef struct iq_weight *iq_weight_t;
 typedef struct iq_moe *iq_moe_t;
+typedef struct iq_gguf *iq_gguf_t;
+typedef struct iq_experts *iq_experts_t;
 typedef void *iq_stream_t;
 
 /* Library version string. */
@@ -269,6 +271,62 @@ int iq_moe_forward_timed(iq_moe_t moe, const float *x, const float *router_logit
  * Replaces: the per-stage timers of QuantizedMoeTimings
  * (src/qwen/quantized_moe.rs:67-96). */
 int iq_moe_forward_stage(iq_moe_t moe, int stage, iq_stream_t stream);
+
+/* ---- GGUF checkpoints and expert residency ------------------------------- */
+
+/* Open a GGUF (v2/v3, little endian) checkpoint and parse its header,
+ * metadata and tensor infos on the host (no device work).  Malformed or
+ * truncated files are refused with IQ_ERR_SHAPE.
+ * Replaces: GgufCheckpoint::open (src/gguf.rs:1200-1232, candle gguf_file). */
+int iq_gguf_open(const char *path, iq_gguf_t *out);
+int iq_gguf_close(iq_gguf_t g);
+
+/* Tensor listing: count, the name of tensor `index` (file's info order). */
+int64_t iq_gguf_tensor_count(iq_gguf_t g);
+const char *iq_gguf_tensor_name(iq_gguf_t g, int64_t index);
+
+/* dtype (GGML type id), dimension count, dims outermost first as the
+ * reference's shapes read ([experts, rows, columns] for expert tensors;
+ * unused trailing entries 0), absolute file offset and byte size (0 for a
+ * dtype this library cannot size) of tensor `name`.
+ * Replaces: GgufCheckpoint::tensor_info (src/gguf.rs:1236-1262). */
+int iq_gguf_tensor_info(iq_gguf_t g, const char *name, int *dtype, int *n_dims, int64_t dims[4],
+                        uint64_t *file_offset, uint64_t *nbytes);
+
+/* Integer (or bool / float truncated) and string metadata values; the
+ * string is owned by the handle, NULL when absent or not a string. */
+int iq_gguf_meta_int(iq_gguf_t g, const char *key, int64_t *value);
+const char *iq_gguf_meta_str(iq_gguf_t g, const char *key);
+
+/* A 2-D quantised tensor streamed from the file into HBM as a matrix.
+ * Replaces: GgufCheckpoint::load_matrix (src/gguf.rs:1234). */
+int iq_gguf_load_matrix(iq_gguf_t g, const char *name, iq_weight_t *out);
+
+/* Raw bytes of tensor `name` into device memory (capacity >= its size),
+ * e.g. the F32 router and shared-expert selector; synchronises `stream`.
+ * Replaces: TensorInfo::read as GgufCheckpoint uses it for F32 tensors
+ * (src/gguf.rs:1263-1274). */
+int iq_gguf_upload_tensor(iq_gguf_t g, const char *name, void *device_dst, size_t capacity, iq_stream_t stream);
+
+/* Make every routed expert of layers [0, n_layers) resident in HBM: the
+ * blk.N.ffn_{gate,up,down}_exps.weight tensors are read in file order
+ * (sequential I/O through pinned staging, overlapped with the copies),
+ * each layer's gate and up placed side by side as the pair one product
+ * reads, and checked for pairing (same dtype and shape) and for down's
+ * transposed shape.  Owned by the handle until iq_experts_free.
+ * Replaces: warm_all_experts with a pinned expert cache
+ * (src/residency.rs:39-131) and GgufCheckpoint::expert_tensor /
+ * expert_pair (src/gguf.rs:1283-1360). */
+int iq_gguf_load_experts(iq_gguf_t g, int64_t n_layers, iq_experts_t *out);
+int iq_experts_free(iq_experts_t r);
+size_t iq_experts_bytes(iq_experts_t r); /* file bytes made resident */
+
+/* Fill the routed-expert fields of an iq_moe_desc (hidden, inter,
+ * n_experts, dtypes, gate/up/down pointers and sizes) for one resident
+ * layer; the caller adds top_k, normalize, the shared expert, selector
+ * and router, then calls iq_moe_create.  The pointers stay valid until
+ * iq_experts_free. */
+int iq_experts_layer(iq_experts_t r, int64_t layer, iq_moe_desc *desc);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,21 @@ _SIGNATURES = {
     "iq_quantize_q80": ([P, I64, I64, P, P], INT),
     "iq_block_sums": ([P, P, I64, P, P, P, P], INT),
     "iq_prefill_block_sums": ([P, P, I64, P, P, P, P], INT),
+    "iq_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(P)], INT),
+    "iq_gguf_close": ([P], INT),
+    "iq_gguf_tensor_count": ([P], I64),
+    "iq_gguf_tensor_name": ([P, I64], ctypes.c_char_p),
+    "iq_gguf_tensor_info": ([P, ctypes.c_char_p, ctypes.POINTER(INT), ctypes.POINTER(INT),
+                             ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+                            INT),
+    "iq_gguf_meta_int": ([P, ctypes.c_char_p, ctypes.POINTER(I64)], INT),
+    "iq_gguf_meta_str": ([P, ctypes.c_char_p], ctypes.c_char_p),
+    "iq_gguf_load_matrix": ([P, ctypes.c_char_p, ctypes.POINTER(P)], INT),
+    "iq_gguf_upload_tensor": ([P, ctypes.c_char_p, P, SZ, P], INT),
+    "iq_gguf_load_experts": ([P, I64, ctypes.POINTER(P)], INT),
+    "iq_experts_free": ([P], INT),
+    "iq_experts_bytes": ([P], SZ),
+    "iq_experts_layer": ([P, I64, P], INT),
     "iq_moe_create": ([P, ctypes.POINTER(P)], INT),
     "iq_moe_destroy": ([P], INT),
     "iq_moe_forward": ([P, P, P, I64, P, P, P, P], INT),

@@ -49,5 +49,9 @@ class WsLease {
 };
 int check_weight(const iq_weight* w);
 WeightView view_of(const iq_weight* w);
+// Shape and size checks of a GGUF matrix (QuantizedMatrix::new); row bytes out.
+int check_matrix(int dtype, int64_t rows, int64_t cols, size_t nbytes, int64_t* row_bytes);
+// A library-owned device matrix of that shape (256 zeroed bytes past the end).
+int alloc_weight(int dtype, int64_t rows, int64_t cols, int64_t row_bytes, iq_weight** out);
 
 }  // namespace iq

@@ -75,6 +75,34 @@ class QuantizedMoeLayer:
         check(lib().iq_moe_create(ctypes.byref(desc), ctypes.byref(h)))
         self._h = h
 
+    @classmethod
+    def from_desc(cls, routed, top_k: int, normalize: bool, shared, selector, router, keepalive) -> "QuantizedMoeLayer":
+        """A layer over routed experts already resident (an iq_moe_desc with
+        the routed fields filled, e.g. from ExpertResidency.desc), plus the
+        shared expert's three QuantizedMatrix objects, its f32 selector and
+        the optional f32 router (device tensors).  `keepalive` holds
+        whatever owns those device bytes."""
+        import torch
+
+        _ensure_init()
+        obj = object.__new__(cls)
+        obj.hidden, obj.inter, obj.n_experts, obj.top_k = routed.hidden, routed.inter, routed.n_experts, top_k
+        obj.device = torch.cuda.current_device()
+        obj._check_device(selector=selector, router=router)
+        obj._keep = keepalive
+        obj.has_router = router is not None
+        d = MoeDesc.from_buffer_copy(routed)
+        d.top_k, d.normalize = top_k, int(normalize)
+        if shared:
+            d.shared_gate_dtype, d.shared_down_dtype = shared[0].ggml_dtype, shared[2].ggml_dtype
+            d.shared_gate, d.shared_up, d.shared_down = (m.device_ptr() for m in shared)
+            d.selector = selector.data_ptr()
+        d.router = None if router is None else router.data_ptr()
+        h = ctypes.c_void_p()
+        check(lib().iq_moe_create(ctypes.byref(d), ctypes.byref(h)))
+        obj._h = h
+        return obj
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and _lib._lib is not None:
