@@ -141,6 +141,20 @@ size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m);
 int iq_matmul_ws(iq_weight_t w, const float *x, int64_t m, float *y, void *workspace, size_t workspace_bytes,
                  iq_stream_t stream);
 
+/* iq_matmul that allocates nothing: its workspace is a fixed 16 MiB device
+ * array per GPU (iq_matmul_noalloc_max_bytes()), resolved once per device
+ * at iq_init (or at the first call on a device) and held until the process
+ * ends.  Calls whose workspace would exceed it fail with IQ_ERR_RANGE
+ * before any launch (iq_matmul_workspace_size tells the need).  Results
+ * are bitwise iq_matmul's.  Every call on one GPU shares that array, so
+ * calls that overlap in time on one device (other streams or threads)
+ * race; serialise them.  Safe under graph capture: no allocation, no
+ * memset, no synchronisation.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (HIP graph capture, allocation-free serving loops). */
+int iq_matmul_noalloc(iq_weight_t w, const float *x, int64_t m, float *y, iq_stream_t stream);
+size_t iq_matmul_noalloc_max_bytes(void);
+
 /* iq_matmul for host x and y (copies in, computes, copies out, synchronises).
  * Replaces: the same entries, for a caller holding host slices
  * (QuantizedMatrix::forward_rows, src/gguf.rs:433-456). */

@@ -46,6 +46,8 @@ _SIGNATURES = {
     "iq_weights_leading_rows": ([P, I64, ctypes.POINTER(P)], INT),
     "iq_matmul": ([P, P, I64, P, P], INT),
     "iq_matmul_via": ([P, P, I64, P, INT, P], INT),
+    "iq_matmul_noalloc": ([P, P, I64, P, P], INT),
+    "iq_matmul_noalloc_max_bytes": ([], SZ),
     "iq_matmul_workspace_size": ([P, I64], SZ),
     "iq_matmul_ws": ([P, P, I64, P, P, SZ, P], INT),
     "iq_matmul_host": ([P, P, I64, P], INT),

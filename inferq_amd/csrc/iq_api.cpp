@@ -110,6 +110,37 @@ int WsLease::acquire(size_t bytes, hipStream_t stream) {
     return IQ_OK;
 }
 
+// ---- allocation-free products (iq_matmul_noalloc) ----
+// A fixed device array serves as the workspace of iq_matmul_noalloc, for
+// callers that must not allocate (graph capture, serving loops).  Each
+// device holds its own copy for the life of the process; its address on a
+// device comes from hipGetSymbolAddress with that device current (the
+// array's name is not a device address in host code).  Every call on a
+// device shares its copy: such calls must not overlap in time on one device.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device, null until resolved
+}  // namespace
+
+// Resolve (once per device) the current device's address of `scratch`.
+int scratch_ptr(void** out) {
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((size_t)dev >= g_scratch_ptr.size()) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress (scratch)");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return IQ_OK;
+}
+
 int check_weight(const iq_weight* w) {
     if (!w || !w->dev) return fail(IQ_ERR_INVALID, "null quantized matrix handle");
     return IQ_OK;
@@ -270,7 +301,8 @@ IQ_API int iq_init(int device) {
     if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(IQ_ERR_HIP, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
-    return IQ_OK;
+    void* sp;
+    return scratch_ptr(&sp);  // set-up of the allocation-free entry on this device
 }
 
 IQ_API int iq_weights_upload(const void* host_bytes, size_t nbytes, int dtype, int64_t rows, int64_t cols,
@@ -376,6 +408,28 @@ IQ_API int iq_matmul(iq_weight_t w, const float* x, int64_t m, float* y, iq_stre
 IQ_API int iq_matmul_via(iq_weight_t w, const float* x, int64_t m, float* y, int path, iq_stream_t stream) {
     return matmul_impl(w, x, m, y, nullptr, 0, path, nullptr, nullptr, (hipStream_t)stream);
 }
+
+IQ_API int iq_matmul_noalloc(iq_weight_t w, const float* x, int64_t m, float* y, iq_stream_t stream) {
+    if (int rc = check_weight(w)) return rc;
+    if (m < 0) return fail(IQ_ERR_SHAPE, "negative input row count %lld", (long long)m);
+    if (m == 0) return IQ_OK;
+    if (!x || !y) return fail(IQ_ERR_INVALID, "null input or output pointer");
+    const size_t need = matmul_ws_bytes(w, m);
+    if (need > kScratchBytes)
+        return fail(IQ_ERR_RANGE,
+                    "%lld input rows of a [%lld, %lld] %s matrix need %zu bytes of scratch; iq_matmul_noalloc has %zu "
+                    "(use iq_matmul or iq_matmul_ws, or split the rows)",
+                    (long long)m, (long long)w->rows, (long long)w->cols, dtype_name(w->dtype), need, kScratchBytes);
+    void* ws;
+    if (int rc = scratch_ptr(&ws)) return rc;
+    // every kernel of the dispatch writes the scratch it reads (quantised
+    // activations, scales, sums) before reading it: nothing needs clearing
+    const hipError_t e = launch_path(w, x, m, y, ws, IQ_PATH_AUTO, nullptr, nullptr, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "matmul launch");
+    return IQ_OK;
+}
+
+IQ_API size_t iq_matmul_noalloc_max_bytes(void) { return kScratchBytes; }
 
 IQ_API size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m) {
     if (!w || m <= 0) return 0;
