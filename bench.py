@@ -4,16 +4,24 @@
 Headline: one Qwen3.6-35B-A3B-shaped MoE
 sublayer at M=1 -- hidden 2048, 256 experts of [512 x 2048] Q4_K gate/up and
 [2048 x 512] Q6_K down, top-8 routing plus one shared expert.  A step is one
-layer call (routing, grouped gate/up + SwiGLU, down + ordered combine +
-shared expert).  Steps rotate over 40 resident layers (~21 GB of experts, as
-the real model's residency) with fresh N(0,1) inputs and router logits, so
-weights come from HBM, not from the 256 MB Infinity Cache.
+layer call (routing, gate/up + SwiGLU, down + ordered combine + shared
+expert).  Steps rotate over --layers resident layers (default 72, about
+37 GB of experts; the model has 40) with fresh N(0,1) inputs and router
+logits, so weights come from HBM, not from the 256 MB Infinity Cache.
+
+Protocol: W eager warm-up calls; then captured HIP graphs replayed
+round-robin --reps times each, every replay timed with HIP events on the
+launch stream: three graphs of exactly --steps layer calls over disjoint
+layer ranges (value and ms_per_step from the median replay, best reported
+beside it), each MoE kernel alone over >= 512 MiB of distinct weights (the
+roofline's per-launch duration), and a MALL-resident graph (one layer, one
+input) reported separately.
 
 Printed JSON line: value = algorithmic HBM bytes per layer / wall time per
 layer (GB/s); roofline = the dominant kernel's algorithmic bytes / its own
-average duration (HIP events on the launch stream); cpu_baseline = the
-oracle's AVX2 restatement of the reference's CPU kernels on this host's
-cores, on a bounded sample of the same workload.
+median duration per launch; cpu_baseline = the oracle's AVX2 restatement of
+the reference's CPU kernels, one pinned thread per physical core, on a
+bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -157,46 +165,86 @@ def time_moe(layers, xs, logits, out, steps, warmup, hip, stream):
     return wall, per
 
 
-def time_moe_graph(layers, xs, logits, out, steps, warmup, hip):
-    """The same `steps` layer calls captured once in a HIP graph and
-    replayed: wall ms per layer call without host submission gaps; then,
-    for each of the two kernels, a graph of `steps` launches of that kernel
-    alone (each layer re-running its last call's stage), giving its average
-    duration per launch (graph node gaps included)."""
-    import torch
+MALL_BYTES = 256 << 20          # MI355X Infinity Cache
+MIN_STREAM_BYTES = 2 * MALL_BYTES  # distinct bytes a timed graph must stream
 
+
+class GraphSet:
+    """Captured graphs replayed round-robin: every graph is replayed `reps`
+    times, interleaved with the others, each replay timed with HIP events on
+    the capture stream.  Reports best and median per graph."""
+
+    def __init__(self, hip):
+        import torch
+
+        self.hip = hip
+        self.cap = torch.cuda.Stream()
+        self.graphs = {}
+
+    def add(self, name, capture, units):
+        """capture(): the launches of one replay; `units` = the steps (or
+        launches) one replay performs."""
+        import torch
+
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(self.cap):
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=self.cap):
+                capture()
+        self.graphs[name] = (g, units)
+
+    def run(self, reps):
+        import torch
+
+        t0, t1 = self.hip.events(2)
+        times = {k: [] for k in self.graphs}
+        with torch.cuda.stream(self.cap):
+            for g, _ in self.graphs.values():  # one untimed replay each
+                g.replay()
+            torch.cuda.synchronize()
+            for _ in range(reps):
+                for name, (g, units) in self.graphs.items():
+                    torch.cuda.synchronize()
+                    self.hip.record(t0, self.cap.cuda_stream)
+                    g.replay()
+                    self.hip.record(t1, self.cap.cuda_stream)
+                    torch.cuda.synchronize()
+                    times[name].append(self.hip.ms(t0, t1) / units)
+        self.hip.destroy([t0, t1])
+        return {k: {"best_ms": min(v), "median_ms": float(np.median(v)), "reps": len(v)} for k, v in times.items()}
+
+
+def moe_protocol(layers, xs, logits, out, steps, reps, hip, kernel_bytes):
+    """The headline's timed graphs.
+
+    * layer_a/b/c: three graphs of exactly `steps` layer calls each, over
+      disjoint ranges of the rotated layers with fresh inputs per call;
+      replayed round-robin, so a graph's bytes were last touched two other
+      graphs ago (>= 2x the MALL for any steps >= 14) and no replay reads
+      its weights from the Infinity Cache.
+    * gate_up / down: each kernel alone (iq_moe_forward_stage re-runs a
+      layer's last call), one launch per layer over as many layers as make
+      >= 512 MiB of distinct weight bytes.
+    * mall_resident: `steps` calls of one layer on one input (every replay
+      after the first reads its 18 MB from the Infinity Cache), reported
+      separately.
+    """
     n = len(layers)
-    cap = torch.cuda.Stream()
-    t0, t1 = hip.events(2)
-
-    def replay(capture):
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=cap):
-            capture()
-        graph.replay()  # warm
-        torch.cuda.synchronize()
-        hip.record(t0, cap.cuda_stream)
-        graph.replay()
-        hip.record(t1, cap.cuda_stream)
-        torch.cuda.synchronize()
-        return hip.ms(t0, t1) / steps
-
-    with torch.cuda.stream(cap):
-        for i in range(warmup):
-            layers[i % n][0].forward_into(xs[i], logits[i], out)
-        torch.cuda.synchronize()
-
-        def full():
+    gs = GraphSet(hip)
+    for j, name in enumerate(("layer_a", "layer_b", "layer_c")):
+        def cap(j=j):
             for s_ in range(steps):
-                i = warmup + s_
-                layers[i % n][0].forward_into(xs[i], logits[i], out)
-
-        wall = replay(full)
-        per = {}
-        for stage, name in ((1, "gate_up"), (2, "down")):
-            per[name] = replay(lambda st=stage: [layers[(warmup + s_) % n][0].forward_stage(st) for s_ in range(steps)])
-    hip.destroy([t0, t1])
-    return wall, per
+                i = j * steps + s_
+                layers[i % n][0].forward_into(xs[i % len(xs)], logits[i % len(logits)], out)
+        gs.add(name, cap, steps)
+    per_kernel = {}
+    for stage, name in ((1, "gate_up"), (2, "down")):
+        launches = max(steps, -(-MIN_STREAM_BYTES // kernel_bytes[name]))
+        per_kernel[name] = launches
+        gs.add(name, lambda st=stage, L_=launches: [layers[i % n][0].forward_stage(st) for i in range(L_)], launches)
+    gs.add("mall_resident", lambda: [layers[0][0].forward_into(xs[0], logits[0], out) for _ in range(steps)], steps)
+    res = gs.run(reps)
+    return res, per_kernel
 
 
 def time_graph(fn, iters, hip, warmup=3):
@@ -236,13 +284,29 @@ def host_layer(t):
     return d
 
 
-def cpu_threads():
-    n = os.cpu_count() or 1
+def physical_cpus():
+    """One logical CPU per physical core among the CPUs this process may run
+    on (the reference sizes its pool to the physical cores,
+    src/threading.rs:75,86-91), and all of them."""
     try:
-        n = len(os.sched_getaffinity(0))
+        cpus = sorted(os.sched_getaffinity(0))
     except AttributeError:
-        pass
-    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n)), 16))
+        cpus = list(range(os.cpu_count() or 1))
+    seen, pick = set(), []
+    for c in cpus:
+        try:
+            topo = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            key = (open(topo + "physical_package_id").read().strip(), open(topo + "core_id").read().strip())
+        except OSError:
+            key = c
+        if key not in seen:
+            seen.add(key)
+            pick.append(c)
+    return pick, cpus
+
+
+def cpu_threads():
+    return len(physical_cpus()[0])
 
 
 def cpu_model():
@@ -262,8 +326,8 @@ def secondary(args, hip, stream, device, layers):
     from inferq_amd import qgemm, synth
 
     extra = {}
-    # config 1: Q8_0 [4096 x 2048] matvec, rotated over copies beyond the MALL
-    copies = 64
+    # config 1: Q8_0 [4096 x 2048] matvec, rotated over copies beyond 2x the MALL
+    copies = -(-MIN_STREAM_BYTES // (4096 * 2048 // 32 * 34))
     mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q8_0, 4096, 2048, device, 50 + c),
                                        synth.Q8_0, 4096, 2048) for c in range(copies)]
     x = torch.randn(2048, 2048, device=device).reshape(-1, 1, 2048)
@@ -303,7 +367,7 @@ def secondary(args, hip, stream, device, layers):
     # configs 2/3: dense projections beside the MoE (attention q/gate, k, v, o),
     # one call each per step, rotated over copies beyond the MALL
     shapes = (("q_gate", 8192, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 4096))
-    copies = 8
+    copies = -(-MIN_STREAM_BYTES // sum(r * c // 256 * 144 for _, r, c in shapes))
     proj = [[qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, n, k, device, 700 + 10 * c + j),
                                         synth.Q4_K, n, k) for j, (_, n, k) in enumerate(shapes)] for c in range(copies)]
     pbytes = sum(p.storage_bytes() for p in proj[0])
@@ -338,7 +402,7 @@ def prefill(args, hip, stream, device):
 
     res = {}
     for n, k in ((8192, 2048), (2048, 4096)):
-        copies = 8
+        copies = -(-MIN_STREAM_BYTES // (n * k // 256 * 144))
         mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, n, k, device, 90 + c), synth.Q4_K,
                                            n, k) for c in range(copies)]
         x = torch.randn(256, k, device=device)
@@ -372,7 +436,7 @@ def decode_sweep(args, hip, device, layers):
 
     from inferq_amd import qgemm, synth
 
-    n = len(layers)
+    n = min(40, len(layers))  # the model's layer count
     attn = ((8192, 2048), (512, 2048), (512, 2048), (2048, 4096))
     delta = ((12288, 2048), (64, 2048), (2048, 4096))
     is_attn = [(li + 1) % 4 == 0 for li in range(n)]
@@ -449,7 +513,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--layers", type=int, default=40, help="resident MoE layers rotated over (40 = the model)")
+    ap.add_argument("--layers", type=int, default=72,
+                    help="resident MoE layers rotated over: the model has 40; 72 make each per-kernel graph stream "
+                         ">= 2x the 256 MB Infinity Cache of distinct weights")
+    ap.add_argument("--reps", type=int, default=7, help="interleaved timed replays of every graph (best and median)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--no-parity", action="store_true")
@@ -484,7 +551,7 @@ def main():
     torch.cuda.synchronize()
     log(f"built {args.layers} resident MoE layers in {time.time() - t:.1f}s")
 
-    total = args.warmup + args.steps
+    total = args.warmup + 3 * args.steps
     g = torch.Generator(device=device)
     g.manual_seed(args.seed)
     xs = torch.randn(total, 1, H, device=device, generator=g)
@@ -492,17 +559,21 @@ def main():
     out = torch.empty(1, H, device=device)
 
     eager_ms, eager_per = time_moe(layers, xs, logits, out, args.steps, args.warmup, hip, stream)
-    wall_ms, per = time_moe_graph(layers, xs, logits, out, args.steps, args.warmup, hip)
     kb = moe_kernel_bytes(1, TOPK)
+    # the protocol's graphs read inputs past the warm-up ones
+    res, per_kernel = moe_protocol(layers, xs[args.warmup:], logits[args.warmup:], out, args.steps, args.reps, hip, kb)
+    layer_runs = [res[k] for k in ("layer_a", "layer_b", "layer_c")]
+    wall_ms = float(np.median([r["median_ms"] for r in layer_runs]))
+    best_ms = min(r["best_ms"] for r in layer_runs)
     gu, dn = expert_bytes()
     layer_bytes = 9 * (gu + dn) + H * 4 + H * 4 + E * 4 + H * 4  # weights + selector, x, logits, out
     value = layer_bytes / (wall_ms * 1e-3) / 1e9
-    avg = {k: float(v) for k, v in per.items()}
+    avg = {k: res[k]["median_ms"] for k in ("gate_up", "down")}
     dom = max(avg, key=avg.get)
     achieved = kb[dom] / (avg[dom] * 1e-3) / 1e9
-    log(f"MoE layer M=1: {wall_ms * 1e3:.2f} us/layer (graph replay), {value:.0f} GB/s; "
-        f"eager {eager_ms * 1e3:.2f} us/layer; kernels alone (us per launch in a graph): "
-        + ", ".join(f"{k} {v * 1e3:.2f}" for k, v in avg.items()))
+    log(f"MoE layer M=1: median {wall_ms * 1e3:.2f} us/layer (best {best_ms * 1e3:.2f}), {value:.0f} GB/s; "
+        f"MALL-resident {res['mall_resident']['median_ms'] * 1e3:.2f} us; eager {eager_ms * 1e3:.2f} us/layer; "
+        "kernels alone (median us per launch): " + ", ".join(f"{k} {v * 1e3:.2f}" for k, v in avg.items()))
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -524,15 +595,21 @@ def main():
         "data": "synthetic: random GGUF blocks, N(0,1) activations and router logits",
         "config": {"workload": "configs[1]: Qwen3.6-35B-A3B-shaped MoE layer at M=1 (256 experts, top-8 + 1 shared, "
                                "hidden 2048, moe_intermediate 512, Q4_K gate/up, Q6_K down)",
-                   "layers_rotated": args.layers,
+                   "layers_rotated": args.layers, "model_layers": 40,
                    "resident_expert_bytes": args.layers * E * (gu + dn),
                    "algorithmic_bytes_per_layer": layer_bytes},
         "us_per_layer": round(wall_ms * 1e3, 3),
-        "timing": "HIP graph of the timed steps replayed once, HIP events on the launch stream; per-kernel: graph of "
-                  "the timed steps' launches of that kernel alone",
+        "us_per_layer_best": round(best_ms * 1e3, 3),
+        "timing": (f"three HIP graphs of exactly {args.steps} layer calls over disjoint rotated layers, replayed "
+                   f"round-robin with the per-kernel and MALL graphs, {args.reps} timed replays each (HIP events on "
+                   "the launch stream): value and ms_per_step from the median replay; per-kernel graphs launch one "
+                   "kernel per layer over >= 512 MiB of distinct weights"),
+        "mall_resident_us_per_layer": round(res["mall_resident"]["median_ms"] * 1e3, 3),
         "eager_us_per_layer": round(eager_ms * 1e3, 3),
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "kernel_us": {k: round(v * 1e3, 3) for k, v in avg.items()},
+        "kernel_us_best": {k: round(res[k]["best_ms"] * 1e3, 3) for k in ("gate_up", "down")},
+        "kernel_graph_launches": per_kernel,
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": kb[dom], "avg_us": round(avg[dom] * 1e3, 3)},
@@ -553,22 +630,33 @@ def main():
                                 float((h.view(np.uint32) == ref.view(np.uint32)).mean()), "tolerance": 1e-4}
         log(f"parity vs oracle: {result['parity']}")
         if args.cpu_seconds > 0:
-            nt = cpu_threads()
+            phys, allowed = physical_cpus()
+            nt = len(phys)
             rng = np.random.default_rng(5)
             xh = rng.standard_normal((64, 1, H), dtype=np.float32)
             lh = rng.standard_normal((64, 1, E), dtype=np.float32)
             impl = 1 if O.have_avx2() else 0
-            O.moe_forward(hl, xh[0], lh[0], mode=0, impl=impl, nthreads=nt)
-            n, t0 = 0, time.perf_counter()
-            while time.perf_counter() - t0 < args.cpu_seconds:
-                O.moe_forward(hl, xh[n % 64], lh[n % 64], mode=0, impl=impl, nthreads=nt)
-                n += 1
-            dt = (time.perf_counter() - t0) / n
+            # one pool thread per physical core, pinned (the caller runs on the first)
+            O.pool_pin(phys)
+            saved = os.sched_getaffinity(0)
+            os.sched_setaffinity(0, {phys[0]})
+            try:
+                O.moe_forward(hl, xh[0], lh[0], mode=0, impl=impl, nthreads=nt)
+                n, t0 = 0, time.perf_counter()
+                while time.perf_counter() - t0 < args.cpu_seconds:
+                    O.moe_forward(hl, xh[n % 64], lh[n % 64], mode=0, impl=impl, nthreads=nt)
+                    n += 1
+                dt = (time.perf_counter() - t0) / n
+            finally:
+                os.sched_setaffinity(0, saved)
+                O.pool_pin([])
             result["cpu_baseline"] = {
-                "value": round(layer_bytes / dt / 1e9, 2), "unit": "GB/s", "cores": nt,
+                "value": round(layer_bytes / dt / 1e9, 2), "unit": "GB/s", "cores": nt, "threads": nt,
+                "host_cpus_allowed": len(allowed), "pinned": True,
                 "kind": "port", "us_per_layer": round(dt * 1e6, 1),
                 "sample": f"{n} MoE-layer calls (M=1, token-major, {'AVX2' if impl else 'scalar'} restatement of "
-                          f"the reference kernels) on one resident layer, {nt} threads, {cpu_model()}",
+                          f"the reference kernels) on one resident layer, {nt} threads pinned one per physical "
+                          f"core of the {len(allowed)} CPUs this process may use, {cpu_model()}",
             }
             log(f"cpu baseline: {result['cpu_baseline']}")
 

@@ -114,6 +114,10 @@ int or_dequantize(int dtype, const void *blocks, size_t n_rows, size_t cols, flo
 int or_matmul(int dtype, const void *w, size_t n_rows, size_t cols,
               const float *x, size_t m, float *y, int impl, int nthreads);
 
+/* Pin the row-spread pool: worker t (t >= 1) runs on cpus[t % n]; the
+ * calling thread is worker 0 and pins itself.  n = 0 unpins new workers. */
+void or_pool_pin(const int *cpus, int n);
+
 /* tiled_multi_row: the same product, in 16-row tiles never leaving one row
  * alone (src/gguf.rs:493-520). */
 int or_matmul_tiled(int dtype, const void *w, size_t n_rows, size_t cols,

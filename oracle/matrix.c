@@ -1,3 +1,4 @@
+#define _GNU_SOURCE
 /*
  * matrix.c -- TEST INFRASTRUCTURE (parity oracle and timed CPU baseline, see
  * iq_oracle.h).
@@ -73,6 +74,28 @@ static pthread_mutex_t sleep_mu = PTHREAD_MUTEX_INITIALIZER;
 static pthread_cond_t sleep_cv = PTHREAD_COND_INITIALIZER;
 static atomic_int sleepers;
 
+/* Optional pinning of pool threads (the CPU baseline pins one thread per
+ * physical core, as the reference's pool does by default): worker t runs on
+ * pin_cpus[t % pin_n]; worker 0 is the caller, which pins itself. */
+static int pin_cpus[OR_MAX_THREADS];
+static int pin_n;
+
+static void pin_thread(pthread_t th, int t) {
+    if (pin_n <= 0) return;
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    CPU_SET(pin_cpus[t % pin_n], &set);
+    pthread_setaffinity_np(th, sizeof set, &set);
+}
+
+void or_pool_pin(const int *cpus, int n) {
+    pthread_mutex_lock(&pool_mu);
+    pin_n = n < 0 ? 0 : (n > OR_MAX_THREADS ? OR_MAX_THREADS : n);
+    for (int i = 0; i < pin_n; i++) pin_cpus[i] = cpus[i];
+    for (int t = 1; t < pool.n; t++) pin_thread(pool.tids[t], t);
+    pthread_mutex_unlock(&pool_mu);
+}
+
 static void *pool_thread(void *arg) {
     (void)arg;
     int seen = 0;
@@ -96,7 +119,10 @@ static void *pool_thread(void *arg) {
 static void pool_run(row_job *jobs, int nchunks, int nthreads) {
     if (nthreads > OR_MAX_THREADS) nthreads = OR_MAX_THREADS;
     if (pool.n < nthreads) {
-        for (int t = pool.n > 0 ? pool.n : 1; t < nthreads; t++) pthread_create(&pool.tids[t], NULL, pool_thread, NULL);
+        for (int t = pool.n > 0 ? pool.n : 1; t < nthreads; t++) {
+            pthread_create(&pool.tids[t], NULL, pool_thread, NULL);
+            pin_thread(pool.tids[t], t);
+        }
         pool.n = nthreads;
     }
     memcpy(pool.jobs, jobs, (size_t)nchunks * sizeof(row_job));

@@ -66,6 +66,7 @@ def _declare(L: ctypes.CDLL) -> None:
     for name in ("or_q4k_q8k_row_avx2", "or_q6k_q8k_row_avx2", "or_q80_q80_row_avx2"):
         getattr(L, name).argtypes, getattr(L, name).restype = [P, S, P, S, P], I
     L.or_have_avx2.argtypes, L.or_have_avx2.restype = [], I
+    L.or_pool_pin.argtypes, L.or_pool_pin.restype = [P, I], None
     L.or_dequantize.argtypes, L.or_dequantize.restype = [I, P, S, S, P], I
     for name in ("or_matmul", "or_matmul_tiled"):
         getattr(L, name).argtypes, getattr(L, name).restype = [I, P, S, S, P, S, P, I, I], I
@@ -78,6 +79,12 @@ def _declare(L: ctypes.CDLL) -> None:
 def _p(a: np.ndarray) -> int:
     assert a.flags.c_contiguous
     return a.ctypes.data
+
+
+def pool_pin(cpus) -> None:
+    """Pin the oracle's row-spread pool: worker t >= 1 on cpus[t % len]."""
+    arr = np.ascontiguousarray(cpus, dtype=np.int32)
+    lib().or_pool_pin(_p(arr) if arr.size else None, int(arr.size))
 
 
 def have_avx2() -> bool:
