@@ -390,7 +390,7 @@ def secondary(args, hip, stream, device, layers):
 
 def prefill(args, hip, stream, device):
     """BASELINE configs[3], dense part: Q4_K [256 x 2048] -> 8192 and
-    [256 x 4096] -> 2048 on int8 MFMA (activation quantisation, MFMA kernel
+    [256 x 4096] -> 2048 (and Q6_K [256 x 2048] -> 8192) on int8 MFMA (activation quantisation, MFMA kernel
     and, for the narrow output, the split-K reduction all inside the timed
     call), on both MFMA paths: the dispatch's exact lane order (bitwise the
     reference) and the prefill tiles a caller requests explicitly (tile
@@ -401,18 +401,43 @@ def prefill(args, hip, stream, device):
     from inferq_amd import _lib, qgemm, synth
 
     res = {}
-    for n, k in ((8192, 2048), (2048, 4096)):
-        copies = -(-MIN_STREAM_BYTES // (n * k // 256 * 144))
-        mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, n, k, device, 90 + c), synth.Q4_K,
-                                           n, k) for c in range(copies)]
+    cases = ((synth.Q4_K, 8192, 2048, ("tiles", "exact")), (synth.Q4_K, 2048, 4096, ("tiles", "exact")),
+             (synth.Q6_K, 8192, 2048, ("exact",)))
+    paths = {"tiles": _lib.PATH_PREFILL_TILES, "exact": _lib.PATH_AUTO}
+    for dt, n, k, labels in cases:
+        copies = -(-MIN_STREAM_BYTES // synth.matrix_bytes(dt, n, k))
+        mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(dt, n, k, device, 90 + c), dt, n, k)
+                for c in range(copies)]
         x = torch.randn(256, k, device=device)
         y = torch.empty(256, n, device=device)
-        for label, path in (("tiles", _lib.PATH_PREFILL_TILES), ("exact", _lib.PATH_AUTO)):
+        for label in labels:
+            path = paths[label]
             ms = time_graph(lambda i: mats[i % copies].forward_into(x, y, path), max(20, args.steps // 4), hip)
             tops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
-            res[f"q4k_256x{k}_to_{n}_{label}"] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
-                                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+            name = "q4k" if dt == synth.Q4_K else "q6k"
+            res[f"{name}_256x{k}_to_{n}_{label}"] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
+                                                     "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         del mats
+    return res
+
+
+def lm_head_only(args, hip, device):
+    """The LM head [248320 x 2048] Q6_K alone at M = 1 and 8 (one 417 MB
+    matrix per launch: larger than the Infinity Cache)."""
+    import torch
+
+    from inferq_amd import qgemm, synth
+
+    lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 60),
+                                    synth.Q6_K, 248320, 2048)
+    b = lm.storage_bytes() + 2048 * 4 + 248320 * 4
+    res = {}
+    for m in (1, 8):
+        x = torch.randn(m, 2048, device=device)
+        y = torch.empty(m, 248320, device=device)
+        ms = time_graph(lambda i: lm.forward_into(x, y), max(10, args.steps // 10), hip)
+        res[f"m{m}"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1),
+                        "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
     return res
 
 
@@ -520,6 +545,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--only", choices=("prefill", "moe_prefill", "lm_head", "decode_sweep"), default=None,
+                    help="run one secondary config alone (for profiling) and print its JSON")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC byte-counter calibration)")
     ap.add_argument("--seed", type=int, default=1234)
@@ -546,6 +573,14 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    if args.only in ("prefill", "lm_head"):
+        if args.only == "prefill":
+            out_only = prefill(args, hip, stream, device)
+        else:
+            out_only = lm_head_only(args, hip, device)
+        print(json.dumps({"only": args.only, "result": out_only}), flush=True)
+        return
+
     t = time.time()
     layers = make_layers(args.layers, device, args.seed)
     torch.cuda.synchronize()
@@ -557,6 +592,13 @@ def main():
     xs = torch.randn(total, 1, H, device=device, generator=g)
     logits = torch.randn(total, 1, E, device=device, generator=g)
     out = torch.empty(1, H, device=device)
+
+    if args.only == "moe_prefill":
+        print(json.dumps({"only": args.only, "result": prefill_moe(args, hip, stream, device, layers)}), flush=True)
+        return
+    if args.only == "decode_sweep":
+        print(json.dumps({"only": args.only, "result": decode_sweep(args, hip, device, layers)}), flush=True)
+        return
 
     eager_ms, eager_per = time_moe(layers, xs, logits, out, args.steps, args.warmup, hip, stream)
     kb = moe_kernel_bytes(1, TOPK)

@@ -26,8 +26,12 @@ namespace iq {
 namespace {
 
 
-constexpr int kPfRows = 64;   // input rows per workgroup
-constexpr int kPfCols = 128;  // output columns per workgroup (16 per wave)
+// Tile shape: ROWS input rows x COLS output columns per workgroup, one
+// wave per 16 columns, each wave all ROWS rows (RT = ROWS / 16 row tiles
+// share every decoded B fragment).  64 x 128 on 8 waves (two per SIMD)
+// measured fastest: 128 x 64 on 4 waves, 128 x 128 on 8 waves with split K,
+// and a smaller stage with two workgroups per CU were all slower.
+constexpr int kPfRows = 64, kPfCols = 128;
 
 // ---- activation quantisation --------------------------------------------------
 // Q8K (bit-exact from_float) into the layouts the MFMA kernel reads:
@@ -66,31 +70,38 @@ struct PrefillArgs {
 };
 
 
-constexpr int kPfThreads = 512;  // 8 waves of 16 columns each
-
-// LDS stage: A int8 [64][kAS], B raw Q4_K [128][kBS], H f16 bsums [64][16],
-// D block scales [64], then a 16-byte sink for idle staging lanes.  Row
-// strides of 32 mod 64 bytes let the fragment reads (16 rows, four 16-byte
-// columns per row) run without bank conflicts on gfx950; strides of 16 mod
-// 64 bytes measure 1.5x slower.
+// LDS stage of one block: A int8 [ROWS][kAS], B raw Q4_K [COLS][kBS], H f16
+// bsums [ROWS][16], D block scales [ROWS], then a 16-byte sink for idle
+// staging lanes.  Row strides of 32 mod 64 bytes let the fragment reads
+// (16 rows, four 16-byte columns per row) run without bank conflicts on
+// gfx950; strides of 16 mod 64 bytes measure 1.5x slower.
 constexpr int kAS = 288;  // activation row stride (256 bytes + pad)
 constexpr int kBS = 160;  // Q4_K block stride (144 bytes + pad)
-constexpr int kStA = 0, kStB = kStA + kPfRows * kAS, kStH = kStB + kPfCols * kBS, kStD = kStH + kPfRows * 32;
-constexpr int kStage = kStD + kPfRows * 4;
-// staging chunks of 16 bytes per block: A 1024, B 1152, H 128, D 16
-constexpr int kChA = kPfRows * 16, kChB = kPfCols * 9, kChH = kPfRows * 2, kChD = kPfRows / 4;
-constexpr int kChunks = kChA + kChB + kChH + kChD;
-constexpr int kChPer = (kChunks + kPfThreads - 1) / kPfThreads;
+template <int ROWS, int COLS>
+struct PfTile {
+    static constexpr int kThreads = COLS / 16 * 64;
+    static constexpr int kRT = ROWS / 16;
+    static constexpr int kStA = 0, kStB = kStA + ROWS * kAS, kStH = kStB + COLS * kBS, kStD = kStH + ROWS * 32;
+    static constexpr int kStage = kStD + ROWS * 4;
+    // staging chunks of 16 bytes per block: A, B (9 per block), H, D
+    static constexpr int kChA = ROWS * 16, kChB = COLS * 9, kChH = ROWS * 2, kChD = ROWS / 4;
+    static constexpr int kChunks = kChA + kChB + kChH + kChD;
+    static constexpr int kChPer = (kChunks + kThreads - 1) / kThreads;
+};
 
-// Wave w owns all 64 rows and columns 16w .. 16w+15 of the tile as four
+// Wave w owns all ROWS rows and columns 16w .. 16w+15 of the tile as RT
 // 16 x 16 tiles of v_mfma_i32_16x16x64_i8 (one decoded B fragment serves
-// four row tiles).  For lane l (g = l / 16,
-// j = l % 16) a fragment holds K 16g..16g+15 of row / column j, and the
-// result rows 4g..4g+3 of column j.  One K step is 64 values: sub-blocks
-// 2s and 2s+1 of the block, whose weights are the low and the high nibbles
-// of qs bytes 32s..32s+31.
-template <bool DBG>
-__global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
+// RT row tiles).  For lane l (g = l / 16, j = l % 16) a fragment holds K
+// 16g..16g+15 of row / column j, and the result rows 4g..4g+3 of column j.
+// One K step is 64 values: sub-blocks 2s and 2s+1 of the block, whose
+// weights are the low and the high nibbles of qs bytes 32s..32s+31.
+template <int ROWS, int COLS, bool DBG>
+__global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(PrefillArgs p) {
+    using T = PfTile<ROWS, COLS>;
+    constexpr int kThreads = T::kThreads, kChPer = T::kChPer, kChunks = T::kChunks;
+    constexpr int kChA = T::kChA, kChB = T::kChB, kChH = T::kChH;
+    constexpr int kStA = T::kStA, kStB = T::kStB, kStH = T::kStH, kStD = T::kStD, kStage = T::kStage;
+    constexpr int RT = T::kRT;
     __shared__ __align__(16) uint8_t st[2][kStage + 16];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -98,17 +109,17 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
     // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs, so
     // ids L, L + 8, L + 16, ... (same XCD) take the m-tiles of one column
     // tile and share its weights in that XCD's L2.
-    const int mtiles = p.mp / kPfRows;
+    const int mtiles = p.mp / ROWS;
     const int grp = blockIdx.x / (8 * mtiles), rem = blockIdx.x - grp * 8 * mtiles;
     const int ntile = 8 * grp + (rem & 7), mtile = rem >> 3;
-    if ((int64_t)ntile * kPfCols >= p.n) return;  // padding workgroup (whole group uniform)
-    const int n0 = ntile * kPfCols;
-    const int row0 = mtile * kPfRows;
+    if ((int64_t)ntile * COLS >= p.n) return;  // padding workgroup (whole group uniform)
+    const int n0 = ntile * COLS;
+    const int row0 = mtile * ROWS;
     const int b0 = blockIdx.z * p.bps;
     const int b1 = min(p.nb, b0 + p.bps);
     const int64_t K = (int64_t)p.nb * 256;
 
-    // staging: chunk t = threadIdx.x + 512 i of a block.  Per chunk a thread
+    // staging: chunk t = threadIdx.x + kThreads i of a block.  Per chunk a thread
     // keeps its source in block 0, the stride per block and its LDS offset
     // (chunks past the block: the sink).  Every thread issues and parks
     // kChPer chunks per block without branches, so that the waits before the
@@ -119,7 +130,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
     int loff[kChPer];
 #pragma unroll
     for (int i = 0; i < kChPer; i++) {
-        int t = min((int)threadIdx.x + kPfThreads * i, kChunks - 1);
+        int t = min((int)threadIdx.x + kThreads * i, kChunks - 1);
         if (t < kChA) {
             gsrc[i] = (const uint8_t*)p.q + (int64_t)(row0 + (t >> 4)) * K + 16 * (t & 15);
             gstr[i] = 256;
@@ -140,7 +151,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
             gstr[i] = (uint32_t)p.mp * 4;
             loff[i] = kStD + 16 * t;
         }
-        if ((int)threadIdx.x + kPfThreads * i >= kChunks) loff[i] = kStage;  // sink
+        if ((int)threadIdx.x + kThreads * i >= kChunks) loff[i] = kStage;  // sink
     }
     u32x4a16 stg[kChPer];
     auto issue = [&](int b) {
@@ -153,9 +164,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
         for (int i = 0; i < kChPer; i++) *(u32x4a16*)(s + loff[i]) = stg[i];
     };
 
-    float out[4][4];  // [row tile][r]
+    float out[RT][4];  // [row tile][r]
 #pragma unroll
-    for (int rt = 0; rt < 4; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) out[rt][r] = 0.f;
 
@@ -170,7 +181,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
         // itself the scheduler sinks them next to the stores that wait on them)
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* bcol = S + kStB + (16 * wave + jj) * kBS;
-        pf_q4k_block<4, kAS>(S + kStA, bcol, S + kStH, (const float*)(S + kStD), g, jj, out,
+        pf_q4k_block<RT, kAS>(S + kStA, bcol, S + kStH, (const float*)(S + kStD), g, jj, out,
                              [&](int rt, int r, int32_t isum, float msum) {
                                  if constexpr (DBG) {
                                      const int64_t row = row0 + 16 * rt + 4 * g + r, gc = n0 + 16 * wave + jj;
@@ -190,7 +201,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_q4k(PrefillArgs p) {
     const int64_t ld = p.splits == 1 ? p.ldy : p.n;
     const int64_t gc = (int64_t)n0 + 16 * wave + jj;
 #pragma unroll
-    for (int rt = 0; rt < 4; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int64_t row = row0 + 16 * rt + 4 * g + r;
@@ -213,6 +224,7 @@ constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct PfPlan {
     int mp, nb, splits, bps;
+    int rows, cols;  // workgroup tile
     size_t q_bytes, d_bytes, hs_bytes, part_bytes;
     size_t total() const { return q_bytes + d_bytes + hs_bytes + part_bytes; }
 };
@@ -220,8 +232,10 @@ struct PfPlan {
 PfPlan plan(const WeightView& w, int64_t m) {
     PfPlan P;
     P.nb = (int)(w.cols / 256);
-    P.mp = (int)((m + kPfRows - 1) / kPfRows * kPfRows);
-    const int64_t tiles = ((w.rows + kPfCols - 1) / kPfCols) * (P.mp / kPfRows);  // real tiles (padding aside)
+    P.rows = kPfRows;
+    P.cols = kPfCols;
+    P.mp = (int)((m + P.rows - 1) / P.rows * P.rows);
+    const int64_t tiles = ((w.rows + P.cols - 1) / P.cols) * (P.mp / P.rows);  // real tiles (padding aside)
     int splits = 1;
     while (tiles * splits < 256 && splits * 2 <= P.nb && splits < 8) splits *= 2;
     P.bps = (P.nb + splits - 1) / splits;
@@ -268,10 +282,11 @@ hipError_t launch_prefill(const WeightView& w, const float* x, int64_t ldx, int6
                        P.nb, (int8_t*)a.q, (float*)a.dT, (_Float16*)a.hs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int64_t ntiles = (w.rows + kPfCols - 1) / kPfCols;
-    dim3 grid((unsigned)((ntiles + 7) / 8 * 8 * (P.mp / kPfRows)), 1, (unsigned)P.splits);
-    if (dbg_isum) hipLaunchKernelGGL(k_prefill_q4k<true>, grid, dim3(kPfThreads), 0, s, a);
-    else hipLaunchKernelGGL(k_prefill_q4k<false>, grid, dim3(kPfThreads), 0, s, a);
+    const int64_t ntiles = (w.rows + P.cols - 1) / P.cols;
+    dim3 grid((unsigned)((ntiles + 7) / 8 * 8 * (P.mp / P.rows)), 1, (unsigned)P.splits);
+    constexpr int TH = PfTile<kPfRows, kPfCols>::kThreads;
+    if (dbg_isum) hipLaunchKernelGGL((k_prefill_q4k<kPfRows, kPfCols, true>), grid, dim3(TH), 0, s, a);
+    else hipLaunchKernelGGL((k_prefill_q4k<kPfRows, kPfCols, false>), grid, dim3(TH), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess || P.splits == 1) return e;
     const int64_t tot = m * w.rows;
