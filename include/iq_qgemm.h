@@ -160,6 +160,24 @@ size_t iq_matmul_noalloc_max_bytes(void);
  * (QuantizedMatrix::forward_rows, src/gguf.rs:433-456). */
 int iq_matmul_host(iq_weight_t w, const float *x_host, int64_t m, float *y_host);
 
+/* ---- Per-row kernel entries (the reference's argument order) ------------- */
+
+/* out[r] = weight-row . input row r for one weight row of GGUF blocks
+ * (weight, weight_blocks of them) and `rows` input rows already quantised
+ * by from_float (Q8K blocks of 292 B for the K-quants, Q8_0 blocks of 34 B),
+ * stored block-major: inputs[block * rows + r], input_blocks of them.  Host
+ * slices; synchronous.  The reference's preconditions are checked and
+ * reported with IQ_ERR_SHAPE (out_len == rows, input_blocks == rows *
+ * weight_blocks).  Results are the reference kernel's bit for bit.
+ * Replaces: q4k_q8k_row / q6k_q8k_row / q80_q80_row (src/qgemm.rs:447-468)
+ * for callers that keep the per-row structure; iq_matmul is the fast path. */
+int iq_q4k_q8k_row(const void *weight, size_t weight_blocks, const void *inputs, size_t input_blocks, size_t rows,
+                   float *out, size_t out_len);
+int iq_q6k_q8k_row(const void *weight, size_t weight_blocks, const void *inputs, size_t input_blocks, size_t rows,
+                   float *out, size_t out_len);
+int iq_q80_q80_row(const void *weight, size_t weight_blocks, const void *inputs, size_t input_blocks, size_t rows,
+                   float *out, size_t out_len);
+
 /* ---- Greedy selection ----------------------------------------------------- */
 
 /* idx[r] = the index of the largest finite value of logit row r of device

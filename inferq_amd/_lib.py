@@ -52,6 +52,9 @@ _SIGNATURES = {
     "iq_matmul_ws": ([P, P, I64, P, P, SZ, P], INT),
     "iq_matmul_host": ([P, P, I64, P], INT),
     "iq_argmax_rows": ([P, I64, I64, P, P, P], INT),
+    "iq_q4k_q8k_row": ([P, SZ, P, SZ, SZ, P, SZ], INT),
+    "iq_q6k_q8k_row": ([P, SZ, P, SZ, SZ, P, SZ], INT),
+    "iq_q80_q80_row": ([P, SZ, P, SZ, SZ, P, SZ], INT),
     "iq_matmul_argmax": ([P, P, I64, P, P, P], INT),
     "iq_quantize_q8k": ([P, I64, I64, P, P], INT),
     "iq_quantize_q80": ([P, I64, I64, P, P], INT),

@@ -235,6 +235,23 @@ class QuantizedMatrix:
         return y, isum, msum
 
 
+def row_kernel(dtype: int, weight_row, inputs_block_major, rows: int) -> np.ndarray:
+    """The reference's per-row entry (q4k_q8k_row / q6k_q8k_row / q80_q80_row,
+    src/qgemm.rs:447-468) on host arrays: one weight row of GGUF blocks
+    against `rows` quantised input rows stored block-major."""
+    _ensure_init()
+    fn = {IQ_Q4_K: "iq_q4k_q8k_row", IQ_Q6_K: "iq_q6k_q8k_row", IQ_Q8_0: "iq_q80_q80_row"}.get(dtype)
+    if fn is None:
+        raise QgemmError(_lib.IQ_ERR_DTYPE, f"no per-row kernel for dtype {dtype}")
+    w = np.ascontiguousarray(weight_row).view(np.uint8).reshape(-1)
+    x = np.ascontiguousarray(inputs_block_major).view(np.uint8).reshape(-1)
+    out = np.empty(rows, np.float32)
+    ib = 34 if dtype == IQ_Q8_0 else 292
+    check(getattr(lib(), fn)(w.ctypes.data, w.size // BLOCK_BYTES[dtype], x.ctypes.data, x.size // ib, rows,
+                             out.ctypes.data, rows))
+    return out
+
+
 def argmax(logits):
     """sampling::argmax (src/sampling.rs:104-110) over the last dimension of
     device f32 logits: (index, value) per row, index -1 when a row has no

@@ -136,3 +136,17 @@ def test_moe_rejects_host_tensors():
                  lambda: layer.forward_timed(x, torch.zeros(1, 4), torch.zeros(1, 256), [None] * 4)):
         with pytest.raises(_lib.QgemmError, match="must be a tensor on cuda:0"):
             call()
+
+
+def test_row_entries_check_the_reference_preconditions(L):
+    """q4k_q8k_row's debug asserts (src/qgemm.rs:450-451) become status
+    codes, checked before any device work."""
+    L = _lib.lib()
+    w = np.zeros(144 * 2, np.uint8)
+    x = np.zeros(292 * 6, np.uint8)
+    out = np.zeros(3, np.float32)
+    _err(L, L.iq_q4k_q8k_row(w.ctypes.data, 2, x.ctypes.data, 6, 3, out.ctypes.data, 2), _lib.IQ_ERR_SHAPE,
+         "out.len() 2 != rows 3")
+    _err(L, L.iq_q6k_q8k_row(w.ctypes.data, 2, x.ctypes.data, 5, 3, out.ctypes.data, 3), _lib.IQ_ERR_SHAPE,
+         "inputs.len() 5 != rows 3 x weight.len() 2")
+    _err(L, L.iq_q80_q80_row(None, 2, x.ctypes.data, 6, 3, out.ctypes.data, 3), _lib.IQ_ERR_INVALID, "null slice")
