@@ -150,3 +150,17 @@ def test_row_entries_check_the_reference_preconditions(L):
     _err(L, L.iq_q6k_q8k_row(w.ctypes.data, 2, x.ctypes.data, 5, 3, out.ctypes.data, 3), _lib.IQ_ERR_SHAPE,
          "inputs.len() 5 != rows 3 x weight.len() 2")
     _err(L, L.iq_q80_q80_row(None, 2, x.ctypes.data, 6, 3, out.ctypes.data, 3), _lib.IQ_ERR_INVALID, "null slice")
+
+
+def test_rust_binding_declares_every_entry():
+    """The FFI crate (inferq_amd/rust/inferq-amd-sys) binds every entry
+    include/*.h declares, and nothing else."""
+    import os
+    import re
+
+    src = os.path.join(os.path.dirname(inferq_amd.__file__), "rust", "inferq-amd-sys", "src", "lib.rs")
+    text = open(src).read()
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    bound = set(re.findall(r"pub fn (iq_[a-z0-9_]+)\(", block))
+    assert bound == set(_lib.declared_symbols())
