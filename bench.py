@@ -456,7 +456,10 @@ def decode_sweep(args, hip, device, layers):
     over that time.  The *_qkv_rows lines also join the attention layers'
     q/gate, k and v into one [9216 x 2048] matrix (QuantizedMatrix::
     concatenate_rows, src/gguf.rs:379-404): one launch instead of three, the
-    same bytes and bitwise the same outputs."""
+    same bytes and bitwise the same outputs; likewise the DeltaNet layers'
+    qkvz and ba, which the reference computes from the same input
+    (src/qwen/quantized_deltanet.rs:537-563), as one [12352 x 2048]
+    matrix."""
     import torch
 
     from inferq_amd import qgemm, synth
@@ -471,7 +474,9 @@ def decode_sweep(args, hip, device, layers):
 
     dense = [[mat(r, c, 5000 + 10 * li + j) for j, (r, c) in enumerate(attn if is_attn[li] else delta)]
              for li in range(n)]
-    qkv = [d[0].concatenate_rows(d[1]).concatenate_rows(d[2]) if is_attn[li] else None for li, d in enumerate(dense)]
+    # joined by rows: attention q/gate + k + v, DeltaNet qkvz + ba
+    qkv = [d[0].concatenate_rows(d[1]).concatenate_rows(d[2]) if is_attn[li] else d[0].concatenate_rows(d[1])
+           for li, d in enumerate(dense)]
     lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 6000), synth.Q6_K,
                                     248320, 2048)
     dense_bytes = sum(m_.storage_bytes() for d in dense for m_ in d)
@@ -482,16 +487,17 @@ def decode_sweep(args, hip, device, layers):
     for m in (1, 8):
         xin = {c: torch.randn(m, c, device=device, generator=g) for c in (2048, 4096)}
         lg = torch.randn(n, m, E, device=device, generator=g)
-        ys = {r: torch.empty(m, r, device=device) for r in {r for r, _ in attn + delta} | {9216}}
+        ys = {r: torch.empty(m, r, device=device) for r in {r for r, _ in attn + delta} | {9216, 12352}}
         out = torch.empty(m, H, device=device)
         ylm = torch.empty(m, 248320, device=device)
 
         def step(i, joined=False):
             for li in range(n):
                 mats = dense[li]
-                if is_attn[li] and joined:
-                    qkv[li].forward_into(xin[2048], ys[9216])
-                    mats[3].forward_into(xin[4096], ys[2048])
+                if joined:
+                    j = qkv[li]
+                    j.forward_into(xin[2048], ys[j.shape()[0]])
+                    mats[-1].forward_into(xin[4096], ys[2048])  # o / out
                 else:
                     for mt in mats:
                         mt.forward_into(xin[mt.shape()[1]], ys[mt.shape()[0]])
