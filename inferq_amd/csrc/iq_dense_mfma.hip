@@ -8,7 +8,8 @@
 //
 // Two launches per call: k_dm_quant quantises x (Q8K, the lane-transposed
 // activation layout, block scales, 16-value sums as f16); k_dm_mm<FMT, RT>
-// takes 64 weight rows x 16 RT input rows per workgroup.
+// takes 64 weight rows x 16 RT input rows per workgroup, and k_dm_mm_pk
+// 64 weight rows x up to 8 input rows with two reference lanes per MFMA.
 #include "iq_internal.h"
 #include "iq_mfma_lanes.h"
 #include "iq_quant.h"
@@ -78,6 +79,44 @@ __global__ __launch_bounds__(256) void k_dm_mm(DmArgs a) {
     }
 }
 
+// At most 8 input rows: 64 weight rows x the 8 rows per workgroup, two
+// reference lanes per MFMA (ml_product_pk).
+template <int FMT>
+__global__ __launch_bounds__(256) void k_dm_mm_pk(DmArgs a) {
+    using L = MlStagePk<FMT>;
+    __shared__ __align__(16) uint8_t st[2][L::END];
+    __shared__ __align__(16) uint8_t zero[256];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15;
+    ((uint32_t*)zero)[threadIdx.x & 63] = 0u;  // read only after the first barrier
+    const int64_t n0 = (int64_t)blockIdx.x * kMlCols;
+    const int rows = a.m;
+    MlOperands op;
+    op.aq = a.q;
+    op.ldq = (int64_t)a.nb * 256;
+    op.ad = a.d;
+    op.ldd = a.nb;
+    op.hs = a.hs;
+    op.b0 = op.b1 = a.w + n0 * a.row_bytes;
+    op.bsplit = kMlCols;
+    op.brow_bytes = a.row_bytes;
+    op.nb = a.nb;
+    const int64_t last = a.n - 1 - n0;
+    auto brow = [&](int t) -> int64_t { return t < last ? (int64_t)t : last; };
+    auto arow = [&](int rr) -> int64_t { return min(rr, rows - 1); };
+    float v[4];
+    ml_product_pk<FMT>(op, arow, brow, st, zero, v);
+    const int64_t n = n0 + 16 * wave + jj;
+    if (q < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = 4 * q + r;
+            if (rr < rows && n < a.n) a.y[(int64_t)rr * a.ldy + n] = v[r];
+        }
+    }
+}
+
 constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct DmPlan {
@@ -92,6 +131,13 @@ DmPlan dm_plan(const WeightView& w, int64_t m) {
     P.d_bytes = align256((size_t)(m * nb * 4));
     P.hs_bytes = align256((size_t)(m * nb * 32));
     return P;
+}
+
+template <int FMT>
+hipError_t launch_pk(const DmArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)((a.n + kMlCols - 1) / kMlCols));
+    hipLaunchKernelGGL((k_dm_mm_pk<FMT>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 template <int FMT, int RT>
@@ -166,8 +212,9 @@ hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ld
     hipLaunchKernelGGL(k_dm_quant, dim3((unsigned)((qwaves + 3) / 4)), dim3(256), 0, s, x, ldx, (int)m, a.nb,
                        (int8_t*)a.q, (float*)a.d, (_Float16*)a.hs);
     if (hipError_t e = hipGetLastError()) return e;
-    if (w.dtype == kQ4_K) return m <= 16 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);
-    return m <= 16 ? launch_t<kQ6_K, 1>(a, s) : launch_t<kQ6_K, 2>(a, s);
+    if (w.dtype == kQ4_K)
+        return m <= 8 ? launch_pk<kQ4_K>(a, s) : m <= 16 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);
+    return m <= 8 ? launch_pk<kQ6_K>(a, s) : m <= 16 ? launch_t<kQ6_K, 1>(a, s) : launch_t<kQ6_K, 2>(a, s);
 }
 
 }  // namespace iq

@@ -12,8 +12,8 @@
 // (dword 8k + c), and B the weight dwords (c, k) with each dword's scale
 // folded in.  Scaled weights exceed int8, so each is split into two int8
 // streams whose integer sums recombine exactly: Q4_K sc*q = 8 (sc >> 3) q +
-// (sc & 7) q; Q6_K sc*(q - 32) = 64 hi + lo with lo in 0..63 and hi in
-// -64..64.  The Q4_K mins msum_k = m_2k s_2k + m_2k+1 s_2k+1 (s = 32-value
+// (sc & 7) q; Q6_K sc*(q - 32) = 256 hi + lo with hi in -16..16 and lo in
+// -128..127.  The Q4_K mins msum_k = m_2k s_2k + m_2k+1 s_2k+1 (s = 32-value
 // activation sums) come from an f16 MFMA over the 16-value sums (integers
 // below 2^24: exact).  A lane keeps the f32 chains of all eight reference
 // lanes for its outputs and joins them at the end in the hsum trees' order,
@@ -44,7 +44,9 @@ struct MlFmt<kQ4_K> {
 template <>
 struct MlFmt<kQ6_K> {
     static constexpr int BB = 210;
-    static constexpr int BS = 224;  // the block's 212-byte dword window, padded
+    // the block's 212-byte dword window, padded to 60 dwords: the 16
+    // columns of a fragment read dwords 60 j + o, 16 distinct banks
+    static constexpr int BS = 240;
     static constexpr int NL = 14;   // staging loads per row-block (16 bytes each)
     static constexpr bool kMins = false;
 };
@@ -63,21 +65,19 @@ struct MlStage {
 
 
 // Four unsigned six-bit values u (bytes) times a signed scale sc, minus
-// 32 sc: p = sc * (u - 32) in -4064..4096, split p = 64 hi + lo; returns the
-// lo bytes (0..63) and the hi bytes (-64..64), byte order kept.
+// 32 sc: p = sc * (u - 32) in -4064..4096, split p = 256 hi + lo with hi in
+// -16..16 and lo in -128..127 (byte order kept).  P = p + 128 is formed in
+// 16-bit lanes (bytes 0, 2 and bytes 1, 3 of u); as a 16-bit two's
+// complement value its high byte is floor(P / 256) = hi and its low byte
+// is lo + 128, so both streams are byte picks of P.
 __device__ __forceinline__ void ml_q6_scaled_split(uint32_t u, int sc, uint32_t& lo, uint32_t& hi) {
-    const s16x2_ml s2 = {(short)sc, (short)sc}, m2 = {(short)(-32 * sc), (short)(-32 * sc)};
-    const s16x2_ml u02 = __builtin_bit_cast(s16x2_ml, u & 0x00ff00ffu);         // bytes 0, 2
-    const s16x2_ml u13 = __builtin_bit_cast(s16x2_ml, (u >> 8) & 0x00ff00ffu);  // bytes 1, 3
-    const s16x2_ml p02 = u02 * s2 + m2, p13 = u13 * s2 + m2;
-    const uint32_t l02 = __builtin_bit_cast(uint32_t, p02) & 0x003f003fu;
-    const uint32_t l13 = __builtin_bit_cast(uint32_t, p13) & 0x003f003fu;
-    lo = l02 | (l13 << 8);
-    const s16x2_ml six = {6, 6};
-    const uint32_t h02 = __builtin_bit_cast(uint32_t, (s16x2_ml)(p02 >> six));
-    const uint32_t h13 = __builtin_bit_cast(uint32_t, (s16x2_ml)(p13 >> six));
-    // bytes 0 and 2 of h02 and of h13, interleaved
-    hi = __builtin_amdgcn_perm(h13, h02, 0x06020400u);
+    const s16x2_ml s2 = {(short)sc, (short)sc}, c2 = {(short)(128 - 32 * sc), (short)(128 - 32 * sc)};
+    const s16x2_ml u02 = __builtin_bit_cast(s16x2_ml, u & 0x00ff00ffu);                         // bytes 0, 2
+    const s16x2_ml u13 = __builtin_bit_cast(s16x2_ml, __builtin_amdgcn_perm(0u, u, 0x0c030c01u));  // bytes 1, 3
+    const uint32_t p02 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u02 * s2 + c2));
+    const uint32_t p13 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u13 * s2 + c2));
+    hi = __builtin_amdgcn_perm(p13, p02, 0x07030501u);                // high bytes, interleaved
+    lo = __builtin_amdgcn_perm(p13, p02, 0x06020400u) ^ 0x80808080u;  // low bytes - 128
 }
 
 // The 4 bytes at byte offset o of a block staged with a dword shift of sh
@@ -255,7 +255,7 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
                     const int scv = (int)(int8_t)(uint8_t)(q6s >> (8 * (2 * cc + hk)));
                     ml_q6_scaled_split(u, scv, w2[cc], w1[cc]);
                 }
-                mul = 64;
+                mul = 256;
             }
             const long b1 = (long)(((uint64_t)w1[1] << 32) | w1[0]);
             const long b2 = (long)(((uint64_t)w2[1] << 32) | w2[0]);
@@ -306,6 +306,225 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
 #pragma unroll
     for (int r = 0; r < 4 * RT; r++) {
         v[r] = ((acc[0][r] + acc[4][r]) + (acc[2][r] + acc[6][r])) + ((acc[1][r] + acc[5][r]) + (acc[3][r] + acc[7][r]));
+        if constexpr (F::kMins) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
+    }
+}
+
+// ---- up to 8 activation rows: two reference lanes per MFMA ------------------
+//
+// With at most 8 rows a 16-row tile would be half padding.  Instead one
+// v_mfma_i32_16x16x64_i8 computes two reference lanes: K 16q..16q+15 of lane
+// group q holds the dwords (c, kq), c = 4 (q & 1) .. +3, of reference lane
+// kq = p + 4 (q >= 2) (pair p = 0..3).  A row i < 8 carries activation row i
+// in the groups q < 2 and zeros in q >= 2; row 8 + i carries activation row i
+// in q >= 2 and zeros in q < 2.  So output rows 0..7 are isum_p and rows
+// 8..15 isum_{p+4} of the same activation rows: lane (q, j) holds
+// activation rows 4 (q & 1) + r of column j for reference lane kq, and the
+// lane 32 apart holds the partner lane (kq +- 4) of the same outputs, which
+// is the pairing of the first level of hsum_f32_8.
+
+// LDS stage: A int8 [8][kMlAS], B [64][BS], D f32 [8], H f16 [8][16].
+template <int FMT>
+struct MlStagePk {
+    static constexpr int A = 0;
+    static constexpr int B = A + 8 * kMlAS;
+    static constexpr int D = B + kMlCols * MlFmt<FMT>::BS;
+    static constexpr int H = D + 32;
+    static constexpr int END = H + (MlFmt<FMT>::kMins ? 8 * 32 : 0);
+};
+
+// As ml_product, for arow(rr) with rr < 8 (at most 8 activation rows); lane
+// (q, j) of wave w ends with v[r] = output (activation row 4 (q & 1) + r,
+// weight row 16 w + j), r < 4, in every lane group q.  `zero` is 256 bytes
+// of LDS holding zeros (16-byte aligned), read by the padding lanes of A.
+template <int FMT, class ARow, class BRow>
+__device__ __forceinline__ void ml_product_pk(const MlOperands& op, ARow arow, BRow brow,
+                                              uint8_t (*st)[MlStagePk<FMT>::END], const uint8_t* zero,
+                                              float (&v)[4]) {
+    using F = MlFmt<FMT>;
+    using L = MlStagePk<FMT>;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15;
+    const int h = q & 1;       // chunks 4h .. 4h+3
+    const int upper = q >> 1;  // reference lanes 4..7
+    const int nb = op.nb;
+
+    // ---- staging, as in ml_product: A 8 rows x 16 chunks, B 64 rows x NL
+    constexpr int kA = 8 * 16;
+    constexpr int kB = kMlCols * F::NL;
+    constexpr int kBPer = (kB + 255) / 256;
+    const int ta = threadIdx.x;  // A chunk of threads 0..127
+    const uint32_t a_src = (uint32_t)(arow((ta >> 4) & 7) * op.ldq + 16 * (ta & 15));
+    const int a_off = ta < kA ? L::A + (ta >> 4) * kMlAS + 16 * (ta & 15) : -1;
+    uint32_t b_src[kBPer];
+    int b_off[kBPer];
+    bool b_hi[kBPer];
+#pragma unroll
+    for (int i = 0; i < kBPer; i++) {
+        const int t = min((int)threadIdx.x + 256 * i, kB - 1);
+        const int c2 = t / F::NL, part = t - c2 * F::NL;
+        const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
+        b_hi[i] = c2 >= op.bsplit;
+        b_src[i] = (uint32_t)(brow(c2) * op.brow_bytes + po);
+        b_off[i] = (int)threadIdx.x + 256 * i < kB ? L::B + c2 * F::BS + po : -1;
+    }
+    // D on threads 128..135, H (Q4_K) on 192..207
+    const int tD = threadIdx.x - 128, tH = threadIdx.x - 192;
+    const int64_t d_row = arow(tD & 7);
+    const int64_t h_row = arow((tH >> 1) & 7);
+
+    v4i_ml sa = {};
+    u32x4 sb[kBPer];
+    float sd = 0.f;
+    v4i_ml sh16 = {};
+    auto issue = [&](int b) {
+        if (ta < kA) sa = *(const v4i_ml*)(op.aq + (int64_t)b * 256 + a_src);
+        const int64_t boff = FMT == kQ6_K ? ((int64_t)b * F::BB) & ~(int64_t)3 : (int64_t)b * F::BB;
+#pragma unroll
+        for (int i = 0; i < kBPer; i++) sb[i] = *(const u32x4*)((b_hi[i] ? op.b1 : op.b0) + boff + b_src[i]);
+        if (tD >= 0 && tD < 8) sd = op.ad[d_row * op.ldd + b];
+        if constexpr (F::kMins)
+            if (tH >= 0 && tH < 16) sh16 = *(const v4i_ml*)(op.hs + (h_row * nb + b) * 16 + 8 * (tH & 1));
+    };
+    auto park = [&](uint8_t* s) {
+        if (a_off >= 0) *(v4i_ml*)(s + a_off) = sa;
+#pragma unroll
+        for (int i = 0; i < kBPer; i++)
+            if (b_off[i] >= 0) *(u32x4*)(s + b_off[i]) = sb[i];
+        if (tD >= 0 && tD < 8) *(float*)(s + L::D + 4 * tD) = sd;
+        if constexpr (F::kMins)
+            if (tH >= 0 && tH < 16) *(v4i_ml*)(s + L::H + 32 * (tH >> 1) + 16 * (tH & 1)) = sh16;
+    };
+
+    const int col = 16 * wave + jj;
+    // A row of this lane: activation row j (q < 2) or j - 8 (q >= 2) where
+    // that lane carries data, else the zero row
+    const bool a_live = (jj < 8) == (upper == 0);
+    // acc[p]: the f32 chains of reference lane p + 4 upper; accm[k]: mins lane k
+    float acc[4][4], accm[4][4];
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[p][r] = accm[p][r] = 0.f;
+    issue(0);
+    park(st[0]);
+    lds_barrier();
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* S = st[b & 1];
+        if (b + 1 < nb) issue(b + 1);
+        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
+        const uint8_t* bcol = S + L::B + col * F::BS;
+        const uint8_t* arowp = a_live ? S + L::A + (jj & 7) * kMlAS + 16 * h : zero + 16 * h;
+        float dd[4], dm[4];
+        float xd, xdm = 0.f;
+        Q4Scales sc{};
+        uint32_t s6w = 0;                    // Q4_K: six-bit scales of sub-blocks 4h .. 4h+3
+        s16x2_ml q6m[4], q6c[4];             // Q6_K: (sc, sc), (128 - 32 sc, ...) of chunks 4h + cc
+        if constexpr (FMT == kQ4_K) {
+            const u32x4a16 hdr = *(const u32x4a16*)bcol;
+            xd = f16_to_f32(hdr.x);
+            xdm = f16_to_f32(hdr.x >> 16);
+            sc = q4_scales(hdr.y, hdr.z, hdr.w);
+            s6w = h ? sc.sc_hi : sc.sc_lo;
+        } else {
+            xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
+            // scales 2c + upper of chunks c = 4h + cc: bytes upper, 2 + upper of two dwords
+            const uint32_t w0 = ml_lds_win(bcol, sh, 192 + 8 * h) >> (8 * upper);
+            const uint32_t w1 = ml_lds_win(bcol, sh, 196 + 8 * h) >> (8 * upper);
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const int scv = (int)(int8_t)(uint8_t)((cc < 2 ? w0 : w1) >> (16 * (cc & 1)));
+                q6m[cc] = s16x2_ml{(short)scv, (short)scv};
+                q6c[cc] = s16x2_ml{(short)(128 - 32 * scv), (short)(128 - 32 * scv)};
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float yd = *(const float*)(S + L::D + 4 * (4 * h + r));
+            dd[r] = yd * xd;
+            if constexpr (F::kMins) dm[r] = -yd * xdm;
+        }
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int kq = p + 4 * upper;
+            uint32_t w1[4], w2[4];
+            int mul;  // isum = mul * (stream 1) + (stream 2)
+            if constexpr (FMT == kQ4_K) {
+                // sub-blocks 4h + cc: qs dword at 16 + 32 (2h + cc / 2) + 4 kq, nibble cc % 2
+                const uint32_t qd0 = *(const uint32_t*)(bcol + 16 + 64 * h + 4 * kq);
+                const uint32_t qd1 = *(const uint32_t*)(bcol + 16 + 64 * h + 32 + 4 * kq);
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    const uint32_t qd = cc < 2 ? qd0 : qd1;
+                    const uint32_t nib = (cc & 1) ? ((qd >> 4) & 0x0f0f0f0fu) : (qd & 0x0f0f0f0fu);
+                    const uint32_t s6 = byte_of(s6w, cc);
+                    w1[cc] = bytes_mul_small(nib, s6 >> 3);
+                    w2[cc] = bytes_mul_small(nib, s6 & 7u);
+                }
+                mul = 8;
+            } else {
+                // chunk c = 4h + cc: ql dword at 64 h + 32 (cc % 2) + 4 kq, the high
+                // nibbles for cc >= 2; qh dword at 128 + 32 h + 4 kq, bits 2 cc
+                const uint32_t la = ml_lds_win(bcol, sh, 64 * h + 4 * kq);
+                const uint32_t lb = ml_lds_win(bcol, sh, 64 * h + 32 + 4 * kq);
+                const uint32_t qh = ml_lds_win(bcol, sh, 128 + 32 * h + 4 * kq);
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    const uint32_t l = (cc & 1) ? lb : la;
+                    const uint32_t lo4 = (cc & 2) ? ((l >> 4) & 0x0f0f0f0fu) : (l & 0x0f0f0f0fu);
+                    const uint32_t u = lo4 | (((qh >> (2 * cc)) & 0x03030303u) << 4);
+                    const s16x2_ml u02 = __builtin_bit_cast(s16x2_ml, u & 0x00ff00ffu);
+                    const s16x2_ml u13 = __builtin_bit_cast(s16x2_ml, __builtin_amdgcn_perm(0u, u, 0x0c030c01u));
+                    const uint32_t p02 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u02 * q6m[cc] + q6c[cc]));
+                    const uint32_t p13 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u13 * q6m[cc] + q6c[cc]));
+                    w1[cc] = __builtin_amdgcn_perm(p13, p02, 0x07030501u);
+                    w2[cc] = __builtin_amdgcn_perm(p13, p02, 0x06020400u) ^ 0x80808080u;
+                }
+                mul = 256;
+            }
+            const v4i_ml a = *(const v4i_ml*)(arowp + 32 * kq);
+            const v4i_ml b1 = {(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+            const v4i_ml b2 = {(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
+            const v4i_ml z = {};
+            const v4i_ml i1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b1, z, 0, 0, 0);
+            const v4i_ml i2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b2, z, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[p][r] = __builtin_fmaf(dd[r], (float)(i1[r] * mul + i2[r]), acc[p][r]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) asm volatile("" : "+v"(acc[p][r]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (F::kMins) {
+            // as in ml_product; rows 8..15 of the f16 MFMA repeat rows 0..7
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t mwd = k < 2 ? sc.mn_lo : sc.mn_hi;
+                const _Float16 mA = (_Float16)(float)byte_of(mwd, 2 * (k & 1));
+                const _Float16 mB = (_Float16)(float)byte_of(mwd, 2 * (k & 1) + 1);
+                const _Float16 zh = (_Float16)0.f;
+                const v4h_ml bm = q == k ? v4h_ml{mA, mA, mB, mB} : v4h_ml{zh, zh, zh, zh};
+                const v4h_ml am = *(const v4h_ml*)(S + L::H + (jj & 7) * 32 + 8 * q);
+                const v4f_ml zf = {};
+                const v4f_ml ms = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, zf, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) accm[k][r] = __builtin_fmaf(dm[r], ms[r], accm[k][r]);
+#pragma unroll
+                for (int r = 0; r < 4; r++) asm volatile("" : "+v"(accm[k][r]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + 1 < nb) park(st[(b + 1) & 1]);
+        lds_barrier();
+    }
+    // hsum_f32_8: the partner lane (32 apart) holds reference lanes kq +- 4
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float s[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) s[p] = acc[p][r] + __shfl_xor(acc[p][r], 32);
+        v[r] = (s[0] + s[2]) + (s[1] + s[3]);
         if constexpr (F::kMins) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
     }
 }

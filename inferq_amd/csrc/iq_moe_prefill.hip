@@ -196,7 +196,11 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
 template <int FMT, int MODE>
 __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
     using L = MlStage<FMT, kMpRT>;
-    __shared__ __align__(16) uint8_t st[2][L::END];
+    using LP = MlStagePk<FMT>;
+    constexpr int kStage = 2 * L::END > 2 * LP::END ? 2 * L::END : 2 * LP::END;
+    __shared__ __align__(16) uint8_t lds[kStage + 256];
+    auto st = (uint8_t (*)[L::END])lds;
+    uint8_t* zero = lds + kStage;
     const int c = blockIdx.y;
     if (c >= p.meta[1]) return;  // whole workgroup
     const int lane = threadIdx.x & 63;
@@ -235,34 +239,53 @@ __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
         const int pos = pos0 + min(rr, rows - 1);
         return MODE == 0 ? (int64_t)p.assign_row[pos] : (int64_t)pos;
     };
+    // chunks of at most 8 rows take two reference lanes per MFMA; output r
+    // of a lane is then row 4 (q & 1) + r (every lane group), else row
+    // 16 (r / 4) + 4 q + r % 4
     float v[4 * kMpRT];
-    ml_product<FMT, kMpRT>(op, arow, brow, st, v);
+    const bool pk = rows <= 8;  // uniform per workgroup
+    if (pk) {
+        ((uint32_t*)zero)[threadIdx.x & 63] = 0u;  // read only after the product's first barrier
+        float vp[4];
+        ml_product_pk<FMT>(op, arow, brow, (uint8_t (*)[LP::END])lds, zero, vp);
+#pragma unroll
+        for (int r = 0; r < 4 * kMpRT; r++) v[r] = r < 4 ? vp[r] : 0.f;
+    } else {
+        ml_product<FMT, kMpRT>(op, arow, brow, st, v);
+    }
+    auto out_row = [&](int r) { return pk ? (r < 4 ? 4 * (q & 1) + r : kMpRows) : 16 * (r >> 2) + 4 * q + (r & 3); };
+    const bool writer = !pk || q < 2;  // pair-lane tiles: lane groups 2, 3 repeat 0, 1
 
     if constexpr (MODE == 0) {
         // waves 2, 3 hold up of the columns waves 0, 1 hold gate of
-        float* s_up = (float*)st[0];  // [kMpRows][32]
-        if (wave >= 2)
+        float* s_up = (float*)lds;  // [kMpRows][32]
+        if (wave >= 2 && writer)
 #pragma unroll
-            for (int r = 0; r < 4 * kMpRT; r++) s_up[(16 * (r >> 2) + 4 * q + (r & 3)) * 32 + 16 * (wave - 2) + jj] = v[r];
+            for (int r = 0; r < 4 * kMpRT; r++) {
+                const int rr = out_row(r);
+                if (rr < kMpRows) s_up[rr * 32 + 16 * (wave - 2) + jj] = v[r];
+            }
         lds_barrier();
-        if (wave < 2) {
+        if (wave < 2 && writer) {
             const int64_t i = (int64_t)blockIdx.x * 32 + 16 * wave + jj;
 #pragma unroll
             for (int r = 0; r < 4 * kMpRT; r++) {
-                const int rr = 16 * (r >> 2) + 4 * q + (r & 3);
-                const float u = s_up[rr * 32 + 16 * wave + jj];
-                // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
-                if (rr < rows && i < p.I)
+                const int rr = out_row(r);
+                if (rr < rows && i < p.I) {
+                    const float u = s_up[rr * 32 + 16 * wave + jj];
+                    // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
                     p.act[(int64_t)(pos0 + rr) * p.I + i] = __fdiv_rn(v[r], 1.f + exp_f32(-v[r])) * u;
+                }
             }
         }
     } else {
         const int64_t n = (int64_t)blockIdx.x * kMlCols + 16 * wave + jj;
+        if (writer)
 #pragma unroll
-        for (int r = 0; r < 4 * kMpRT; r++) {
-            const int rr = 16 * (r >> 2) + 4 * q + (r & 3);
-            if (rr < rows && n < p.H) p.vals[(int64_t)(pos0 + rr) * p.H + n] = v[r];
-        }
+            for (int r = 0; r < 4 * kMpRT; r++) {
+                const int rr = out_row(r);
+                if (rr < rows && n < p.H) p.vals[(int64_t)(pos0 + rr) * p.H + n] = v[r];
+            }
     }
 }
 

@@ -152,12 +152,13 @@ def large_matrices():
 
 @pytest.mark.parametrize("dtype", [Q6, Q4], ids=["q6k", "q4k"])
 def test_large_matrix_rows_bitexact(gpu, oracle, large_matrices, dtype):
-    """2..63 input rows on a large matrix (one and two 16-row tiles, ragged
-    tails) are bitwise the oracle's, hence bitwise the one-row results."""
+    """2..63 input rows on a large matrix (pair-lane tiles up to 8 rows, one
+    and two 16-row tiles, ragged tails) are bitwise the oracle's, hence
+    bitwise the one-row results."""
     w, rows = large_matrices[dtype]
     mat = Q.QuantizedMatrix.upload(w, dtype, rows, 2048)
     impl = 1 if oracle.have_avx2() else 0
-    for m in (1, 2, 3, 8, 16, 17, 33, 63):
+    for m in (1, 2, 3, 5, 8, 9, 16, 17, 33, 63):
         x = S.normal((m, 2048), np.random.default_rng(2000 + m))
         expected = oracle.matmul(dtype, w, rows, 2048, x, impl=impl, nthreads=8)
         got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()

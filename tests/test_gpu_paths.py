@@ -79,7 +79,7 @@ def test_each_path_bitexact(gpu, oracle, path, dtype, rows, cols):
     rng = np.random.default_rng(path * 100 + dtype)
     w = S.random_matrix(dtype, rows, cols, rng)
     mat = Q.QuantizedMatrix.upload(w, dtype, rows, cols)
-    for m in (1, 3, 16, 63, 64, 70):
+    for m in (1, 3, 5, 8, 9, 16, 63, 64, 70):
         x = S.normal((m, cols), np.random.default_rng(4000 + m))
         xt = torch.from_numpy(x).to(gpu)
         if not _covers(path, dtype, m):
