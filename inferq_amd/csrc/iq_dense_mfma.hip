@@ -117,6 +117,139 @@ __global__ __launch_bounds__(256) void k_dm_mm_pk(DmArgs a) {
     }
 }
 
+// Mid-size matrices of width 2048 or 4096 at up to 8 rows: 64 weight rows
+// per workgroup leave too few workgroups (128 for [8192 x 2048]), each a
+// chain of dependent block loads.  Here a workgroup takes 16 weight rows
+// and each of its NW waves two of the 2 NW blocks, all loaded at once; the
+// waves form their blocks' exact integers in parallel, then the f32 chains
+// pass from wave to wave in block order through LDS, so every output is
+// the one-row kernel's bit for bit.
+template <int FMT>
+struct SkRegion {  // one block of one wave in LDS
+    static constexpr int A = 0;                                    // int8 [8][kMlAS]
+    static constexpr int B = A + 8 * kMlAS;                        // [16][BS]
+    static constexpr int D = B + 16 * MlFmt<FMT>::BS;              // f32 [8]
+    static constexpr int H = D + 32;                               // f16 [8][16] (Q4_K)
+    static constexpr int END = H + (MlFmt<FMT>::kMins ? 8 * 32 : 0);
+};
+constexpr int kSkBPW = 2;  // blocks per wave
+
+template <int FMT, int NW>
+__global__ __launch_bounds__(NW * 64) void k_dm_sk(DmArgs a) {
+    using F = MlFmt<FMT>;
+    using R = SkRegion<FMT>;
+    constexpr int BPW = kSkBPW, NH = FMT == kQ4_K ? 32 : 16;  // handed-over floats per lane
+    __shared__ __align__(16) uint8_t reg[NW][BPW][R::END];
+    __shared__ __align__(16) uint8_t zero[256];
+    // the chains' hand-over [NH][64] reuses wave 0's stage: wave 0 writes it
+    // after its own blocks, and the other waves' stages stay untouched
+    static_assert(NH * 64 * 4 <= BPW * R::END, "hand-over fits wave 0's stage");
+    float (*hand)[64] = (float (*)[64])reg[0][0];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15, h = q & 1;
+    ((uint32_t*)zero)[lane] = 0u;
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+    const int rows = a.m, b0 = wave * BPW;
+    const int64_t last = a.n - 1 - n0;
+    const uint8_t* wbase = a.w + n0 * a.row_bytes;
+    auto arow = [&](int rr) -> int64_t { return min(rr, rows - 1); };
+
+    // staging of this wave's blocks b0, b0 + 1: A 8 rows x 16 chunks, B 16
+    // rows x NL chunks, D 8 scales, H 8 x 2 chunks (Q4_K), per block
+    constexpr int kA = 8 * 16 * BPW, kB = 16 * F::NL * BPW;
+    constexpr int kAPer = kA / 64, kBPer = (kB + 63) / 64;
+    v4i_ml sa[kAPer];
+    u32x4 sb[kBPer];
+#pragma unroll
+    for (int i = 0; i < kAPer; i++) {
+        const int t = lane + 64 * i, bi = t >> 7, row = (t >> 4) & 7, part = t & 15;
+        sa[i] = *(const v4i_ml*)(a.q + arow(row) * (int64_t)a.nb * 256 + (int64_t)(b0 + bi) * 256 + 16 * part);
+    }
+#pragma unroll
+    for (int i = 0; i < kBPer; i++) {
+        const int t = min(lane + 64 * i, kB - 1);
+        const int cb = t / F::NL, part = t - cb * F::NL, col = cb / BPW, bi = cb - col * BPW;
+        const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
+        const int64_t b = b0 + bi;
+        const int64_t boff = FMT == kQ6_K ? (b * F::BB) & ~(int64_t)3 : b * F::BB;
+        sb[i] = *(const u32x4*)(wbase + (col < last ? col : last) * a.row_bytes + boff + po);
+    }
+    float sd = 0.f;
+    if (lane < 8 * BPW) sd = a.d[arow(lane & 7) * a.nb + b0 + (lane >> 3)];
+    v4i_ml sh16 = {};
+    if constexpr (F::kMins)
+        if (lane < 16 * BPW)
+            sh16 = *(const v4i_ml*)(a.hs + (arow((lane >> 1) & 7) * a.nb + b0 + (lane >> 4)) * 16 + 8 * (lane & 1));
+#pragma unroll
+    for (int i = 0; i < kAPer; i++) {
+        const int t = lane + 64 * i, bi = t >> 7, row = (t >> 4) & 7, part = t & 15;
+        *(v4i_ml*)(reg[wave][bi] + R::A + row * kMlAS + 16 * part) = sa[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kBPer; i++) {
+        const int t = lane + 64 * i;
+        if (t < kB) {
+            const int cb = t / F::NL, part = t - cb * F::NL, col = cb / BPW, bi = cb - col * BPW;
+            const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
+            *(u32x4*)(reg[wave][bi] + R::B + col * F::BS + po) = sb[i];
+        }
+    }
+    if (lane < 8 * BPW) *(float*)(reg[wave][lane >> 3] + R::D + 4 * (lane & 7)) = sd;
+    if constexpr (F::kMins)
+        if (lane < 16 * BPW) *(v4i_ml*)(reg[wave][lane >> 4] + R::H + 32 * ((lane >> 1) & 7) + 16 * (lane & 1)) = sh16;
+    lds_barrier();  // the zero row and every wave's stage
+
+    // this wave's blocks: exact integers and scales
+    const bool a_live = (jj < 8) == (q < 2);
+    MlPkBlock<FMT> o[BPW];
+#pragma unroll
+    for (int bi = 0; bi < BPW; bi++) {
+        const uint8_t* S = reg[wave][bi];
+        const int sh = FMT == kQ6_K ? (int)(((int64_t)(b0 + bi) * F::BB) & 3) : 0;
+        const uint8_t* arowp = a_live ? S + R::A + (jj & 7) * kMlAS + 16 * h : zero + 16 * h;
+        ml_pk_block<FMT>(S + R::B + jj * F::BS, sh, arowp, (const float*)(S + R::D), S + R::H, q, jj, o[bi]);
+    }
+    // the chains, wave 0 first: each wave continues them over its blocks
+    float acc[4][4], accm[4][4];
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[p][r] = accm[p][r] = 0.f;
+    for (int w2 = 0; w2 < NW; w2++) {
+        if (wave == w2) {
+            if (w2 > 0) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[i >> 2][i & 3] = hand[i][lane];
+                if constexpr (F::kMins)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) accm[i >> 2][i & 3] = hand[16 + i][lane];
+            }
+#pragma unroll
+            for (int bi = 0; bi < BPW; bi++) ml_pk_chain<FMT>(o[bi], acc, accm);
+            if (w2 < NW - 1) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) hand[i][lane] = acc[i >> 2][i & 3];
+                if constexpr (F::kMins)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) hand[16 + i][lane] = accm[i >> 2][i & 3];
+            }
+        }
+        if (w2 < NW - 1) lds_barrier();
+    }
+    if (wave == NW - 1) {
+        float v[4];
+        ml_pk_finish<FMT>(acc, accm, v);
+        const int64_t n = n0 + jj;
+        if (q < 2)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int rr = 4 * q + r;
+                if (rr < rows && n < a.n) a.y[(int64_t)rr * a.ldy + n] = v[r];
+            }
+    }
+}
+
 constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct DmPlan {
@@ -131,6 +264,14 @@ DmPlan dm_plan(const WeightView& w, int64_t m) {
     P.d_bytes = align256((size_t)(m * nb * 4));
     P.hs_bytes = align256((size_t)(m * nb * 32));
     return P;
+}
+
+template <int FMT>
+hipError_t launch_sk(const DmArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)((a.n + 15) / 16));
+    if (a.nb == 8) hipLaunchKernelGGL((k_dm_sk<FMT, 4>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_dm_sk<FMT, 8>), grid, dim3(512), 0, s, a);
+    return hipGetLastError();
 }
 
 template <int FMT>
@@ -149,6 +290,10 @@ hipError_t launch_t(const DmArgs& a, hipStream_t s) {
 
 }  // namespace
 
+// Largest matrix the split-K tile takes (larger ones keep 64 weight rows per
+// workgroup and load the activations once per 64 rows)
+constexpr int64_t kDmSkMaxBytes = (int64_t)64 << 20;
+
 // Whether the tile can read W at all: staging reads 16-byte chunks of Q4_K
 // rows and 4-byte-aligned windows of Q6_K blocks, so rows must keep that
 // alignment (Q6_K: an even block count per row).
@@ -159,24 +304,30 @@ bool dm_layout_ok(const WeightView& w) {
     return false;
 }
 
-// Where the dispatch uses this kernel.  At 2..63 rows: from 64 MiB of
-// weights (an LM head: 2.2x-4.5x over the GEMV at 8-48 rows); from 8 MiB at
-// 16 rows or more (q/gate [8192 x 2048]: 1.8x-2.4x); and from 8 MiB at 8 rows
-// with 8192 weight rows or more (q/gate at 8 rows 16.7 -> 15.9 us, q/gate + k
-// + v joined [9216 x 2048] 23.1 -> 15.6 us, q/gate at 12 rows 23.4 -> 15.9
-// us).  Smaller or narrower matrices keep the GEMV, whose latency is lower
-// there (64 weight rows per workgroup leave a [512 x 2048] matrix 8
-// workgroups and o [2048 x 4096] 32, which ran 2.5x slower).  From 64 rows
-// (prefill widths) every K-quant matrix the tile can read takes it: the
-// result stays bitwise the one-row result, which speculative decoding needs
-// (src/gguf.rs:493-520 tiles prefill rows under the same guarantee).
+// Where the dispatch uses these kernels (measured on MI355X, per call over
+// distinct matrices):
+//  - from 64 MiB of weights at 2..63 rows (an LM head: the GEMV is 1.3x-2.3x
+//    slower at 2-8 rows, 2.2x-4.5x at 8-48);
+//  - at 3..8 rows from 8 MiB (the split-K tile: q/gate [8192 x 2048] at 4
+//    rows 12.6 -> 10.2 us, at 8 rows 18.4 -> 10.3 us; q/gate + k + v joined
+//    [9216 x 2048] at 4 rows 20.9 -> 11.3 us; qkvz + ba [12352 x 2048] at 3
+//    rows 22.9 -> 12.2 us), and at 6..8 rows from 4 MiB (Q6_K [2048 x 4096]
+//    at 6 rows 14.0 -> 10.6 us; Q4_K o [2048 x 4096] 11.0 -> 10.9 us); at 2
+//    rows the GEMV stays faster (q/gate 8.3 against 9.9 us);
+//  - at 9..63 rows from 8 MiB with 16 rows or more or 8192 weight rows or
+//    more (q/gate at 12 rows 23.4 -> 15.9 us, at 16 rows 1.8x-2.4x);
+//  - from 64 rows (prefill widths) every K-quant matrix the tile can read:
+//    the result stays bitwise the one-row result, which speculative decoding
+//    needs (src/gguf.rs:493-520 tiles prefill rows under the same guarantee).
+// Smaller or narrower matrices keep the GEMV, whose latency is lower there
+// (a [512 x 2048] matrix: 4.1 against 7.9 us at 8 rows).
 bool dense_mfma_supported(const WeightView& w, int64_t m) {
     if (m < 2 || !dm_layout_ok(w)) return false;
     if (m >= kPrefillMinRows) return true;
-    const int64_t bytes = w.rows * w.row_bytes;
-    const bool large = bytes >= ((int64_t)64 << 20);
-    const bool mid = bytes >= ((int64_t)8 << 20) && (m >= 16 || (m >= 8 && w.rows >= 8192));
-    return large || mid;
+    const int64_t bytes = w.rows * w.row_bytes, MiB = (int64_t)1 << 20;
+    if (bytes >= 64 * MiB) return true;
+    if (m <= 8) return m >= 3 && (bytes >= 8 * MiB || (m >= 6 && bytes >= 4 * MiB));
+    return bytes >= 8 * MiB && (m >= 16 || w.rows >= 8192);
 }
 
 size_t dense_mfma_workspace_any(const WeightView& w, int64_t m) {
@@ -212,9 +363,13 @@ hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ld
     hipLaunchKernelGGL(k_dm_quant, dim3((unsigned)((qwaves + 3) / 4)), dim3(256), 0, s, x, ldx, (int)m, a.nb,
                        (int8_t*)a.q, (float*)a.d, (_Float16*)a.hs);
     if (hipError_t e = hipGetLastError()) return e;
+    // up to 8 rows: the split-K tile on mid-size matrices of width 2048 or 4096
+    const bool sk = m <= 8 && (a.nb == 8 || a.nb == 16) && w.rows * w.row_bytes <= kDmSkMaxBytes;
     if (w.dtype == kQ4_K)
-        return m <= 8 ? launch_pk<kQ4_K>(a, s) : m <= 16 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);
-    return m <= 8 ? launch_pk<kQ6_K>(a, s) : m <= 16 ? launch_t<kQ6_K, 1>(a, s) : launch_t<kQ6_K, 2>(a, s);
+        return sk ? launch_sk<kQ4_K>(a, s) : m <= 8 ? launch_pk<kQ4_K>(a, s)
+                                       : m <= 16 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);
+    return sk ? launch_sk<kQ6_K>(a, s) : m <= 8 ? launch_pk<kQ6_K>(a, s)
+                                   : m <= 16 ? launch_t<kQ6_K, 1>(a, s) : launch_t<kQ6_K, 2>(a, s);
 }
 
 }  // namespace iq

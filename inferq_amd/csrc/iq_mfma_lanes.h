@@ -323,6 +323,150 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
 // lane 32 apart holds the partner lane (kq +- 4) of the same outputs, which
 // is the pairing of the first level of hsum_f32_8.
 
+// One block of a pair-lane tile for lane (q, j), all operands in LDS:
+//   bcol  this lane's weight row (column j of the tile), staged as in
+//         ml_product (Q6_K: the dword window at shift sh);
+//   arow  this lane's A row: activation row j (q < 2) or j - 8 (q >= 2) of
+//         the block's 256 int8 values, or 256 zero bytes where the lane
+//         carries padding;
+//   D     the block scales of activation rows 0..7; H their 16-value sums
+//         (Q4_K), row r at H + 32 r.
+// Returns the lane's isum[p][r] (reference lane p + 4 (q >= 2), activation
+// row 4 (q & 1) + r), dd[r] = y.d * x.d, and for Q4_K the mins ms[k][r]
+// (mins lane k) with dm[r] = -y.d * x.dmin.
+template <int FMT>
+struct MlPkBlock {
+    int32_t isum[4][4];
+    float dd[4];
+    float ms[4][4];
+    float dm[4];
+};
+template <int FMT>
+__device__ __forceinline__ void ml_pk_block(const uint8_t* bcol, int sh, const uint8_t* arow, const float* D,
+                                            const uint8_t* H, int q, int jj, MlPkBlock<FMT>& o) {
+    const int h = q & 1, upper = q >> 1;
+    float xd, xdm = 0.f;
+    Q4Scales sc{};
+    uint32_t s6w = 0;         // Q4_K: six-bit scales of sub-blocks 4h .. 4h+3
+    s16x2_ml q6m[4], q6c[4];  // Q6_K: (sc, sc), (128 - 32 sc, ...) of chunks 4h + cc
+    if constexpr (FMT == kQ4_K) {
+        const u32x4a16 hdr = *(const u32x4a16*)bcol;
+        xd = f16_to_f32(hdr.x);
+        xdm = f16_to_f32(hdr.x >> 16);
+        sc = q4_scales(hdr.y, hdr.z, hdr.w);
+        s6w = h ? sc.sc_hi : sc.sc_lo;
+    } else {
+        xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
+        // scales 2c + upper of chunks c = 4h + cc: bytes upper, 2 + upper of two dwords
+        const uint32_t w0 = ml_lds_win(bcol, sh, 192 + 8 * h) >> (8 * upper);
+        const uint32_t w1 = ml_lds_win(bcol, sh, 196 + 8 * h) >> (8 * upper);
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const int scv = (int)(int8_t)(uint8_t)((cc < 2 ? w0 : w1) >> (16 * (cc & 1)));
+            q6m[cc] = s16x2_ml{(short)scv, (short)scv};
+            q6c[cc] = s16x2_ml{(short)(128 - 32 * scv), (short)(128 - 32 * scv)};
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float yd = D[4 * h + r];
+        o.dd[r] = yd * xd;
+        if constexpr (FMT == kQ4_K) o.dm[r] = -yd * xdm;
+    }
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int kq = p + 4 * upper;
+        uint32_t w1[4], w2[4];
+        int mul;  // isum = mul * (stream 1) + (stream 2)
+        if constexpr (FMT == kQ4_K) {
+            // sub-blocks 4h + cc: qs dword at 16 + 32 (2h + cc / 2) + 4 kq, nibble cc % 2
+            const uint32_t qd0 = *(const uint32_t*)(bcol + 16 + 64 * h + 4 * kq);
+            const uint32_t qd1 = *(const uint32_t*)(bcol + 16 + 64 * h + 32 + 4 * kq);
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const uint32_t qd = cc < 2 ? qd0 : qd1;
+                const uint32_t nib = (cc & 1) ? ((qd >> 4) & 0x0f0f0f0fu) : (qd & 0x0f0f0f0fu);
+                const uint32_t s6 = byte_of(s6w, cc);
+                w1[cc] = bytes_mul_small(nib, s6 >> 3);
+                w2[cc] = bytes_mul_small(nib, s6 & 7u);
+            }
+            mul = 8;
+        } else {
+            // chunk c = 4h + cc: ql dword at 64 h + 32 (cc % 2) + 4 kq, the high
+            // nibbles for cc >= 2; qh dword at 128 + 32 h + 4 kq, bits 2 cc
+            const uint32_t la = ml_lds_win(bcol, sh, 64 * h + 4 * kq);
+            const uint32_t lb = ml_lds_win(bcol, sh, 64 * h + 32 + 4 * kq);
+            const uint32_t qh = ml_lds_win(bcol, sh, 128 + 32 * h + 4 * kq);
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const uint32_t l = (cc & 1) ? lb : la;
+                const uint32_t lo4 = (cc & 2) ? ((l >> 4) & 0x0f0f0f0fu) : (l & 0x0f0f0f0fu);
+                const uint32_t u = lo4 | (((qh >> (2 * cc)) & 0x03030303u) << 4);
+                const s16x2_ml u02 = __builtin_bit_cast(s16x2_ml, u & 0x00ff00ffu);
+                const s16x2_ml u13 = __builtin_bit_cast(s16x2_ml, __builtin_amdgcn_perm(0u, u, 0x0c030c01u));
+                const uint32_t p02 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u02 * q6m[cc] + q6c[cc]));
+                const uint32_t p13 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u13 * q6m[cc] + q6c[cc]));
+                w1[cc] = __builtin_amdgcn_perm(p13, p02, 0x07030501u);
+                w2[cc] = __builtin_amdgcn_perm(p13, p02, 0x06020400u) ^ 0x80808080u;
+            }
+            mul = 256;
+        }
+        const v4i_ml a = *(const v4i_ml*)(arow + 32 * kq);
+        const v4i_ml b1 = {(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+        const v4i_ml b2 = {(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
+        const v4i_ml z = {};
+        const v4i_ml i1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b1, z, 0, 0, 0);
+        const v4i_ml i2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b2, z, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) o.isum[p][r] = i1[r] * mul + i2[r];
+    }
+    if constexpr (FMT == kQ4_K) {
+        // mins as in ml_product; rows 8..15 of the f16 MFMA repeat rows 0..7
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t mwd = k < 2 ? sc.mn_lo : sc.mn_hi;
+            const _Float16 mA = (_Float16)(float)byte_of(mwd, 2 * (k & 1));
+            const _Float16 mB = (_Float16)(float)byte_of(mwd, 2 * (k & 1) + 1);
+            const _Float16 zh = (_Float16)0.f;
+            const v4h_ml bm = q == k ? v4h_ml{mA, mA, mB, mB} : v4h_ml{zh, zh, zh, zh};
+            const v4h_ml am = *(const v4h_ml*)(H + (jj & 7) * 32 + 8 * q);
+            const v4f_ml zf = {};
+            const v4f_ml m4 = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, zf, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) o.ms[k][r] = m4[r];
+        }
+    }
+}
+
+// The chains of one block: acc[p][r] of reference lane p + 4 (q >= 2),
+// accm[k][r] of mins lane k.
+template <int FMT>
+__device__ __forceinline__ void ml_pk_chain(const MlPkBlock<FMT>& o, float (&acc)[4][4], float (&accm)[4][4]) {
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[p][r] = __builtin_fmaf(o.dd[r], (float)o.isum[p][r], acc[p][r]);
+    if constexpr (FMT == kQ4_K)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) accm[k][r] = __builtin_fmaf(o.dm[r], o.ms[k][r], accm[k][r]);
+}
+
+// hsum_f32_8 (and the mins' hsum_f32_4) of a pair-lane tile: the lane 32
+// apart holds reference lanes kq +- 4 of the same outputs.
+template <int FMT>
+__device__ __forceinline__ void ml_pk_finish(const float (&acc)[4][4], const float (&accm)[4][4], float (&v)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float s[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) s[p] = acc[p][r] + __shfl_xor(acc[p][r], 32);
+        v[r] = (s[0] + s[2]) + (s[1] + s[3]);
+        if constexpr (FMT == kQ4_K) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
+    }
+}
+
 // LDS stage: A int8 [8][kMlAS], B [64][BS], D f32 [8], H f16 [8][16].
 template <int FMT>
 struct MlStagePk {
@@ -346,8 +490,8 @@ __device__ __forceinline__ void ml_product_pk(const MlOperands& op, ARow arow, B
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, jj = lane & 15;
-    const int h = q & 1;       // chunks 4h .. 4h+3
-    const int upper = q >> 1;  // reference lanes 4..7
+    const int h = q & 1;
+    const int upper = q >> 1;
     const int nb = op.nb;
 
     // ---- staging, as in ml_product: A 8 rows x 16 chunks, B 64 rows x NL
@@ -401,7 +545,6 @@ __device__ __forceinline__ void ml_product_pk(const MlOperands& op, ARow arow, B
     // A row of this lane: activation row j (q < 2) or j - 8 (q >= 2) where
     // that lane carries data, else the zero row
     const bool a_live = (jj < 8) == (upper == 0);
-    // acc[p]: the f32 chains of reference lane p + 4 upper; accm[k]: mins lane k
     float acc[4][4], accm[4][4];
 #pragma unroll
     for (int p = 0; p < 4; p++)
@@ -414,119 +557,15 @@ __device__ __forceinline__ void ml_product_pk(const MlOperands& op, ARow arow, B
         const uint8_t* S = st[b & 1];
         if (b + 1 < nb) issue(b + 1);
         const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
-        const uint8_t* bcol = S + L::B + col * F::BS;
         const uint8_t* arowp = a_live ? S + L::A + (jj & 7) * kMlAS + 16 * h : zero + 16 * h;
-        float dd[4], dm[4];
-        float xd, xdm = 0.f;
-        Q4Scales sc{};
-        uint32_t s6w = 0;                    // Q4_K: six-bit scales of sub-blocks 4h .. 4h+3
-        s16x2_ml q6m[4], q6c[4];             // Q6_K: (sc, sc), (128 - 32 sc, ...) of chunks 4h + cc
-        if constexpr (FMT == kQ4_K) {
-            const u32x4a16 hdr = *(const u32x4a16*)bcol;
-            xd = f16_to_f32(hdr.x);
-            xdm = f16_to_f32(hdr.x >> 16);
-            sc = q4_scales(hdr.y, hdr.z, hdr.w);
-            s6w = h ? sc.sc_hi : sc.sc_lo;
-        } else {
-            xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
-            // scales 2c + upper of chunks c = 4h + cc: bytes upper, 2 + upper of two dwords
-            const uint32_t w0 = ml_lds_win(bcol, sh, 192 + 8 * h) >> (8 * upper);
-            const uint32_t w1 = ml_lds_win(bcol, sh, 196 + 8 * h) >> (8 * upper);
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const int scv = (int)(int8_t)(uint8_t)((cc < 2 ? w0 : w1) >> (16 * (cc & 1)));
-                q6m[cc] = s16x2_ml{(short)scv, (short)scv};
-                q6c[cc] = s16x2_ml{(short)(128 - 32 * scv), (short)(128 - 32 * scv)};
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float yd = *(const float*)(S + L::D + 4 * (4 * h + r));
-            dd[r] = yd * xd;
-            if constexpr (F::kMins) dm[r] = -yd * xdm;
-        }
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const int kq = p + 4 * upper;
-            uint32_t w1[4], w2[4];
-            int mul;  // isum = mul * (stream 1) + (stream 2)
-            if constexpr (FMT == kQ4_K) {
-                // sub-blocks 4h + cc: qs dword at 16 + 32 (2h + cc / 2) + 4 kq, nibble cc % 2
-                const uint32_t qd0 = *(const uint32_t*)(bcol + 16 + 64 * h + 4 * kq);
-                const uint32_t qd1 = *(const uint32_t*)(bcol + 16 + 64 * h + 32 + 4 * kq);
-#pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    const uint32_t qd = cc < 2 ? qd0 : qd1;
-                    const uint32_t nib = (cc & 1) ? ((qd >> 4) & 0x0f0f0f0fu) : (qd & 0x0f0f0f0fu);
-                    const uint32_t s6 = byte_of(s6w, cc);
-                    w1[cc] = bytes_mul_small(nib, s6 >> 3);
-                    w2[cc] = bytes_mul_small(nib, s6 & 7u);
-                }
-                mul = 8;
-            } else {
-                // chunk c = 4h + cc: ql dword at 64 h + 32 (cc % 2) + 4 kq, the high
-                // nibbles for cc >= 2; qh dword at 128 + 32 h + 4 kq, bits 2 cc
-                const uint32_t la = ml_lds_win(bcol, sh, 64 * h + 4 * kq);
-                const uint32_t lb = ml_lds_win(bcol, sh, 64 * h + 32 + 4 * kq);
-                const uint32_t qh = ml_lds_win(bcol, sh, 128 + 32 * h + 4 * kq);
-#pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    const uint32_t l = (cc & 1) ? lb : la;
-                    const uint32_t lo4 = (cc & 2) ? ((l >> 4) & 0x0f0f0f0fu) : (l & 0x0f0f0f0fu);
-                    const uint32_t u = lo4 | (((qh >> (2 * cc)) & 0x03030303u) << 4);
-                    const s16x2_ml u02 = __builtin_bit_cast(s16x2_ml, u & 0x00ff00ffu);
-                    const s16x2_ml u13 = __builtin_bit_cast(s16x2_ml, __builtin_amdgcn_perm(0u, u, 0x0c030c01u));
-                    const uint32_t p02 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u02 * q6m[cc] + q6c[cc]));
-                    const uint32_t p13 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u13 * q6m[cc] + q6c[cc]));
-                    w1[cc] = __builtin_amdgcn_perm(p13, p02, 0x07030501u);
-                    w2[cc] = __builtin_amdgcn_perm(p13, p02, 0x06020400u) ^ 0x80808080u;
-                }
-                mul = 256;
-            }
-            const v4i_ml a = *(const v4i_ml*)(arowp + 32 * kq);
-            const v4i_ml b1 = {(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
-            const v4i_ml b2 = {(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
-            const v4i_ml z = {};
-            const v4i_ml i1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b1, z, 0, 0, 0);
-            const v4i_ml i2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b2, z, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[p][r] = __builtin_fmaf(dd[r], (float)(i1[r] * mul + i2[r]), acc[p][r]);
-#pragma unroll
-            for (int r = 0; r < 4; r++) asm volatile("" : "+v"(acc[p][r]));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (F::kMins) {
-            // as in ml_product; rows 8..15 of the f16 MFMA repeat rows 0..7
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t mwd = k < 2 ? sc.mn_lo : sc.mn_hi;
-                const _Float16 mA = (_Float16)(float)byte_of(mwd, 2 * (k & 1));
-                const _Float16 mB = (_Float16)(float)byte_of(mwd, 2 * (k & 1) + 1);
-                const _Float16 zh = (_Float16)0.f;
-                const v4h_ml bm = q == k ? v4h_ml{mA, mA, mB, mB} : v4h_ml{zh, zh, zh, zh};
-                const v4h_ml am = *(const v4h_ml*)(S + L::H + (jj & 7) * 32 + 8 * q);
-                const v4f_ml zf = {};
-                const v4f_ml ms = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, zf, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; r++) accm[k][r] = __builtin_fmaf(dm[r], ms[r], accm[k][r]);
-#pragma unroll
-                for (int r = 0; r < 4; r++) asm volatile("" : "+v"(accm[k][r]));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+        MlPkBlock<FMT> o;
+        ml_pk_block<FMT>(S + L::B + col * F::BS, sh, arowp, (const float*)(S + L::D), S + L::H, q, jj, o);
+        ml_pk_chain<FMT>(o, acc, accm);
         __builtin_amdgcn_sched_barrier(0);
         if (b + 1 < nb) park(st[(b + 1) & 1]);
         lds_barrier();
     }
-    // hsum_f32_8: the partner lane (32 apart) holds reference lanes kq +- 4
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        float s[4];
-#pragma unroll
-        for (int p = 0; p < 4; p++) s[p] = acc[p][r] + __shfl_xor(acc[p][r], 32);
-        v[r] = (s[0] + s[2]) + (s[1] + s[3]);
-        if constexpr (F::kMins) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
-    }
+    ml_pk_finish<FMT>(acc, accm, v);
 }
 
 }  // namespace iq

@@ -71,7 +71,8 @@ def _covers(path, dtype, m):
 
 
 @pytest.mark.parametrize("path", list(PATHS), ids=list(PATHS.values()))
-@pytest.mark.parametrize("dtype,rows,cols", [(Q4, 256, 2048), (Q6, 130, 4096), (Q8, 96, 2048)])
+@pytest.mark.parametrize("dtype,rows,cols", [(Q4, 256, 2048), (Q4, 90, 4096), (Q6, 130, 4096), (Q6, 70, 2048),
+                                             (Q8, 96, 2048)])
 def test_each_path_bitexact(gpu, oracle, path, dtype, rows, cols):
     """Every fixed kernel, at row counts the dispatch would not give it,
     returns the oracle's bits; a kernel that does not cover a case says so
