@@ -247,15 +247,17 @@ def moe_protocol(layers, xs, logits, out, steps, reps, hip, kernel_bytes):
     return res, per_kernel
 
 
-def time_graph(fn, iters, hip, warmup=3):
+def time_graph(fn, iters, hip, warmup=3, reps=5):
     """`iters` calls of fn(i) captured once in a HIP graph and replayed: GPU
-    time per call without host submission gaps.  Every captured call runs
-    once eagerly first, which grows the library's per-layer workspaces, so
-    the capture itself allocates nothing."""
+    time per call without host submission gaps, the median of `reps` timed
+    replays.  Every captured call runs once eagerly first, which grows the
+    library's per-layer workspaces, so the capture itself allocates
+    nothing."""
     import torch
 
     cap = torch.cuda.Stream()
     t0, t1 = hip.events(2)
+    times = []
     with torch.cuda.stream(cap):
         for i in range(warmup + iters):
             fn(i)
@@ -266,13 +268,14 @@ def time_graph(fn, iters, hip, warmup=3):
                 fn(warmup + i)
         graph.replay()
         torch.cuda.synchronize()
-        hip.record(t0, cap.cuda_stream)
-        graph.replay()
-        hip.record(t1, cap.cuda_stream)
-        torch.cuda.synchronize()
-    ms = hip.ms(t0, t1) / iters
+        for _ in range(reps):
+            hip.record(t0, cap.cuda_stream)
+            graph.replay()
+            hip.record(t1, cap.cuda_stream)
+            torch.cuda.synchronize()
+            times.append(hip.ms(t0, t1) / iters)
     hip.destroy([t0, t1])
-    return ms
+    return float(np.median(times))
 
 
 def host_layer(t):
