@@ -124,129 +124,37 @@ __global__ __launch_bounds__(256) void k_dm_mm_pk(DmArgs a) {
 // waves form their blocks' exact integers in parallel, then the f32 chains
 // pass from wave to wave in block order through LDS, so every output is
 // the one-row kernel's bit for bit.
-template <int FMT>
-struct SkRegion {  // one block of one wave in LDS
-    static constexpr int A = 0;                                    // int8 [8][kMlAS]
-    static constexpr int B = A + 8 * kMlAS;                        // [16][BS]
-    static constexpr int D = B + 16 * MlFmt<FMT>::BS;              // f32 [8]
-    static constexpr int H = D + 32;                               // f16 [8][16] (Q4_K)
-    static constexpr int END = H + (MlFmt<FMT>::kMins ? 8 * 32 : 0);
-};
-constexpr int kSkBPW = 2;  // blocks per wave
-
 template <int FMT, int NW>
 __global__ __launch_bounds__(NW * 64) void k_dm_sk(DmArgs a) {
-    using F = MlFmt<FMT>;
-    using R = SkRegion<FMT>;
-    constexpr int BPW = kSkBPW, NH = FMT == kQ4_K ? 32 : 16;  // handed-over floats per lane
-    __shared__ __align__(16) uint8_t reg[NW][BPW][R::END];
+    __shared__ __align__(16) uint8_t reg[NW][kSkBPW][MlSkRegion<FMT>::END];
     __shared__ __align__(16) uint8_t zero[256];
-    // the chains' hand-over [NH][64] reuses wave 0's stage: wave 0 writes it
-    // after its own blocks, and the other waves' stages stay untouched
-    static_assert(NH * 64 * 4 <= BPW * R::END, "hand-over fits wave 0's stage");
-    float (*hand)[64] = (float (*)[64])reg[0][0];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int q = lane >> 4, jj = lane & 15, h = q & 1;
-    ((uint32_t*)zero)[lane] = 0u;
+    const int q = lane >> 4, jj = lane & 15;
     const int64_t n0 = (int64_t)blockIdx.x * 16;
-    const int rows = a.m, b0 = wave * BPW;
+    const int rows = a.m;
+    MlOperands op;
+    op.aq = a.q;
+    op.ldq = (int64_t)a.nb * 256;
+    op.ad = a.d;
+    op.ldd = a.nb;
+    op.hs = a.hs;
+    op.b0 = op.b1 = a.w + n0 * a.row_bytes;
+    op.bsplit = 16;
+    op.brow_bytes = a.row_bytes;
+    op.nb = a.nb;
     const int64_t last = a.n - 1 - n0;
-    const uint8_t* wbase = a.w + n0 * a.row_bytes;
+    auto brow = [&](int t) -> int64_t { return t < last ? (int64_t)t : last; };
     auto arow = [&](int rr) -> int64_t { return min(rr, rows - 1); };
-
-    // staging of this wave's blocks b0, b0 + 1: A 8 rows x 16 chunks, B 16
-    // rows x NL chunks, D 8 scales, H 8 x 2 chunks (Q4_K), per block
-    constexpr int kA = 8 * 16 * BPW, kB = 16 * F::NL * BPW;
-    constexpr int kAPer = kA / 64, kBPer = (kB + 63) / 64;
-    v4i_ml sa[kAPer];
-    u32x4 sb[kBPer];
-#pragma unroll
-    for (int i = 0; i < kAPer; i++) {
-        const int t = lane + 64 * i, bi = t >> 7, row = (t >> 4) & 7, part = t & 15;
-        sa[i] = *(const v4i_ml*)(a.q + arow(row) * (int64_t)a.nb * 256 + (int64_t)(b0 + bi) * 256 + 16 * part);
-    }
-#pragma unroll
-    for (int i = 0; i < kBPer; i++) {
-        const int t = min(lane + 64 * i, kB - 1);
-        const int cb = t / F::NL, part = t - cb * F::NL, col = cb / BPW, bi = cb - col * BPW;
-        const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
-        const int64_t b = b0 + bi;
-        const int64_t boff = FMT == kQ6_K ? (b * F::BB) & ~(int64_t)3 : b * F::BB;
-        sb[i] = *(const u32x4*)(wbase + (col < last ? col : last) * a.row_bytes + boff + po);
-    }
-    float sd = 0.f;
-    if (lane < 8 * BPW) sd = a.d[arow(lane & 7) * a.nb + b0 + (lane >> 3)];
-    v4i_ml sh16 = {};
-    if constexpr (F::kMins)
-        if (lane < 16 * BPW)
-            sh16 = *(const v4i_ml*)(a.hs + (arow((lane >> 1) & 7) * a.nb + b0 + (lane >> 4)) * 16 + 8 * (lane & 1));
-#pragma unroll
-    for (int i = 0; i < kAPer; i++) {
-        const int t = lane + 64 * i, bi = t >> 7, row = (t >> 4) & 7, part = t & 15;
-        *(v4i_ml*)(reg[wave][bi] + R::A + row * kMlAS + 16 * part) = sa[i];
-    }
-#pragma unroll
-    for (int i = 0; i < kBPer; i++) {
-        const int t = lane + 64 * i;
-        if (t < kB) {
-            const int cb = t / F::NL, part = t - cb * F::NL, col = cb / BPW, bi = cb - col * BPW;
-            const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
-            *(u32x4*)(reg[wave][bi] + R::B + col * F::BS + po) = sb[i];
-        }
-    }
-    if (lane < 8 * BPW) *(float*)(reg[wave][lane >> 3] + R::D + 4 * (lane & 7)) = sd;
-    if constexpr (F::kMins)
-        if (lane < 16 * BPW) *(v4i_ml*)(reg[wave][lane >> 4] + R::H + 32 * ((lane >> 1) & 7) + 16 * (lane & 1)) = sh16;
-    lds_barrier();  // the zero row and every wave's stage
-
-    // this wave's blocks: exact integers and scales
-    const bool a_live = (jj < 8) == (q < 2);
-    MlPkBlock<FMT> o[BPW];
-#pragma unroll
-    for (int bi = 0; bi < BPW; bi++) {
-        const uint8_t* S = reg[wave][bi];
-        const int sh = FMT == kQ6_K ? (int)(((int64_t)(b0 + bi) * F::BB) & 3) : 0;
-        const uint8_t* arowp = a_live ? S + R::A + (jj & 7) * kMlAS + 16 * h : zero + 16 * h;
-        ml_pk_block<FMT>(S + R::B + jj * F::BS, sh, arowp, (const float*)(S + R::D), S + R::H, q, jj, o[bi]);
-    }
-    // the chains, wave 0 first: each wave continues them over its blocks
-    float acc[4][4], accm[4][4];
-#pragma unroll
-    for (int p = 0; p < 4; p++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[p][r] = accm[p][r] = 0.f;
-    for (int w2 = 0; w2 < NW; w2++) {
-        if (wave == w2) {
-            if (w2 > 0) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) acc[i >> 2][i & 3] = hand[i][lane];
-                if constexpr (F::kMins)
-#pragma unroll
-                    for (int i = 0; i < 16; i++) accm[i >> 2][i & 3] = hand[16 + i][lane];
-            }
-#pragma unroll
-            for (int bi = 0; bi < BPW; bi++) ml_pk_chain<FMT>(o[bi], acc, accm);
-            if (w2 < NW - 1) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) hand[i][lane] = acc[i >> 2][i & 3];
-                if constexpr (F::kMins)
-#pragma unroll
-                    for (int i = 0; i < 16; i++) hand[16 + i][lane] = accm[i >> 2][i & 3];
-            }
-        }
-        if (w2 < NW - 1) lds_barrier();
-    }
-    if (wave == NW - 1) {
-        float v[4];
-        ml_pk_finish<FMT>(acc, accm, v);
+    float v[4];
+    ml_product_sk<FMT, NW>(op, arow, brow, reg, zero, v);
+    if (wave == NW - 1 && q < 2) {
         const int64_t n = n0 + jj;
-        if (q < 2)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int rr = 4 * q + r;
-                if (rr < rows && n < a.n) a.y[(int64_t)rr * a.ldy + n] = v[r];
-            }
+        for (int r = 0; r < 4; r++) {
+            const int rr = 4 * q + r;
+            if (rr < rows && n < a.n) a.y[(int64_t)rr * a.ldy + n] = v[r];
+        }
     }
 }
 
