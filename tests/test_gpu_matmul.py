@@ -165,6 +165,22 @@ def test_large_matrix_rows_bitexact(gpu, oracle, large_matrices, dtype):
         assert_bitexact(got, expected, f"{S.NAMES[dtype]} [{rows}x2048] m={m}")
 
 
+def test_large_wide_matrix_rows_bitexact(gpu, oracle):
+    """Width 4096 past 64 MiB (Q4_K [30000 x 4096], 69 MB): 2..8 rows take
+    the pair-lane tile over 16 blocks per row, 9+ rows the 16-row tile; all
+    bitwise the oracle's."""
+    rng = np.random.default_rng(78)
+    rows = 30000
+    w = S.random_matrix(Q4, rows, 4096, rng)
+    mat = Q.QuantizedMatrix.upload(w, Q4, rows, 4096)
+    impl = 1 if oracle.have_avx2() else 0
+    for m in (2, 5, 8, 9):
+        x = S.normal((m, 4096), np.random.default_rng(2100 + m))
+        expected = oracle.matmul(Q4, w, rows, 4096, x, impl=impl, nthreads=8)
+        got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+        assert_bitexact(got, expected, f"Q4_K [{rows}x4096] m={m}")
+
+
 @pytest.mark.parametrize("m", [1, 2, 8, 16])
 def test_joined_attention_projections_match_separate_calls(gpu, m):
     """q/gate [8192 x 2048], k and v [512 x 2048] joined by rows give bitwise
