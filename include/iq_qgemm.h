@@ -238,6 +238,9 @@ int iq_prefill_block_sums(iq_weight_t w, const float *x, int64_t m, float *y, in
  *   down         [n_experts, hidden, inter]   (blk.N.ffn_down_exps)
  *   shared_gate, shared_up [inter, hidden]; shared_down [hidden, inter]
  *   selector     f32 [hidden]                 (blk.N.ffn_gate_inp_shexp)
+ * Expert formats: Q4_K, Q5_K, Q6_K or Q8_0, each matrix pair in its own
+ * (gate and up share one); the shared expert's formats may differ from the
+ * routed experts', as a GGUF file may mix them per tensor.
  * Replaces: QuantizedMoeLayer::load (src/qwen/quantized_moe.rs:141-225) over
  * a fully resident expert cache (src/residency.rs:39-131). */
 typedef struct {

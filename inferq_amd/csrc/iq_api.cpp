@@ -48,7 +48,7 @@ const char* dtype_name(int dtype) {
 int64_t block_elems(int dtype) { return dtype == kQ8_0 ? 32 : 256; }
 int64_t block_bytes(int dtype) { return dtype == kQ4_K ? 144 : dtype == kQ5_K ? 176 : dtype == kQ6_K ? 210 : 34; }
 bool dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0; }
-bool moe_dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ6_K || dtype == kQ8_0; }
+bool moe_dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0; }
 
 namespace {
 

@@ -25,7 +25,7 @@ const char* dtype_name(int dtype);
 int64_t block_elems(int dtype);
 int64_t block_bytes(int dtype);
 bool dtype_ok(int dtype);
-bool moe_dtype_ok(int dtype);  // expert formats of the MoE kernels (no Q5_K)
+bool moe_dtype_ok(int dtype);  // expert formats of the MoE layer
 // Library-owned device workspace of one (device, stream) pair.  A lease
 // holds the library's workspace lock until it is destroyed, so a caller
 // keeps it across every launch that uses the memory: another thread can
@@ -48,6 +48,11 @@ class WsLease {
     void* p_ = nullptr;
 };
 int check_weight(const iq_weight* w);
+// y = x . W^T through the dispatch (or a fixed path), with the caller's
+// workspace when ws is not null (ws_bytes >= matmul_ws_bytes(w, m)).
+size_t matmul_ws_bytes(const iq_weight* w, int64_t m);
+int matmul_impl(const iq_weight* w, const float* x, int64_t m, float* y, void* ws, size_t ws_bytes, int path,
+                int32_t* isum, int32_t* msum, hipStream_t s);
 WeightView view_of(const iq_weight* w);
 // Shape and size checks of a GGUF matrix (QuantizedMatrix::new); row bytes out.
 int check_matrix(int dtype, int64_t rows, int64_t cols, size_t nbytes, int64_t* row_bytes);

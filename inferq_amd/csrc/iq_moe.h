@@ -52,6 +52,14 @@ struct MoeParams {
     int32_t* chunk_group = nullptr;  // [max_chunks] group of each chunk of rows
     int32_t* chunk_r0 = nullptr;     // [max_chunks] first row of the chunk in its group
     int max_chunks = 0;
+    // a shared expert run apart (formats other than the routed experts'):
+    // gate, up, SwiGLU rows [M][I], output [M][H] and the products' workspace
+    float* shared_g = nullptr;
+    float* shared_u = nullptr;
+    float* shared_act = nullptr;
+    float* shared_out = nullptr;
+    void* shared_ws = nullptr;
+    size_t shared_ws_bytes = 0;
 };
 
 // logits_ws[t][e] = x[t] . router[e] (the router matmul of
@@ -59,6 +67,13 @@ struct MoeParams {
 // x[h] * r[h] for h = l, l + 64, ... in order, then the lanes meet in a
 // butterfly; every (token, expert) pair is formed the same way at any M.
 hipError_t launch_moe_router(const MoeParams& p, hipStream_t s);
+
+// A shared expert run apart from the routed experts (formats that differ
+// from theirs): act = SwiGLU(g, u) over n values, then out = residual +
+// (out + shared * sigmoid(x . selector)) for m tokens of width H.
+hipError_t launch_moe_swiglu(const float* g, const float* u, int64_t n, float* act, hipStream_t s);
+hipError_t launch_moe_shared_combine(const float* x, const float* selector, const float* shared, const float* residual,
+                                     int64_t m, int64_t H, float* out, hipStream_t s);
 
 // Launch prep, gate_up and down for one layer call.
 // events (may be null): 4 hipEvent_t recorded before and between the launches.

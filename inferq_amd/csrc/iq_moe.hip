@@ -609,7 +609,8 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
 // kMoeTokenMajorMax tokens; other calls take the grouped paths.
 bool moe1_supported(const MoeParams& p, int gfmt, int dfmt) {
     const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
-    return p.M >= 1 && p.M <= kMoeTokenMajorMax && gfmt != kQ8_0 && dfmt != kQ8_0 && p.H == 2048 && p.I == 512 && nslots <= kMoe1MaxSlots &&
+    const bool fmts = (gfmt == kQ4_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ6_K);
+    return p.M >= 1 && p.M <= kMoeTokenMajorMax && fmts && p.H == 2048 && p.I == 512 && nslots <= kMoe1MaxSlots &&
            p.E <= kMoeMaxExperts;
 }
 
@@ -733,6 +734,7 @@ template <int GFMT>
 hipError_t launch_g(const MoeParams& p, int dfmt, hipStream_t s, hipEvent_t const* ev) {
     switch (dfmt) {
     case kQ4_K: return launch_gd<GFMT, kQ4_K>(p, s, ev);
+    case kQ5_K: return launch_gd<GFMT, kQ5_K>(p, s, ev);
     case kQ6_K: return launch_gd<GFMT, kQ6_K>(p, s, ev);
     case kQ8_0: return launch_gd<GFMT, kQ8_0>(p, s, ev);
     default: return hipErrorInvalidValue;
@@ -760,10 +762,65 @@ hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hip
     if (ev) (void)hipEventRecord(ev[1], s);
     switch (gfmt) {
     case kQ4_K: return launch_g<kQ4_K>(p, dfmt, s, ev);
+    case kQ5_K: return launch_g<kQ5_K>(p, dfmt, s, ev);
     case kQ6_K: return launch_g<kQ6_K>(p, dfmt, s, ev);
     case kQ8_0: return launch_g<kQ8_0>(p, dfmt, s, ev);
     default: return hipErrorInvalidValue;
     }
+}
+
+// ------------------------------------------- a shared expert run apart
+// When the shared expert's formats differ from the routed experts', the
+// layer runs it as plain products (gate and up on x, down on the SwiGLU
+// rows: QuantizedMoeLayer's shared path, src/qwen/quantized_moe.rs:266-273)
+// and these two kernels finish it.
+
+// act[t][i] = (g / (1 + exp(-g))) * u, the reference's SwiGLU.
+__global__ __launch_bounds__(256) void k_moe_swiglu(const float* __restrict__ g, const float* __restrict__ u,
+                                                    int64_t n, float* __restrict__ act) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    act[i] = __fdiv_rn(gv, 1.f + exp_f32(-gv)) * u[i];
+}
+
+// out[t] = residual[t] + (out[t] + shared[t] * sigmoid(x[t] . selector)):
+// `out` holds the routed sum (the routed launches ran without the shared
+// expert and the residual), so the additions keep the fused kernels' order.
+// Grid (ceil(H / 256), M); wave 0 forms the token's gate.
+__global__ __launch_bounds__(256) void k_moe_shared_combine(const float* __restrict__ x,
+                                                            const float* __restrict__ selector,
+                                                            const float* __restrict__ shared,
+                                                            const float* __restrict__ residual, int64_t H,
+                                                            float* __restrict__ out) {
+    __shared__ float s_gate;
+    const int64_t t = blockIdx.y;
+    if (threadIdx.x < 64) {
+        const float gate = selector_gate(x + t * H, selector, H);
+        if (threadIdx.x == 0) s_gate = gate;
+    }
+    __syncthreads();
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (n >= H) return;
+    float v = out[t * H + n] + shared[t * H + n] * s_gate;
+    if (residual) v = residual[t * H + n] + v;  // src/qwen/quantized_layer.rs:212
+    out[t * H + n] = v;
+}
+
+
+
+hipError_t launch_moe_swiglu(const float* g, const float* u, int64_t n, float* act, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_moe_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, n, act);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_shared_combine(const float* x, const float* selector, const float* shared, const float* residual,
+                                     int64_t m, int64_t H, float* out, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_moe_shared_combine, dim3((unsigned)((H + 255) / 256), (unsigned)m), dim3(256), 0, s, x,
+                       selector, shared, residual, H, out);
+    return hipGetLastError();
 }
 
 hipError_t launch_moe_router(const MoeParams& p, hipStream_t s) {

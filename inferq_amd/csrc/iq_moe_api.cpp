@@ -1,6 +1,7 @@
 // iq_moe_api.cpp -- C ABI of the MoE sublayer (include/iq_qgemm.h).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/iq_qgemm.h"
@@ -14,6 +15,12 @@ struct iq_moe {
     iq::MoeParams last;  // parameters of the last forward call
     bool has_last = false;
     int gfmt = 0, dfmt = 0;
+    // A shared expert whose formats differ from the routed experts' runs
+    // apart: the routed launches go without it, then its three products
+    // (views of the caller's matrices) and a combine.
+    bool shared_apart = false;
+    iq_weight sgate, sup, sdown;
+    const float* selector = nullptr;
     std::mutex mu;
     void* ws = nullptr;
     size_t ws_bytes = 0;
@@ -60,7 +67,25 @@ size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
     uint8_t* chg = take((size_t)maxch * 4);
     uint8_t* chr = take((size_t)maxch * 4);
     uint8_t* lgw = L->layer.router ? take((size_t)m * L->layer.E * 4) : nullptr;
+    // the shared expert run apart: gate, up and SwiGLU rows [m x I], its
+    // output [m x H] and the products' workspace
+    uint8_t *sg = nullptr, *su = nullptr, *sa = nullptr, *so = nullptr, *smw = nullptr;
+    size_t smw_bytes = 0;
+    if (L->shared_apart) {
+        sg = take((size_t)m * I * 4);
+        su = take((size_t)m * I * 4);
+        sa = take((size_t)m * I * 4);
+        so = take((size_t)m * H * 4);
+        smw_bytes = std::max({matmul_ws_bytes(&L->sgate, m), matmul_ws_bytes(&L->sup, m), matmul_ws_bytes(&L->sdown, m)});
+        smw = take(smw_bytes);
+    }
     if (p) {
+        p->shared_g = (float*)sg;
+        p->shared_u = (float*)su;
+        p->shared_act = (float*)sa;
+        p->shared_out = (float*)so;
+        p->shared_ws = smw;
+        p->shared_ws_bytes = smw_bytes;
         p->logits_ws = (float*)lgw;
         p->experts = (int32_t*)experts;
         p->weights = (float*)weights;
@@ -96,8 +121,8 @@ IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
         return fail(IQ_ERR_RANGE, "this build supports at most %d experts and top-%d (got %lld, %lld)", kMoeMaxExperts,
                     kMoeMaxTopK, (long long)E, (long long)K);
     if (!moe_dtype_ok(d->gate_dtype) || !moe_dtype_ok(d->down_dtype))
-        return fail(IQ_ERR_DTYPE, "unsupported expert dtypes %d / %d; expected Q4_K, Q6_K or Q8_0", d->gate_dtype,
-                    d->down_dtype);
+        return fail(IQ_ERR_DTYPE, "unsupported expert dtypes %d / %d; expected Q4_K, Q5_K, Q6_K or Q8_0",
+                    d->gate_dtype, d->down_dtype);
     if (H <= 0 || I <= 0 || H % block_elems(d->gate_dtype) || I % block_elems(d->down_dtype) || I % 32)
         return fail(IQ_ERR_SHAPE, "hidden %lld / intermediate %lld do not fit %s gate and %s down blocks",
                     (long long)H, (long long)I, dtype_name(d->gate_dtype), dtype_name(d->down_dtype));
@@ -117,14 +142,36 @@ IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
         if ((uintptr_t)ptr & 15u) return fail(IQ_ERR_INVALID, "device tensors must be 16-byte aligned");
     const int nshared = (d->shared_gate != nullptr) + (d->shared_up != nullptr) + (d->shared_down != nullptr);
     if (nshared != 0 && nshared != 3) return fail(IQ_ERR_INVALID, "shared expert needs gate, up and down matrices");
+    const bool apart = nshared == 3 && (d->shared_gate_dtype != d->gate_dtype || d->shared_down_dtype != d->down_dtype);
     if (nshared == 3) {
         if (!d->selector) return fail(IQ_ERR_INVALID, "shared expert needs its f32 selector vector");
-        if (d->shared_gate_dtype != d->gate_dtype || d->shared_down_dtype != d->down_dtype)
-            return fail(IQ_ERR_DTYPE, "shared expert dtypes %s / %s differ from the routed experts' %s / %s",
-                        dtype_name(d->shared_gate_dtype), dtype_name(d->shared_down_dtype),
-                        dtype_name(d->gate_dtype), dtype_name(d->down_dtype));
+        if (!moe_dtype_ok(d->shared_gate_dtype) || !moe_dtype_ok(d->shared_down_dtype))
+            return fail(IQ_ERR_DTYPE, "unsupported shared expert dtypes %d / %d; expected Q4_K, Q5_K, Q6_K or Q8_0",
+                        d->shared_gate_dtype, d->shared_down_dtype);
+        // the shared matrices are [inter, hidden] and [hidden, inter] in their own formats
+        if (H % block_elems(d->shared_gate_dtype) || I % block_elems(d->shared_down_dtype))
+            return fail(IQ_ERR_SHAPE, "hidden %lld / intermediate %lld do not fit %s shared gate and %s down blocks",
+                        (long long)H, (long long)I, dtype_name(d->shared_gate_dtype),
+                        dtype_name(d->shared_down_dtype));
     }
     iq_moe* L = new iq_moe;
+    if (apart) {
+        L->shared_apart = true;
+        auto view = [&](iq_weight& w, const void* ptr, int dt, int64_t rows, int64_t cols) {
+            w.dtype = dt;
+            w.rows = rows;
+            w.cols = cols;
+            w.row_bytes = row_bytes_of(dt, cols);
+            w.nbytes = (size_t)(rows * w.row_bytes);
+            w.dev = (uint8_t*)ptr;
+            w.owned = false;
+            (void)hipGetDevice(&w.device);
+        };
+        view(L->sgate, d->shared_gate, d->shared_gate_dtype, I, H);
+        view(L->sup, d->shared_up, d->shared_gate_dtype, I, H);
+        view(L->sdown, d->shared_down, d->shared_down_dtype, H, I);
+        L->selector = d->selector;
+    }
     MoeParams& p = L->layer;
     p.H = H;
     p.I = I;
@@ -134,7 +181,7 @@ IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
     p.gate = (const uint8_t*)d->gate;
     p.up = (const uint8_t*)d->up;
     p.down = (const uint8_t*)d->down;
-    if (nshared == 3) {
+    if (nshared == 3 && !apart) {
         p.sgate_w = (const uint8_t*)d->shared_gate;
         p.sup_w = (const uint8_t*)d->shared_up;
         p.sdown_w = (const uint8_t*)d->shared_down;
@@ -214,7 +261,8 @@ static int moe_forward(iq_moe_t L, const float* x, const float* logits, const fl
     p.x = x;
     p.M = (int)m;
     p.out = out;
-    p.residual = residual;
+    // a shared expert run apart adds its term and the residual at the end
+    p.residual = L->shared_apart ? nullptr : residual;
     L->has_last = false;
     hipError_t e = hipSuccess;
     if (logits) {
@@ -226,6 +274,24 @@ static int moe_forward(iq_moe_t L, const float* x, const float* logits, const fl
     }
     e = launch_moe(p, L->gfmt, L->dfmt, s, (hipEvent_t const*)events);
     if (e != hipSuccess) return hip_fail(e, "MoE launch");
+    if (L->shared_apart) {
+        // the reference's shared path: down(SwiGLU(gate . x, up . x)), then
+        // out = residual + (routed + shared * sigmoid(x . selector))
+        const int64_t I = L->layer.I, H = L->layer.H;
+        if (int rc = matmul_impl(&L->sgate, x, m, p.shared_g, p.shared_ws, p.shared_ws_bytes, IQ_PATH_AUTO, nullptr,
+                                 nullptr, s))
+            return rc;
+        if (int rc = matmul_impl(&L->sup, x, m, p.shared_u, p.shared_ws, p.shared_ws_bytes, IQ_PATH_AUTO, nullptr,
+                                 nullptr, s))
+            return rc;
+        e = launch_moe_swiglu(p.shared_g, p.shared_u, m * I, p.shared_act, s);
+        if (e != hipSuccess) return hip_fail(e, "MoE shared SwiGLU launch");
+        if (int rc = matmul_impl(&L->sdown, p.shared_act, m, p.shared_out, p.shared_ws, p.shared_ws_bytes,
+                                 IQ_PATH_AUTO, nullptr, nullptr, s))
+            return rc;
+        e = launch_moe_shared_combine(x, L->selector, p.shared_out, residual, m, H, out, s);
+        if (e != hipSuccess) return hip_fail(e, "MoE shared combine launch");
+    }
     L->last = p;
     L->has_last = true;
     const size_t rb = (size_t)(m * L->layer.K) * 4;
@@ -260,6 +326,8 @@ IQ_API int iq_moe_forward_stage(iq_moe_t L, int stage, iq_stream_t stream) {
     if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
     std::lock_guard<std::mutex> lock(L->mu);
     if (!L->has_last) return fail(IQ_ERR_INVALID, "iq_moe_forward_stage needs a previous iq_moe_forward call");
+    if (L->shared_apart)
+        return fail(IQ_ERR_RANGE, "stage launches cover layers whose shared expert runs in the fused kernels");
     hipError_t e = launch_moe_stage(L->last, L->gfmt, L->dfmt, stage, (hipStream_t)stream);
     if (e == hipErrorNotSupported)
         return fail(IQ_ERR_RANGE, "stage launches cover the single-token path of this layer shape only");

@@ -77,8 +77,8 @@ def moe_layer_tensors(layer: int, lay: dict, router: np.ndarray):
         (f"{p}.ffn_gate_exps.weight", lay["gate_dtype"], [E, I, H], lay["gate"]),
         (f"{p}.ffn_up_exps.weight", lay["gate_dtype"], [E, I, H], lay["up"]),
         (f"{p}.ffn_down_exps.weight", lay["down_dtype"], [E, H, I], lay["down"]),
-        (f"{p}.ffn_gate_shexp.weight", lay["gate_dtype"], [I, H], lay["shared_gate"]),
-        (f"{p}.ffn_up_shexp.weight", lay["gate_dtype"], [I, H], lay["shared_up"]),
-        (f"{p}.ffn_down_shexp.weight", lay["down_dtype"], [H, I], lay["shared_down"]),
+        (f"{p}.ffn_gate_shexp.weight", lay.get("shared_gate_dtype", lay["gate_dtype"]), [I, H], lay["shared_gate"]),
+        (f"{p}.ffn_up_shexp.weight", lay.get("shared_gate_dtype", lay["gate_dtype"]), [I, H], lay["shared_up"]),
+        (f"{p}.ffn_down_shexp.weight", lay.get("shared_down_dtype", lay["down_dtype"]), [H, I], lay["shared_down"]),
         (f"{p}.ffn_gate_inp_shexp.weight", GGML_F32, [H], lay["selector"].astype(np.float32)),
     ]

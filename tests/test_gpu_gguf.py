@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_normwise
+from conftest import assert_bitexact, assert_close_normwise
 from inferq_amd import gguf as G
 from inferq_amd import synth as S
 
@@ -40,8 +40,8 @@ def _device_bytes(ptr, n):
 
 def _host_layer(lay, router, top_k):
     d = dict(lay)
-    d.update(top_k=top_k, normalize=True, shared_gate_dtype=lay["gate_dtype"], shared_down_dtype=lay["down_dtype"],
-             router=router)
+    d.update(top_k=top_k, normalize=True, shared_gate_dtype=lay.get("shared_gate_dtype", lay["gate_dtype"]),
+             shared_down_dtype=lay.get("shared_down_dtype", lay["down_dtype"]), router=router)
     return d
 
 
@@ -104,3 +104,32 @@ def test_qwen_shaped_checkpoint(gpu, oracle, tmp_path):
     res = ck.warm_all_experts(2)
     for li, (lay, router) in enumerate(layers):
         _check_layer(oracle, ck, res, li, lay, router, 8, (1, 8, 40), gpu)
+
+
+def test_reference_mixed_format_checkpoint(gpu, oracle, tmp_path):
+    """The file of the reference's MoE GGUF test (src/qwen/quantized_moe.rs:
+    490-592): Q4_K gate/up and Q5_K down experts, a Q8_0 shared expert with
+    a zero selector, a router favouring expert 1; hidden and intermediate
+    256, two experts, top-1.  Loaded through the checkpoint, an input of
+    ones routes to expert 1 with a finite output, three tokens equal three
+    one-token calls bitwise, and random inputs match the oracle."""
+    rng = np.random.default_rng(491)
+    lay = S.random_moe_layer(256, 256, 2, S.Q4_K, S.Q5_K, rng, shared=False)
+    lay.update({
+        "shared_gate_dtype": S.Q8_0, "shared_down_dtype": S.Q8_0,
+        "shared_gate": S.random_matrix(S.Q8_0, 256, 256, rng), "shared_up": S.random_matrix(S.Q8_0, 256, 256, rng),
+        "shared_down": S.random_matrix(S.Q8_0, 256, 256, rng), "selector": np.zeros(256, np.float32),
+    })
+    router = np.concatenate([np.zeros(256, np.float32), np.full(256, 0.01, np.float32)]).reshape(2, 256)
+    path = str(tmp_path / "moe.gguf")
+    W.write_gguf(path, W.moe_layer_tensors(0, lay, router))
+    ck = G.GgufCheckpoint(path)
+    res = ck.warm_all_experts(1)
+    moe = ck.moe_layer(res, 0, 1)
+    out = moe.forward(torch.ones(1, 256, device=gpu))
+    assert [r.experts for r in out.routes] == [[1]]
+    assert np.isfinite(out.hidden.cpu().numpy()).all()
+    batch = torch.ones(3, 256, device=gpu)
+    singles = np.concatenate([moe.forward(batch[i:i + 1]).hidden.cpu().numpy() for i in range(3)])
+    assert_bitexact(moe.forward(batch).hidden.cpu().numpy(), singles, "3 tokens vs one-token calls")
+    _check_layer(oracle, ck, res, 0, lay, router, 1, (1, 3), gpu)

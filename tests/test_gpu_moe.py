@@ -22,12 +22,14 @@ pytestmark = pytest.mark.gpu
 Q4, Q6, Q8 = S.Q4_K, S.Q6_K, S.Q8_0
 
 
-def _device_layer(layer, top_k, gpu, normalize=True):
+def _device_layer(layer, top_k, gpu, normalize=True, router=None):
     t = {k: torch.from_numpy(v).to(gpu) for k, v in layer.items() if isinstance(v, np.ndarray)}
     return MOE.QuantizedMoeLayer(
         layer["hidden"], layer["inter"], layer["n_experts"], top_k, layer["gate_dtype"], layer["down_dtype"],
         t["gate"], t["up"], t["down"], t.get("shared_gate"), t.get("shared_up"), t.get("shared_down"),
-        t.get("selector"), normalize=normalize), t
+        t.get("selector"), normalize=normalize, shared_gate_dtype=layer.get("shared_gate_dtype"),
+        shared_down_dtype=layer.get("shared_down_dtype"),
+        router=None if router is None else torch.from_numpy(router).to(gpu)), t
 
 
 def _oracle_layer(layer, top_k, normalize=True):
@@ -285,3 +287,87 @@ def test_graph_replays_match_eager_calls(gpu, qwen_layer, m):
             moe.forward_into(xs[(i + 1) % 3], ls[(i + 1) % 3], o)
             torch.cuda.synchronize()
             assert_bitexact(o.cpu().numpy(), eager[(i + 1) % 3], "eager between replays")
+
+
+def _mixed_layer(rng, hidden, inter, n_experts, gate_dtype, down_dtype, shared_gate_dtype, shared_down_dtype):
+    """A layer whose shared expert has its own formats (a GGUF file may mix
+    them per tensor; QuantizedMoeLayer::load takes each as it comes)."""
+    layer = S.random_moe_layer(hidden, inter, n_experts, gate_dtype, down_dtype, rng, shared=False)
+    layer.update({
+        "shared_gate_dtype": shared_gate_dtype, "shared_down_dtype": shared_down_dtype,
+        "shared_gate": S.random_matrix(shared_gate_dtype, inter, hidden, rng),
+        "shared_up": S.random_matrix(shared_gate_dtype, inter, hidden, rng),
+        "shared_down": S.random_matrix(shared_down_dtype, hidden, inter, rng),
+        "selector": rng.standard_normal(hidden, dtype=np.float32) / np.float32(np.sqrt(hidden)),
+    })
+    return layer
+
+
+def test_reference_mixed_format_layer(gpu, oracle):
+    """The reference's own MoE GGUF test layer (src/qwen/quantized_moe.rs:
+    490-592): hidden and intermediate 256, two experts, top-1, Q4_K gate/up,
+    Q5_K down, a Q8_0 shared expert with a zero selector, and a router whose
+    second row is 0.01 everywhere.  On an input of ones the route is expert 1
+    and the output is finite; three tokens in one call equal three one-token
+    calls bitwise (the reference: grouped == token-major); the output matches
+    the oracle within 1e-4 (Q5_K bitwise is unpinned by nature)."""
+    rng = np.random.default_rng(490)
+    layer = _mixed_layer(rng, 256, 256, 2, Q4, S.Q5_K, Q8, Q8)
+    layer["selector"] = np.zeros(256, np.float32)
+    router = np.concatenate([np.zeros(256, np.float32), np.full(256, 0.01, np.float32)]).reshape(2, 256)
+    moe, _ = _device_layer(layer, 1, gpu, router=router)
+    ones = torch.ones(1, 256, device=gpu)
+    out = moe.forward(ones)
+    assert [r.experts for r in out.routes] == [[1]]
+    assert np.isfinite(out.hidden.cpu().numpy()).all()
+    batch = torch.ones(3, 256, device=gpu)
+    wide = moe.forward(batch).hidden.cpu().numpy()
+    singles = np.concatenate([moe.forward(batch[i:i + 1]).hidden.cpu().numpy() for i in range(3)])
+    assert_bitexact(wide, singles, "3 tokens vs one-token calls")
+    x = S.normal((4, 256), rng)
+    logits = S.normal((4, 2), rng)
+    got = moe.forward(torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu))
+    ref, ref_e, _ = oracle.moe_forward(_oracle_layer(layer, 1), x, logits, mode=0, impl=_impl(oracle))
+    assert [r.experts for r in got.routes] == ref_e.tolist()
+    assert_close_normwise(got.hidden.cpu().numpy(), ref, 1e-4, "reference mixed-format layer")
+
+
+@pytest.mark.parametrize("formats", [(Q4, Q6, Q6, Q4), (Q4, Q6, Q8, Q8), (S.Q5_K, Q6, Q4, Q6), (Q4, S.Q5_K, Q4, S.Q5_K)],
+                         ids=["q4q6-shared-q6q4", "q4q6-shared-q8", "q5q6-shared-q4q6", "q4q5-shared-q4q5"])
+def test_mixed_format_layers_match_oracle(gpu, oracle, formats):
+    """Qwen-shaped layers (hidden 2048, intermediate 512, 32 experts, top-4)
+    with Q5_K experts or a shared expert in other formats than the routed
+    ones, at 1, 5 and 40 tokens (token-major, grouped): routes equal the
+    oracle's, outputs within 1e-4 of it, and every token's output bitwise
+    the one-token call's."""
+    g, d, sg, sd = formats
+    rng = np.random.default_rng(sum(formats))
+    layer = _mixed_layer(rng, 2048, 512, 32, g, d, sg, sd)
+    moe, _ = _device_layer(layer, 4, gpu)
+    for m in (1, 5, 40):
+        x = S.normal((m, 2048), rng)
+        logits = S.normal((m, 32), rng)
+        xt, lt = torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu)
+        out = moe.forward(xt, lt)
+        ref, ref_e, _ = oracle.moe_forward(_oracle_layer(layer, 4), x, logits, mode=0, impl=_impl(oracle),
+                                           nthreads=8)
+        assert [r.experts for r in out.routes] == ref_e.tolist(), f"routes m={m}"
+        got = out.hidden.cpu().numpy()
+        assert_close_normwise(got, ref, 1e-4, f"mixed formats {formats} m={m}")
+        if m > 1:
+            singles = np.concatenate([moe.forward(xt[i:i + 1], lt[i:i + 1]).hidden.cpu().numpy() for i in range(m)])
+            assert_bitexact(got, singles, f"{m} tokens vs one-token calls")
+
+
+def test_mixed_format_residual_is_added_last(gpu):
+    """With the shared expert run apart, out = residual + (routed + shared *
+    gate): bitwise the output without the residual, plus the residual."""
+    rng = np.random.default_rng(212)
+    layer = _mixed_layer(rng, 2048, 512, 32, Q4, Q6, Q6, Q4)
+    router = rng.standard_normal((32, 2048), dtype=np.float32) / np.float32(45.0)
+    moe, _ = _device_layer(layer, 4, gpu, router=router)
+    x = torch.from_numpy(S.normal((3, 2048), rng)).to(gpu)
+    r = torch.from_numpy(S.normal((3, 2048), rng)).to(gpu)
+    plain = moe.forward(x).hidden
+    with_res = moe.forward(x, residual=r).hidden
+    assert_bitexact(with_res.cpu().numpy(), (plain + r).cpu().numpy(), "residual + MoE(x)")

@@ -71,9 +71,9 @@ def test_q5k_m_invariance_and_concat(gpu):
                     "Q5_K concatenate_rows")
 
 
-def test_moe_rejects_q5k_experts(gpu):
+def test_moe_refuses_unknown_expert_dtypes(gpu):
     from inferq_amd import moe as MOE
 
     t = torch.zeros(4 * 256 * 176, dtype=torch.uint8, device=gpu)
     with pytest.raises(Q.QgemmError, match="unsupported expert dtypes"):
-        MOE.QuantizedMoeLayer(256, 256, 4, 2, Q5, S.Q6_K, t, t, t)
+        MOE.QuantizedMoeLayer(256, 256, 4, 2, 2, S.Q6_K, t, t, t)  # 2 = Q4_0, not executable
