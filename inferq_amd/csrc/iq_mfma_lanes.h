@@ -1,6 +1,11 @@
-// iq_mfma_lanes.h -- the reference's exact per-lane products on int8 MFMA,
-// for a tile of up to 16 RT activation rows against 64 weight rows (Q4_K or
-// Q6_K), shared by the grouped MoE kernels and the multi-row dense kernel.
+// iq_mfma_lanes.h -- the reference's exact per-lane products on int8 MFMA
+// (Q4_K or Q6_K weights), shared by the grouped MoE kernels and the dense
+// multi-row kernels, in three forms:
+//   ml_product     up to 16 RT activation rows x 64 weight rows;
+//   ml_product_pk  up to 8 activation rows x 64 weight rows, two reference
+//                  lanes per v_mfma_i32_16x16x64_i8;
+//   ml_product_sk  up to 8 activation rows x 16 weight rows, the blocks
+//                  split over the waves and the f32 chains handed on.
 //
 // The reference's lane k (src/qgemm.rs:175-346) owns bytes 4k..4k+3 of every
 // 32-value chunk c of a block: isum_k = sum_c sc_c * dot4(w[c][k], a[c][k])
