@@ -371,3 +371,40 @@ def test_mixed_format_residual_is_added_last(gpu):
     plain = moe.forward(x).hidden
     with_res = moe.forward(x, residual=r).hidden
     assert_bitexact(with_res.cpu().numpy(), (plain + r).cpu().numpy(), "residual + MoE(x)")
+
+
+@pytest.mark.parametrize("m", [1, 40])
+def test_mixed_format_graph_replays_match_eager_calls(gpu, m):
+    """A layer whose shared expert runs apart (its own formats), captured in
+    a HIP graph and replayed with fresh inputs and eager calls between the
+    replays: bitwise the eager output each time."""
+    rng = np.random.default_rng(600 + m)
+    layer = _mixed_layer(rng, 2048, 512, 32, Q4, Q6, Q6, Q4)
+    moe, _ = _device_layer(layer, 4, gpu)
+    xs = [torch.from_numpy(S.normal((m, 2048), rng)).to(gpu) for _ in range(3)]
+    ls = [torch.from_numpy(S.normal((m, 32), rng)).to(gpu) for _ in range(3)]
+    eager = []
+    for x, lg in zip(xs, ls):
+        o = torch.empty(m, 2048, device=gpu)
+        moe.forward_into(x, lg, o)
+        eager.append(o.cpu().numpy())
+    x_buf, l_buf, o_buf = torch.zeros(m, 2048, device=gpu), torch.zeros(m, 32, device=gpu), \
+        torch.empty(m, 2048, device=gpu)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        moe.forward_into(x_buf, l_buf, o_buf)  # sizes the workspace outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        moe.forward_into(x_buf, l_buf, o_buf)
+    for rep in range(2):
+        for i in range(3):
+            x_buf.copy_(xs[i])
+            l_buf.copy_(ls[i])
+            graph.replay()
+            torch.cuda.synchronize()
+            assert_bitexact(o_buf.cpu().numpy(), eager[i], f"replay {rep}.{i} m={m}")
+            o = torch.empty(m, 2048, device=gpu)
+            moe.forward_into(xs[(i + 1) % 3], ls[(i + 1) % 3], o)
+            torch.cuda.synchronize()
+            assert_bitexact(o.cpu().numpy(), eager[(i + 1) % 3], "eager between replays")
