@@ -71,10 +71,9 @@ struct PrefillArgs {
 
 
 // LDS stage of one block: A int8 [ROWS][kAS], B raw Q4_K [COLS][kBS], H f16
-// bsums [ROWS][16], D block scales [ROWS], then a 16-byte sink for idle
-// staging lanes.  Row strides of 32 mod 64 bytes let the fragment reads
-// (16 rows, four 16-byte columns per row) run without bank conflicts on
-// gfx950; strides of 16 mod 64 bytes measure 1.5x slower.
+// bsums [ROWS][16], D block scales [ROWS].  Row strides of 32 mod 64 bytes
+// let the fragment reads (16 rows, four 16-byte columns per row) run without
+// bank conflicts on gfx950; strides of 16 mod 64 bytes measure 1.5x slower.
 constexpr int kAS = 288;  // activation row stride (256 bytes + pad)
 constexpr int kBS = 160;  // Q4_K block stride (144 bytes + pad)
 template <int ROWS, int COLS>
@@ -83,10 +82,6 @@ struct PfTile {
     static constexpr int kRT = ROWS / 16;
     static constexpr int kStA = 0, kStB = kStA + ROWS * kAS, kStH = kStB + COLS * kBS, kStD = kStH + ROWS * 32;
     static constexpr int kStage = kStD + ROWS * 4;
-    // staging chunks of 16 bytes per block: A, B (9 per block), H, D
-    static constexpr int kChA = ROWS * 16, kChB = COLS * 9, kChH = ROWS * 2, kChD = ROWS / 4;
-    static constexpr int kChunks = kChA + kChB + kChH + kChD;
-    static constexpr int kChPer = (kChunks + kThreads - 1) / kThreads;
 };
 
 // Wave w owns all ROWS rows and columns 16w .. 16w+15 of the tile as RT
@@ -98,11 +93,10 @@ struct PfTile {
 template <int ROWS, int COLS, bool DBG>
 __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(PrefillArgs p) {
     using T = PfTile<ROWS, COLS>;
-    constexpr int kThreads = T::kThreads, kChPer = T::kChPer, kChunks = T::kChunks;
-    constexpr int kChA = T::kChA, kChB = T::kChB, kChH = T::kChH;
+    constexpr int kThreads = T::kThreads;
     constexpr int kStA = T::kStA, kStB = T::kStB, kStH = T::kStH, kStD = T::kStD, kStage = T::kStage;
     constexpr int RT = T::kRT;
-    __shared__ __align__(16) uint8_t st[2][kStage + 16];
+    __shared__ __align__(16) uint8_t st[2][kStage];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, jj = lane & 15;
@@ -119,49 +113,52 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
     const int b1 = min(p.nb, b0 + p.bps);
     const int64_t K = (int64_t)p.nb * 256;
 
-    // staging: chunk t = threadIdx.x + kThreads i of a block.  Per chunk a thread
-    // keeps its source in block 0, the stride per block and its LDS offset
-    // (chunks past the block: the sink).  Every thread issues and parks
-    // kChPer chunks per block without branches, so that the waits before the
-    // LDS stores stay exact (a store under a branch leaves the compiler's
-    // count of loads in flight unknown there, and it then waits for more).
-    const uint8_t* gsrc[kChPer];
-    uint32_t gstr[kChPer];
-    int loff[kChPer];
+    // staging straight into LDS (global_load_lds_dwordx4): instruction i of
+    // wave w of W fills the 64 consecutive 16-byte granules (W i + w) * 64 .. +63
+    // of a stage, each lane the granule at base + 16 lane.  The stage keeps
+    // its padded layout (A rows of 18 granules, B columns of 10, then H and
+    // D); pad granules and those past the stage load nothing.
+    constexpr int kGA = ROWS * 18, kGB = COLS * 10, kGH = ROWS * 2, kGD = ROWS / 4;
+    constexpr int kG = kGA + kGB + kGH + kGD;
+    constexpr int kWaves = kThreads / 64, kIPer = (kG + kThreads - 1) / kThreads;
+    static_assert(kStB == kGA * 16 && kStH == kStB + kGB * 16 && kStD == kStH + kGH * 16, "stage layout");
+    const uint8_t* gsrc[kIPer];
+    uint32_t gstr[kIPer];
+    bool gok[kIPer];
 #pragma unroll
-    for (int i = 0; i < kChPer; i++) {
-        int t = min((int)threadIdx.x + kThreads * i, kChunks - 1);
-        if (t < kChA) {
-            gsrc[i] = (const uint8_t*)p.q + (int64_t)(row0 + (t >> 4)) * K + 16 * (t & 15);
+    for (int i = 0; i < kIPer; i++) {
+        int t = (i * kWaves + wave) * 64 + lane;
+        gok[i] = t < kG;
+        t = min(t, kG - 1);
+        if (t < kGA) {
+            const int r = t / 18, gr = t - 18 * r;
+            gok[i] = gok[i] && gr < 16;
+            gsrc[i] = (const uint8_t*)p.q + (int64_t)(row0 + r) * K + 16 * min(gr, 15);
             gstr[i] = 256;
-            loff[i] = kStA + (t >> 4) * kAS + 16 * (t & 15);
-        } else if ((t -= kChA) < kChB) {
-            const int col = t / 9, pc = t - 9 * col;
+        } else if ((t -= kGA) < kGB) {
+            const int col = t / 10, gr = t - 10 * col;
+            gok[i] = gok[i] && gr < 9;
             const int64_t gc = min((int64_t)n0 + col, p.n - 1);
-            gsrc[i] = p.w + gc * p.row_bytes + 16 * pc;
+            gsrc[i] = p.w + gc * p.row_bytes + 16 * min(gr, 8);
             gstr[i] = 144;
-            loff[i] = kStB + col * kBS + 16 * pc;
-        } else if ((t -= kChB) < kChH) {
+        } else if ((t -= kGB) < kGH) {
             gsrc[i] = (const uint8_t*)(p.hs + (int64_t)(row0 + (t >> 1)) * p.nb * 16 + 8 * (t & 1));
             gstr[i] = 32;
-            loff[i] = kStH + 16 * t;
         } else {
-            t -= kChH;
+            t -= kGH;
             gsrc[i] = (const uint8_t*)(p.dT + row0 + 4 * t);
             gstr[i] = (uint32_t)p.mp * 4;
-            loff[i] = kStD + 16 * t;
         }
-        if ((int)threadIdx.x + kThreads * i >= kChunks) loff[i] = kStage;  // sink
     }
-    u32x4a16 stg[kChPer];
-    auto issue = [&](int b) {
+    auto issue = [&](int b, uint8_t* s) {
         b = min(b, b1 - 1);
 #pragma unroll
-        for (int i = 0; i < kChPer; i++) stg[i] = *(const u32x4a16*)(gsrc[i] + (int64_t)b * gstr[i]);
-    };
-    auto park = [&](uint8_t* s) {
-#pragma unroll
-        for (int i = 0; i < kChPer; i++) *(u32x4a16*)(s + loff[i]) = stg[i];
+        for (int i = 0; i < kIPer; i++) {
+            if (gok[i])
+                __builtin_amdgcn_global_load_lds(
+                    (const void __attribute__((address_space(1)))*)(gsrc[i] + (int64_t)b * gstr[i]),
+                    (void __attribute__((address_space(3)))*)(s + (i * kWaves + wave) * 1024), 16, 0, 0);
+        }
     };
 
     float out[RT][4];  // [row tile][r]
@@ -170,15 +167,13 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
 #pragma unroll
         for (int r = 0; r < 4; r++) out[rt][r] = 0.f;
 
-    issue(b0);
-    park(st[0]);
+    issue(b0, st[0]);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's granules are in LDS
     lds_barrier();
 
     for (int b = b0; b < b1; b++) {
         const uint8_t* S = st[(b - b0) & 1];
-        issue(b + 1);
-        // the next block's loads go out before this block's work (left to
-        // itself the scheduler sinks them next to the stores that wait on them)
+        if (b + 1 < b1) issue(b + 1, st[(b - b0 + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* bcol = S + kStB + (16 * wave + jj) * kBS;
         pf_q4k_block<RT, kAS>(S + kStA, bcol, S + kStH, (const float*)(S + kStD), g, jj, out,
@@ -191,9 +186,8 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
                                      }
                                  }
                              });
-        // the next block's loads have had this whole block to land
         __builtin_amdgcn_sched_barrier(0);
-        park(st[(b - b0 + 1) & 1]);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
         lds_barrier();
     }
 
