@@ -283,6 +283,10 @@ constexpr int kMoe1MaxSlots = 12;  // top-k routes plus the shared expert
 // against 195 us in graph replays; 24: 105-108 either way)
 constexpr int kMoeTokenMajorMax = 28;
 constexpr int kMoeRouteLaunchMin = 12;  // calls this wide route in a launch of their own
+// 8-row groups of gate (and of up) per workgroup of the multi-token form:
+// 1, 2 and 4 measure 45.3 / 44.1 / 44.9 us at 8 tokens, 17.2 / 17.0 / 17.9
+// at 2 and 118 / 111 / 109 at 28
+constexpr int kMoe1RowGroups = 2;
 
 // Routing workgroup of token t's gate/up slice: wave 0 routes the token
 // (top-k, exact softmax weights), wave 1 computes the shared-expert gate.
@@ -306,136 +310,18 @@ __device__ void moe1_route(const MoeParams& p, int wave, int t) {
     }
 }
 
-// Grid (I/8, slots + 1, M).  Workgroup (x, s + 1, t): 8 intermediate rows
-// of gate and up of token t's expert at route rank s (or the shared
-// expert), 4 waves each taking a quarter of the NG blocks along hidden.
-// Each wave forms its blocks' exact lane integers and f32 scales; wave 0
-// then advances the accumulators through all NG blocks in order (the
-// reference's chain), reduces them with the hsum trees, applies SwiGLU and
-// stores act[t][s][i].  PRE = false: row 0 of each token holds its routing
-// workgroup (x == 0) and every workgroup finds its expert by a top-k of its
-// own; PRE = true (grid y = slots): a routing launch ran first and the
-// workgroups read the expert ids, which wide calls amortise better.
-template <int GFMT, int NG, bool PRE>
-__global__ __launch_bounds__(256) void k_moe1_gate_up(MoeParams p) {
-    constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
-    static_assert(NG % NW == 0 && (VPL == 8 || VPL == 16 || VPL == 32), "shape");
-    __shared__ __align__(16) int8_t s_q[NG * 256];
-    __shared__ __align__(16) float s_d[NG * 8];
-    __shared__ __align__(16) int16_t s_s8[NG * 8];
-    __shared__ int s_isum[2][8][8][NG];  // [gate/up][row][lane k][block]
-    __shared__ int s_msum[2][8][4][NG];
-    __shared__ float s_dd[2][8][NG], s_dm[2][8][NG];
-    const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K = (int)p.K, t = blockIdx.z;
-    const int nslots = K + (p.sdown_w ? 1 : 0);
-    if (!PRE && blockIdx.y == 0) {
-        if (blockIdx.x == 0) moe1_route(p, wave, t);
-        return;
-    }
-    const int sidx = PRE ? (int)blockIdx.y : (int)blockIdx.y - 1;
-    // small inputs first: logits (or the expert id), and this wave's x blocks
-    constexpr int LPB = 256 / VPL;
-    const int g0 = wave * NB;
-    const int gx = g0 + lane / LPB;  // x block this lane quantises
-    float xv[VPL];
-    int e = (int)p.E;
-    if constexpr (PRE) {
-        if (sidx < K) e = __builtin_amdgcn_readfirstlane(p.experts[t * K + sidx]);
-        q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
-    } else {
-        // wave 0 routes and hands the id over in LDS: the other waves keep
-        // their SIMDs free for the workgroups around them
-        __shared__ int s_e4;
-        q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
-        if (wave == 0 && sidx < K) {
-            float lv[kRoutePer];
-            route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
-            int sel[kMoe1MaxSlots];
-            route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
-            if (lane == 0) s_e4 = sel[sidx];
-        }
-        lds_barrier();
-        if (sidx < K) e = __builtin_amdgcn_readfirstlane(s_e4);
-    }
-    const bool shared = sidx >= K;
-    const uint8_t* gb = shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes;
-    const uint8_t* ub = shared ? p.sup_w : p.up + (int64_t)e * p.g_exp_bytes;
-    const int64_t i = (int64_t)blockIdx.x * 8 + slot;
-    const bool ok = i < p.I;
-    const int64_t ic = ok ? i : p.I - 1;
-    const uint8_t* wrow[2] = {gb + ic * p.g_row_bytes + (int64_t)g0 * WT<GFMT>::kBlockBytes,
-                              ub + ic * p.g_row_bytes + (int64_t)g0 * WT<GFMT>::kBlockBytes};
-    typename WT<GFMT>::T w[2][NB];
-    lanes_load_exact<GFMT, 2, NB>(wrow, k, w);
-    ActView a;
-    a.ng = NG;
-    a.ldq = NG * 256;
-    a.ldd = NG * 8;
-    a.m = 1;
-    a.q = s_q;
-    a.d = s_d;
-    a.s8 = s_s8;
-    quant_q8k_vpl<VPL>(xv, true, 0, gx, a);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const int g = g0 + b;
-            uint32_t av[8];
-            load_act(a, 0, g, k, av);
-            const float yd = a.d[g];
-            if constexpr (GFMT == kQ4_K) {
-                const Q4Dec dec = q4_decode(w[r][b], k);
-                const uint32_t q8s = *(const uint32_t*)(a.s8 + g * 8 + 2 * (k & 3));
-                int32_t isum, msum;
-                float d, dmin;
-                q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
-                s_isum[r][slot][k][g] = isum;
-                if (k < 4) s_msum[r][slot][k][g] = msum;
-                if (k == 0) {
-                    s_dd[r][slot][g] = d;
-                    s_dm[r][slot][g] = dmin;
-                }
-            } else {
-                const Q6Dec dec = q6_decode(w[r][b], k);
-                int32_t isum;
-                float d;
-                q6_dot(dec, av, yd, isum, d);
-                s_isum[r][slot][k][g] = isum;
-                if (k == 0) s_dd[r][slot][g] = d;
-            }
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-    float o[2];
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        float acc = 0.f, accm = 0.f;
-#pragma unroll
-        for (int g = 0; g < NG; g++) {
-            acc = __builtin_fmaf(s_dd[r][slot][g], (float)s_isum[r][slot][k][g], acc);
-            if constexpr (GFMT == kQ4_K) accm = __builtin_fmaf(s_dm[r][slot][g], (float)s_msum[r][slot][k & 3][g], accm);
-        }
-        float v = hsum8(acc);
-        if constexpr (GFMT == kQ4_K) v = v + hsum4(accm);
-        o[r] = v;
-    }
-    // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
-    if (k == 0 && ok) p.act[((int64_t)t * nslots + sidx) * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
-}
-
-// The one-token form on eight waves: gate on waves 0-3 and up on waves 4-7,
-// each wave a quarter of the blocks of one matrix, so each wave forms half
-// the per-block integers of the four-wave kernel.  Wave 0 alone runs the
-// top-k and hands the expert id over in LDS (eight waves each repeating it
-// were slower than four); waves 0-3 quantise x for all eight.  Grid as
-// k_moe1_gate_up<GFMT, NG, false>.
+// The one-token form.  Grid (I/8, slots + 1, M): row 0 of each token
+// holds its routing workgroup (x == 0); workgroup (x, s + 1, t) forms the 8
+// intermediate rows from 8 x of gate and up of token t's expert at route
+// rank s (or the shared expert), split by K over eight waves: gate on
+// waves 0-3 and up on waves 4-7, each wave a quarter of the blocks of one
+// matrix.  Each wave forms its blocks' exact lane integers and f32 scales;
+// wave 0 then advances the accumulators through all NG blocks in order (the
+// reference's chain), reduces them with the hsum trees and applies SwiGLU.
+// Splitting by K shortens the one token's dependent chain: each wave decodes
+// a quarter of a row.  Wave 0 alone runs the top-k and hands the expert id
+// over in LDS (eight waves each repeating it were slower than four); waves
+// 0-3 quantise x for all eight.
 template <int GFMT, int NG>
 __global__ __launch_bounds__(512) void k_moe1_gate_up8(MoeParams p) {
     constexpr int NW = 4, NB = NG / NW, VPL = NB * 4;  // blocks and x values per lane per wave
@@ -538,6 +424,93 @@ __global__ __launch_bounds__(512) void k_moe1_gate_up8(MoeParams p) {
     if (k == 0 && ok) p.act[((int64_t)t * nslots + sidx) * p.I + i] = __fdiv_rn(o[0], 1.f + exp_f32(-o[0])) * o[1];
 }
 
+// The form for 2..kMoeTokenMajorMax tokens: grid (I / (8 RG), slots (+1
+// routing row when !PRE), M), 2 RG waves.  Workgroup (x, s, t): the 8 RG
+// intermediate rows from 8 RG x of gate (waves 0..RG-1) and up (waves
+// RG..2RG-1) of token t's expert at route rank s.  Every wave runs the
+// reference chain of its own 8 rows through all NG blocks (no hand-over
+// between waves), so a workgroup forms 8 RG rows of SwiGLU for one top-k
+// and one x quantisation; the gate waves hand their products to the up
+// waves in LDS.  With many tokens the GPU is full of such workgroups, and
+// the shorter chain of the split-K form no longer pays for its hand-over
+// and its repeated top-k (8 tokens 45.6 -> 44.0 us, 16 tokens 77.6 -> 69.2,
+// 28 tokens 120 -> 111).  The chain, the hsum trees and SwiGLU are the
+// one-token form's, so the outputs are the same bits.  PRE = false: every
+// workgroup finds its expert by a top-k of its own; PRE = true (grid y =
+// slots): k_moe1_route ran first and the workgroups read the expert ids,
+// which wide calls amortise better.
+template <int GFMT, int NG, bool PRE, int RG>
+__global__ __launch_bounds__(128 * RG) void k_moe1_gate_up_rows(MoeParams p) {
+    constexpr int NWQ = 2 * RG < 4 ? 2 * RG : 4;  // waves that quantise x
+    constexpr int VPL = NG * 4 / NWQ;
+    static_assert(VPL == 8 || VPL == 16 || VPL == 32, "shape");
+    __shared__ __align__(16) int8_t s_q[NG * 256];
+    __shared__ __align__(16) float s_d[NG * 8];
+    __shared__ __align__(16) int16_t s_s8[NG * 8];
+    __shared__ float s_g[RG][8];
+    const int lane = threadIdx.x & 63, k = lane & 7, slot = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = wave / RG, rg = wave - r * RG;  // r: 0 gate, 1 up
+    const int K = (int)p.K, t = blockIdx.z;
+    const int nslots = K + (p.sdown_w ? 1 : 0);
+    if (!PRE && blockIdx.y == 0) {
+        if (blockIdx.x == 0) moe1_route(p, wave, t);
+        return;
+    }
+    const int sidx = PRE ? (int)blockIdx.y : (int)blockIdx.y - 1;
+    constexpr int LPB = 256 / VPL;
+    const int gx = wave * (64 / LPB) + lane / LPB;  // x block this lane quantises
+    float xv[VPL];
+    if (wave < NWQ) q8k_vpl_load<VPL>(p.x + (int64_t)t * p.H + (int64_t)gx * 256, xv);
+    int e = (int)p.E;
+    if constexpr (PRE) {
+        if (sidx < K) e = __builtin_amdgcn_readfirstlane(p.experts[t * K + sidx]);
+    } else {
+        __shared__ int s_e;
+        if (wave == 0 && sidx < K) {
+            float lv[kRoutePer];
+            route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
+            int sel[kMoe1MaxSlots];
+            route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
+            if (lane == 0) s_e = sel[sidx];
+        }
+        lds_barrier();
+        if (sidx < K) e = __builtin_amdgcn_readfirstlane(s_e);
+    }
+    const bool shared = sidx >= K;
+    const uint8_t* mb = r == 0 ? (shared ? p.sgate_w : p.gate + (int64_t)e * p.g_exp_bytes)
+                               : (shared ? p.sup_w : p.up + (int64_t)e * p.g_exp_bytes);
+    const int64_t i = ((int64_t)blockIdx.x * RG + rg) * 8 + slot;
+    const bool ok = i < p.I;
+    const int64_t ic = ok ? i : p.I - 1;
+    const uint8_t* wrow[1] = {mb + ic * p.g_row_bytes};
+    typename WT<GFMT>::T w[1][NG];
+    lanes_load_exact<GFMT, 1, NG>(wrow, k, w);
+    ActView a;
+    a.ng = NG;
+    a.ldq = NG * 256;
+    a.ldd = NG * 8;
+    a.m = 1;
+    a.q = s_q;
+    a.d = s_d;
+    a.s8 = s_s8;
+    if (wave < NWQ) quant_q8k_vpl<VPL>(xv, true, 0, gx, a);
+    lds_barrier();  // the quantised x for every wave
+    float acc[1][1] = {{0.f}}, accm[1][1] = {{0.f}};
+    const int64_t arow[1][1] = {{0}};
+    const int mc[1] = {1};
+    lanes_accumulate<GFMT, 1, 1, NG>(w, wrow, 0, NG, NG, a, arow, mc, k, acc, accm);
+    float o[1][1];
+    lanes_finish<GFMT, 1, 1>(acc, accm, o);
+    if (r == 0 && k == 0) s_g[rg][slot] = o[0][0];
+    lds_barrier();
+    // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
+    if (r == 1 && k == 0 && ok) {
+        const float g = s_g[rg][slot];
+        p.act[((int64_t)t * nslots + sidx) * p.I + i] = __fdiv_rn(g, 1.f + exp_f32(-g)) * o[0][0];
+    }
+}
+
 // Routing of every token of a call (grid M, two waves each).
 __global__ __launch_bounds__(128) void k_moe1_route(MoeParams p) { moe1_route(p, (int)(threadIdx.x >> 6), blockIdx.x); }
 
@@ -621,16 +594,17 @@ hipError_t launch_moe1_stage(const MoeParams& p, int stage, hipStream_t s) {
     const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
     const unsigned m = (unsigned)p.M, rows_i = (unsigned)(p.I / 8);
     if (stage == 1) {
+        constexpr int RG = kMoe1RowGroups;
+        const unsigned rows_g = (unsigned)(p.I / (8 * RG));
         if (p.M >= kMoeRouteLaunchMin) {
             hipLaunchKernelGGL(k_moe1_route, dim3(m), dim3(128), 0, s, p);
-            hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8, true>), dim3(rows_i, nslots, m), dim3(256), 0, s, p);
+            hipLaunchKernelGGL((k_moe1_gate_up_rows<GFMT, 8, true, RG>), dim3(rows_g, nslots, m), dim3(128 * RG), 0, s,
+                               p);
         } else if (m == 1) {
-            // one token: eight waves per workgroup halve each wave's block
-            // products (layer 13.1 -> 12.8 us); wider calls fill the GPU
-            // with workgroups and keep four waves (8 tokens: 49 against 58 us)
             hipLaunchKernelGGL((k_moe1_gate_up8<GFMT, 8>), dim3(rows_i, nslots + 1, m), dim3(512), 0, s, p);
         } else {
-            hipLaunchKernelGGL((k_moe1_gate_up<GFMT, 8, false>), dim3(rows_i, nslots + 1, m), dim3(256), 0, s, p);
+            hipLaunchKernelGGL((k_moe1_gate_up_rows<GFMT, 8, false, RG>), dim3(rows_g, nslots + 1, m), dim3(128 * RG), 0,
+                               s, p);
         }
     } else if (stage == 2) {
         hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), m), dim3(64 * nslots), 0, s, p);
