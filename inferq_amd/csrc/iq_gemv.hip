@@ -2,13 +2,23 @@
 // (decode and verify shapes: LM head, dense projections), in the reference's
 // exact f32 order (src/qgemm.rs:175-397 via src/gguf.rs:608-690).
 //
-// Each wave owns groups of 8 consecutive weight rows.  A group is consumed
+// Each wave owns groups of RPW consecutive weight rows.  A group is consumed
 // in slices of 2048 weights (Q8_0: 1024) per row: the wave copies the slice
-// bytes of its 8 rows -- one contiguous span per row -- with 16-byte loads
+// bytes of its rows -- one contiguous span per row -- with 16-byte loads
 // spread evenly over its 64 lanes, parks them in its own LDS region, and
 // decodes from there with the same lane structure as iq_lanes.h (lane
-// (slot, k) owns lane k of row `slot`).  Two slices are in flight per wave:
-// while one is decoded, the loads of the next two are outstanding.
+// (slot, k) owns lane k of row `slot`).
+//
+// Two forms.  Tiles of several input rows (and Q8_0) take groups of 8 rows
+// with two slices in flight per wave: while one is decoded, the loads of
+// the next two are outstanding.  One input row on K-quant weights
+// (k_gemv4) takes groups of 4 rows: lanes 0-7 and 8-15 of a row's 16 form
+// the integers of units 0-3 and 4-7 of the slice, and lanes 0-7 run the
+// reference chain through both halves in unit order.  Half the LDS per wave
+// and one slice in flight (116 VGPRs) give four waves per SIMD instead of
+// two, which hides the decode under the stream: the LM head [248320 x 2048]
+// Q6_K 73.2 -> 67.8 us at steady clocks, [40960 x 2048] Q6_K 21.3 -> 16.2 us,
+// [61440 x 2048] Q4_K 23.8 -> 17.3 us.
 //
 // Every workgroup quantises the input rows itself (from_float, bit-exact to
 // iq_quant.h) into LDS, after issuing its first weight loads, so a call is
@@ -17,7 +27,7 @@
 // Weights are read with non-temporal loads: they stream through once, and
 // keeping them out of the caches' retention lifts sustained HBM throughput.
 //
-// LDS rows are padded so that the 8 rows of a wave start in different bank
+// LDS rows are padded so that the rows of a wave start in different bank
 // groups.  Q6_K blocks at 2 (mod 4) bytes are read as aligned dword pairs and
 // funnel-shifted; the parity of every block in a slice is a compile-time
 // constant because slices hold a multiple of 8 blocks.
@@ -48,14 +58,14 @@ struct GvFmt<kQ8_0> {
     static constexpr int UB = 272, SU = 4, PAD = 96, DPU = 8;  // unit = 8 blocks of 34 B
 };
 
-template <int FMT>
+template <int FMT, int RPW = 8>
 struct GvGeom {
     static constexpr int UB = GvFmt<FMT>::UB, SU = GvFmt<FMT>::SU, DPU = GvFmt<FMT>::DPU;
     static constexpr int SB = UB * SU;               // slice bytes per row
     static constexpr int RS = SB + GvFmt<FMT>::PAD;  // LDS row stride
     static constexpr int CPR = SB / 16;              // 16-byte chunks per row slice
-    static constexpr int NL = (8 * CPR + 63) / 64;   // chunks per lane per slice
-    static constexpr int WAVE_LDS = 8 * RS;
+    static constexpr int NL = (RPW * CPR + 63) / 64;   // chunks per lane per slice
+    static constexpr int WAVE_LDS = RPW * RS;
     static_assert(SB % 16 == 0 && RS % 16 == 0, "slices must be 16-byte granular");
 };
 
@@ -243,15 +253,18 @@ __device__ __forceinline__ Q8Dec q8_decode_lds(const uint8_t* b, int k) {
 
 // ---- the kernel ----------------------------------------------------------------
 
-template <int FMT, int MT>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
-    using G = GvGeom<FMT>;
+template <int FMT, int MT, int RPW>
+__device__ __forceinline__ void gemv_run(const GemvArgs& p) {
+    using G = GvGeom<FMT, RPW>;
+    static_assert(RPW == 8 || (RPW == 4 && MT == 1 && FMT != kQ8_0), "four-row items: one input row, K-quants");
+    constexpr int UPL = RPW == 8 ? G::SU : G::SU / 2;  // units of a slice per lane
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     // wave-uniform in a register the compiler knows is uniform, so that
     // every loop and branch on the item index is scalar
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int k = lane & 7, slot = lane >> 3;
+    const int k = lane & 7, slot = RPW == 8 ? lane >> 3 : lane >> 4;
+    const int half = RPW == 8 ? 0 : (lane >> 3) & 1;
     const int m0 = blockIdx.y * MT;
     const int mc = min(MT, p.m - m0);
     const int nsl = p.nu / G::SU;
@@ -268,8 +281,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
 #pragma unroll
     for (int i = 0; i < G::NL; i++) {
         int q = i * 64 + lane;
-        const bool ok = q < 8 * G::CPR;
-        if (!ok) q = 8 * G::CPR - 1;
+        const bool ok = q < RPW * G::CPR;
+        if (!ok) q = RPW * G::CPR - 1;
         const int r = q / G::CPR, cq = q - r * G::CPR;
         goff[i] = (uint32_t)(r * p.row_bytes + cq * 16);
         loff[i] = ok ? r * G::RS + cq * 16 : -1;
@@ -284,15 +297,15 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
     auto issue = [&](u32x4a16 (&st)[G::NL], int it_) {
         const int it = min(it_, ilast);
         const int g8 = gbase + (it / nsl) * gstride, sl = it - (it / nsl) * nsl;
-        const uint8_t* base = p.w + (int64_t)g8 * 8 * p.row_bytes + (int64_t)sl * G::SB;
-        if ((int64_t)g8 * 8 + 8 <= p.n) {  // uniform: a full group
+        const uint8_t* base = p.w + (int64_t)g8 * RPW * p.row_bytes + (int64_t)sl * G::SB;
+        if ((int64_t)g8 * RPW + RPW <= p.n) {  // uniform: a full group
 #pragma unroll
             for (int i = 0; i < G::NL; i++) st[i] = __builtin_nontemporal_load((const u32x4a16*)(base + goff[i]));
         } else {  // the last group: rows past the end re-read the last row
-            const int last = (int)(p.n - (int64_t)g8 * 8) - 1;
+            const int last = (int)(p.n - (int64_t)g8 * RPW) - 1;
 #pragma unroll
             for (int i = 0; i < G::NL; i++) {
-                const int q = min(i * 64 + lane, 8 * G::CPR - 1);
+                const int q = min(i * 64 + lane, RPW * G::CPR - 1);
                 const int r = q / G::CPR, cq = q - r * G::CPR;
                 st[i] = __builtin_nontemporal_load((const u32x4a16*)(base + (int64_t)min(r, last) * p.row_bytes + cq * 16));
             }
@@ -323,7 +336,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
             float xv[VPL];
             q8k_vpl_load<VPL>(p.x + (int64_t)m0 * p.ldx + (int64_t)gq * 256, xv);
             issue(stA, 0);
-            issue(stB, 1);
+            if constexpr (RPW == 8) issue(stB, 1);
             quant_q8k_vpl<VPL>(xv, true, 0, gq, al, corr);
         };
         if (p.nu == 8) early(std::integral_constant<int, 8>{});
@@ -332,7 +345,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
         float xv[32];
         if (wave < npass) quant_pass_load<MT>(p, m0, mc, wave, xv);
         issue(stA, 0);
-        issue(stB, 1);
+        if constexpr (RPW == 8) issue(stB, 1);
         if (wave < npass) quant_pass_store<FMT, MT>(p, al, corr, wave, xv);
     } else if (npass <= 8) {
         // up to two passes per wave: the wave's input loads, then the first
@@ -343,7 +356,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
         for (int i = 0; i < 2; i++)
             if (wave + 4 * i < npass) quant_pass_load<MT>(p, m0, mc, wave + 4 * i, xv[i]);
         issue(stA, 0);
-        issue(stB, 1);
+        if constexpr (RPW == 8) issue(stB, 1);
 #pragma unroll
         for (int i = 0; i < 2; i++)
             if (wave + 4 * i < npass) quant_pass_store<FMT, MT>(p, al, corr, wave + 4 * i, xv[i]);
@@ -354,14 +367,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
             quant_pass_store<FMT, MT>(p, al, corr, ps, xv);
         }
         issue(stA, 0);
-        issue(stB, 1);
+        if constexpr (RPW == 8) issue(stB, 1);
     }
     lds_barrier();
     if (nitems == 0) return;  // uniform per wave; no barrier follows
 
     const ActLds<FMT, MT> act(smem, p.nu);
     uint8_t* wl = smem + p.act_lds + wave * G::WAVE_LDS;
-    const uint8_t* rowl = wl + slot * G::RS;
+    const uint8_t* rowl = wl + slot * G::RS + half * UPL * G::UB;
     float acc[MT], accm[MT];
 #pragma unroll
     for (int i = 0; i < MT; i++) acc[i] = accm[i] = 0.f;
@@ -374,6 +387,52 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if constexpr (RPW == 4) {
+            // lanes of half h form units 4h .. 4h+3 of the slice; half 0
+            // then runs the chain through its own units and the other
+            // half's (lane ^ 8), in unit order
+            int32_t is[UPL], ms[UPL];
+            float dd[UPL], dm[UPL];
+#pragma unroll
+            for (int j = 0; j < UPL; j++) {
+                const int ug = sl * G::SU + half * UPL + j;
+                const uint8_t* b = rowl + j * G::UB;
+                uint32_t av[8];
+                act.load_q(0, ug, k, av);
+                const float yd = act.d[ug];
+                if constexpr (FMT == kQ4_K) {
+                    const Q4Dec dec = q4_decode_lds(b, k);
+                    const uint32_t q8s = *(const uint32_t*)(act.s8 + (size_t)ug * 8 + 2 * (k & 3));
+                    q4_dot(dec, av, yd, q8s, is[j], ms[j], dd[j], dm[j]);
+                } else {
+                    // unit 4h + j sits at 2j (mod 4)
+                    const Q6Dec dec = (j & 1) ? q6_decode_lds<true>(b, k) : q6_decode_lds<false>(b, k);
+                    int32_t cv[8];
+                    act.load_corr(0, ug, k, cv);
+                    int32_t isum = 0;
+#pragma unroll
+                    for (int c = 0; c < 8; c++) isum = imad24(dec.sc[c], sdot4(dec.v[c], av[c], cv[c]), isum);
+                    is[j] = isum;
+                    dd[j] = yd * dec.xd;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < UPL; j++) {
+                acc[0] = __builtin_fmaf(dd[j], (float)is[j], acc[0]);
+                if constexpr (FMT == kQ4_K) accm[0] = __builtin_fmaf(dm[j], (float)ms[j], accm[0]);
+            }
+#pragma unroll
+            for (int j = 0; j < UPL; j++) {
+                const int pi = __builtin_amdgcn_mov_dpp(is[j], 0x128, 0xF, 0xF, false);  // row_ror:8
+                const float pd = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, dd[j]), 0x128, 0xF, 0xF, false));
+                acc[0] = __builtin_fmaf(pd, (float)pi, acc[0]);
+                if constexpr (FMT == kQ4_K) {
+                    const int pm = __builtin_amdgcn_mov_dpp(ms[j], 0x128, 0xF, 0xF, false);
+                    const float pdm = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, dm[j]), 0x128, 0xF, 0xF, false));
+                    accm[0] = __builtin_fmaf(pdm, (float)pm, accm[0]);
+                }
+            }
+        } else
 #pragma unroll
         for (int u = 0; u < G::SU; u++) {
             const int ug = sl * G::SU + u;
@@ -429,17 +488,27 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
             }
         }
         if (sl == nsl - 1) {
-            const int64_t row = (int64_t)g8 * 8 + slot;
+            const int64_t row = (int64_t)g8 * RPW + slot;
 #pragma unroll
             for (int mi = 0; mi < MT; mi++) {
                 float v = hsum8(acc[mi]);
                 if constexpr (FMT == kQ4_K) v = v + hsum4(accm[mi]);
-                if (k == 0 && row < p.n && (MT == 1 || mi < mc)) p.y[(int64_t)(m0 + mi) * p.ldy + row] = v;
+                if (k == 0 && half == 0 && row < p.n && (MT == 1 || mi < mc)) p.y[(int64_t)(m0 + mi) * p.ldy + row] = v;
                 acc[mi] = accm[mi] = 0.f;
             }
         }
     };
 
+    if constexpr (RPW == 4) {
+        // one slice in flight while the parked one is decoded (past the
+        // last item the last item again, as above)
+        for (int it = 0; it < nitems; it++) {
+            park(stA, wl);
+            issue(stA, it + 1);
+            compute(it);
+        }
+        return;
+    }
     // Two items per trip with one exit at the bottom: every path through
     // the body parks and reissues both buffers in the same order (an odd
     // last item parks and reloads B once more, from L2, without using it).
@@ -451,6 +520,16 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
         issue(stB, it + 3);
         if (it + 1 < nitems) compute(it + 1);
     }
+}
+
+template <int FMT, int MT>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
+    gemv_run<FMT, MT, 8>(p);
+}
+// four workgroups of four waves per CU: at most 128 VGPRs
+template <int FMT>
+__global__ __launch_bounds__(256, 4) void k_gemv4(GemvArgs p) {
+    gemv_run<FMT, 1, 4>(p);
 }
 
 struct DevLimits {
@@ -474,26 +553,38 @@ const DevLimits& limits() {
     return L;
 }
 
-template <int FMT, int MT>
+template <int FMT, int MT, int RPW>
+const void* kfn() {
+    if constexpr (RPW == 4) return (const void*)k_gemv4<FMT>;
+    else return (const void*)k_gemv<FMT, MT>;
+}
+template <int FMT, int MT, int RPW = 8>
 hipError_t launch_t(GemvArgs args, hipStream_t s) {
-    using G = GvGeom<FMT>;
+    using G = GvGeom<FMT, RPW>;
     args.act_lds = act_lds_bytes<FMT, MT>(args.nu);
+    args.groups = (int)((args.n + RPW - 1) / RPW);
     const size_t lds = (size_t)args.act_lds + 4 * G::WAVE_LDS;
     const DevLimits& L = limits();
     if (lds > (size_t)L.lds_block) return hipErrorNotSupported;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv<FMT, MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        hipError_t e = hipFuncSetAttribute(kfn<FMT, MT, RPW>(), hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds);
         if (e != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorNotSupported;
         }
     }
-    const int per_cu = (int)(L.lds_cu / lds);
+    int per_cu = (int)(L.lds_cu / lds);
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn<FMT, MT, RPW>(), 256, lds) == hipSuccess &&
+        occ > 0 && occ < per_cu)
+        per_cu = occ;
+    (void)hipGetLastError();
     const int64_t wgs = ((int64_t)args.groups + 3) / 4;
     const int64_t cap = (int64_t)L.cus * (per_cu < 1 ? 1 : per_cu);
     dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)((args.m + MT - 1) / MT));
-    hipLaunchKernelGGL((k_gemv<FMT, MT>), grid, dim3(256), lds, s, args);
+    if constexpr (RPW == 4) hipLaunchKernelGGL((k_gemv4<FMT>), grid, dim3(256), lds, s, args);
+    else hipLaunchKernelGGL((k_gemv<FMT, MT>), grid, dim3(256), lds, s, args);
     return hipGetLastError();
 }
 
@@ -508,7 +599,9 @@ hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
     const int mt_min = args.nu <= 16 ? 1 : 2;  // one-row tiles quantise at most 16 groups
     while (mt > mt_min && (int64_t)args.groups * ((m + mt - 1) / mt) < 2048) mt /= 2;
     switch (mt) {
-    case 1: return launch_t<FMT, 1>(args, s);
+    case 1:
+        if constexpr (FMT != kQ8_0) return launch_t<FMT, 1, 4>(args, s);
+        else return launch_t<FMT, 1>(args, s);
     case 2: return launch_t<FMT, 2>(args, s);
     case 4: return launch_t<FMT, 4>(args, s);
     default: return launch_t<FMT, 8>(args, s);

@@ -144,10 +144,12 @@ def test_concatenated_rows_match_separate_matrices(gpu):
 @pytest.fixture(scope="module")
 def large_matrices():
     """Matrices past the size where 2..63-row calls take the exact-order MFMA
-    kernel (iq_dense_mfma.hip): Q6_K [40960 x 2048] (68.8 MB, LM-head-like)
-    and Q4_K [61440 x 2048] (70.8 MB)."""
+    kernel (iq_dense_mfma.hip) and one-row calls the four-row GEMV items:
+    Q6_K [40962 x 2048] (68.8 MB, LM-head-like) and Q4_K [61441 x 2048]
+    (70.8 MB); neither row count is a multiple of 4 or 8, so every kernel
+    ends on a ragged group."""
     rng = np.random.default_rng(77)
-    return {Q6: (S.random_matrix(Q6, 40960, 2048, rng), 40960), Q4: (S.random_matrix(Q4, 61440, 2048, rng), 61440)}
+    return {Q6: (S.random_matrix(Q6, 40962, 2048, rng), 40962), Q4: (S.random_matrix(Q4, 61441, 2048, rng), 61441)}
 
 
 @pytest.mark.parametrize("dtype", [Q6, Q4], ids=["q6k", "q4k"])
@@ -166,15 +168,16 @@ def test_large_matrix_rows_bitexact(gpu, oracle, large_matrices, dtype):
 
 
 def test_large_wide_matrix_rows_bitexact(gpu, oracle):
-    """Width 4096 past 64 MiB (Q4_K [30000 x 4096], 69 MB): 2..8 rows take
-    the pair-lane tile over 16 blocks per row, 9+ rows the 16-row tile; all
-    bitwise the oracle's."""
+    """Width 4096 past 64 MiB (Q4_K [30000 x 4096], 69 MB): one row takes the
+    four-row GEMV items over two slices per row, 2..8 rows the pair-lane
+    tile over 16 blocks per row, 9+ rows the 16-row tile; all bitwise the
+    oracle's."""
     rng = np.random.default_rng(78)
     rows = 30000
     w = S.random_matrix(Q4, rows, 4096, rng)
     mat = Q.QuantizedMatrix.upload(w, Q4, rows, 4096)
     impl = 1 if oracle.have_avx2() else 0
-    for m in (2, 5, 8, 9):
+    for m in (1, 2, 5, 8, 9):
         x = S.normal((m, 4096), np.random.default_rng(2100 + m))
         expected = oracle.matmul(Q4, w, rows, 4096, x, impl=impl, nthreads=8)
         got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
