@@ -167,6 +167,7 @@ def time_moe(layers, xs, logits, out, steps, warmup, hip, stream):
 
 MALL_BYTES = 256 << 20          # MI355X Infinity Cache
 MIN_STREAM_BYTES = 2 * MALL_BYTES  # distinct bytes a timed graph must stream
+SETTLE_MS = 30.0  # untimed graph replays before each timed secondary line
 
 
 class GraphSet:
@@ -247,12 +248,15 @@ def moe_protocol(layers, xs, logits, out, steps, reps, hip, kernel_bytes):
     return res, per_kernel
 
 
-def time_graph(fn, iters, hip, warmup=3, reps=5):
+def time_graph(fn, iters, hip, warmup=3, reps=5, settle_ms=SETTLE_MS):
     """`iters` calls of fn(i) captured once in a HIP graph and replayed: GPU
     time per call without host submission gaps, the median of `reps` timed
     replays.  Every captured call runs once eagerly first, which grows the
     library's per-layer workspaces, so the capture itself allocates
-    nothing."""
+    nothing.  Before the timed replays the graph runs untimed for about
+    `settle_ms`: a large stream (the LM head) measures 10-20% slower in its
+    first few milliseconds on an idle MI355X than once the clocks have
+    settled, which is the state of a decode loop."""
     import torch
 
     cap = torch.cuda.Stream()
@@ -266,7 +270,12 @@ def time_graph(fn, iters, hip, warmup=3, reps=5):
         with torch.cuda.graph(graph, stream=cap):
             for i in range(iters):
                 fn(warmup + i)
+        hip.record(t0, cap.cuda_stream)
         graph.replay()
+        hip.record(t1, cap.cuda_stream)
+        torch.cuda.synchronize()
+        for _ in range(min(200, int(settle_ms / max(hip.ms(t0, t1), 1e-3)))):
+            graph.replay()
         torch.cuda.synchronize()
         for _ in range(reps):
             hip.record(t0, cap.cuda_stream)
