@@ -273,11 +273,19 @@ hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ld
     if (hipError_t e = hipGetLastError()) return e;
     // up to 8 rows: the split-K tile on mid-size matrices of width 2048 or 4096
     const bool sk = m <= 8 && (a.nb == 8 || a.nb == 16) && w.rows * w.row_bytes <= kDmSkMaxBytes;
+    // 16-row tiles up to 16 rows, and wider where 32-row tiles would leave
+    // the GPU short of workgroups (at most 256 of them for Q4_K, 128 for
+    // Q6_K, whose 16-row tiles cost more): [2048 x 4096] Q4_K at 64 / 256
+    // rows 35.4 -> 27.1 / 37.2 -> 30.9 us, [4096 x 2048] Q6_K at 64 rows
+    // 21.7 -> 18.2 us; from 512 workgroups the 32-row tiles win (Q6_K
+    // [8192 x 2048] at 256 rows 45.4 against 59.5 us)
+    const int64_t g32 = (w.rows + kMlCols - 1) / kMlCols * ((m + 31) / 32);
+    const bool rt1 = m <= 16 || g32 <= (w.dtype == kQ4_K ? 256 : 128);
     if (w.dtype == kQ4_K)
         return sk ? launch_sk<kQ4_K>(a, s) : m <= 8 ? launch_pk<kQ4_K>(a, s)
-                                       : m <= 16 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);
+                                       : rt1 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);
     return sk ? launch_sk<kQ6_K>(a, s) : m <= 8 ? launch_pk<kQ6_K>(a, s)
-                                   : m <= 16 ? launch_t<kQ6_K, 1>(a, s) : launch_t<kQ6_K, 2>(a, s);
+                                   : rt1 ? launch_t<kQ6_K, 1>(a, s) : launch_t<kQ6_K, 2>(a, s);
 }
 
 }  // namespace iq
