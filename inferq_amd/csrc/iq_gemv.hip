@@ -9,16 +9,17 @@
 // decodes from there with the same lane structure as iq_lanes.h (lane
 // (slot, k) owns lane k of row `slot`).
 //
-// Two forms.  Tiles of several input rows (and Q8_0) take groups of 8 rows
-// with two slices in flight per wave: while one is decoded, the loads of
-// the next two are outstanding.  One input row on K-quant weights
-// (k_gemv4) takes groups of 4 rows: lanes 0-7 and 8-15 of a row's 16 form
-// the integers of units 0-3 and 4-7 of the slice, and lanes 0-7 run the
-// reference chain through both halves in unit order.  Half the LDS per wave
-// and one slice in flight (116 VGPRs) give four waves per SIMD instead of
-// two, which hides the decode under the stream: the LM head [248320 x 2048]
-// Q6_K 73.2 -> 67.8 us at steady clocks, [40960 x 2048] Q6_K 21.3 -> 16.2 us,
-// [61440 x 2048] Q4_K 23.8 -> 17.3 us.
+// Two forms.  Tiles of several input rows take groups of 8 rows with two
+// slices in flight per wave: while one is decoded, the loads of the next
+// two are outstanding.  One-row tiles (k_gemv4) take groups of 4 rows:
+// lanes 0-7 and 8-15 of a row's 16 form the chain steps of the first and
+// the second half of the slice's units, and lanes 0-7 run the reference
+// chain through both halves in order.  Half the LDS per wave and, on grids
+// that fill the GPU, one slice in flight (Q6_K: 116 VGPRs) give four waves
+// per SIMD instead of two, which hides the decode under the stream: the LM
+// head [248320 x 2048] Q6_K 73.2 -> 67.8 us at steady clocks, [40960 x
+// 2048] Q6_K 21.3 -> 16.2 us, [61440 x 2048] Q4_K 23.8 -> 17.3 us; on small
+// grids the shorter items alone pay (Q8_0 [4096 x 2048] 7.25 -> 6.3 us).
 //
 // Every workgroup quantises the input rows itself (from_float, bit-exact to
 // iq_quant.h) into LDS, after issuing its first weight loads, so a call is
@@ -253,10 +254,10 @@ __device__ __forceinline__ Q8Dec q8_decode_lds(const uint8_t* b, int k) {
 
 // ---- the kernel ----------------------------------------------------------------
 
-template <int FMT, int MT, int RPW>
+template <int FMT, int MT, int RPW, int NBUF>
 __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
     using G = GvGeom<FMT, RPW>;
-    static_assert(RPW == 8 || (RPW == 4 && MT == 1 && FMT != kQ8_0), "four-row items: one input row, K-quants");
+    static_assert(RPW == 8 || (RPW == 4 && MT == 1), "four-row items: one input row");
     constexpr int UPL = RPW == 8 ? G::SU : G::SU / 2;  // units of a slice per lane
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -336,7 +337,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
             float xv[VPL];
             q8k_vpl_load<VPL>(p.x + (int64_t)m0 * p.ldx + (int64_t)gq * 256, xv);
             issue(stA, 0);
-            if constexpr (RPW == 8) issue(stB, 1);
+            if constexpr (NBUF == 2) issue(stB, 1);
             quant_q8k_vpl<VPL>(xv, true, 0, gq, al, corr);
         };
         if (p.nu == 8) early(std::integral_constant<int, 8>{});
@@ -345,7 +346,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
         float xv[32];
         if (wave < npass) quant_pass_load<MT>(p, m0, mc, wave, xv);
         issue(stA, 0);
-        if constexpr (RPW == 8) issue(stB, 1);
+        if constexpr (NBUF == 2) issue(stB, 1);
         if (wave < npass) quant_pass_store<FMT, MT>(p, al, corr, wave, xv);
     } else if (npass <= 8) {
         // up to two passes per wave: the wave's input loads, then the first
@@ -356,7 +357,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
         for (int i = 0; i < 2; i++)
             if (wave + 4 * i < npass) quant_pass_load<MT>(p, m0, mc, wave + 4 * i, xv[i]);
         issue(stA, 0);
-        if constexpr (RPW == 8) issue(stB, 1);
+        if constexpr (NBUF == 2) issue(stB, 1);
 #pragma unroll
         for (int i = 0; i < 2; i++)
             if (wave + 4 * i < npass) quant_pass_store<FMT, MT>(p, al, corr, wave + 4 * i, xv[i]);
@@ -367,7 +368,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
             quant_pass_store<FMT, MT>(p, al, corr, ps, xv);
         }
         issue(stA, 0);
-        if constexpr (RPW == 8) issue(stB, 1);
+        if constexpr (NBUF == 2) issue(stB, 1);
     }
     lds_barrier();
     if (nitems == 0) return;  // uniform per wave; no barrier follows
@@ -388,17 +389,31 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if constexpr (RPW == 4) {
-            // lanes of half h form units 4h .. 4h+3 of the slice; half 0
-            // then runs the chain through its own units and the other
-            // half's (lane ^ 8), in unit order
-            int32_t is[UPL], ms[UPL];
-            float dd[UPL], dm[UPL];
+            // lanes of half h form the chain steps of units UPL h ..
+            // UPL h + UPL - 1 of the slice (one step per unit, Q8_0 one per
+            // 32-value block); half 0 then runs the chain through its own
+            // steps and the other half's (lane ^ 8), in order
+            constexpr int SPU = FMT == kQ8_0 ? 8 : 1, NS = UPL * SPU;
+            int32_t is[NS], ms[NS];
+            float dd[NS], dm[NS];
 #pragma unroll
             for (int j = 0; j < UPL; j++) {
                 const int ug = sl * G::SU + half * UPL + j;
                 const uint8_t* b = rowl + j * G::UB;
                 uint32_t av[8];
                 act.load_q(0, ug, k, av);
+                if constexpr (FMT == kQ8_0) {
+                    const Q8Dec dec = q8_decode_lds(b, k);
+                    const float* dp = act.d + (size_t)ug * 8;
+                    const f32x4 d0 = *(const f32x4*)dp, d1 = *(const f32x4*)(dp + 4);
+                    const float yd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                    for (int c = 0; c < 8; c++) {
+                        is[8 * j + c] = sdot4(dec.q[c], av[c], 0);
+                        dd[8 * j + c] = dec.d[c] * yd[c];
+                    }
+                    continue;
+                }
                 const float yd = act.d[ug];
                 if constexpr (FMT == kQ4_K) {
                     const Q4Dec dec = q4_decode_lds(b, k);
@@ -417,12 +432,12 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
                 }
             }
 #pragma unroll
-            for (int j = 0; j < UPL; j++) {
+            for (int j = 0; j < NS; j++) {
                 acc[0] = __builtin_fmaf(dd[j], (float)is[j], acc[0]);
                 if constexpr (FMT == kQ4_K) accm[0] = __builtin_fmaf(dm[j], (float)ms[j], accm[0]);
             }
 #pragma unroll
-            for (int j = 0; j < UPL; j++) {
+            for (int j = 0; j < NS; j++) {
                 const int pi = __builtin_amdgcn_mov_dpp(is[j], 0x128, 0xF, 0xF, false);  // row_ror:8
                 const float pd = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, dd[j]), 0x128, 0xF, 0xF, false));
                 acc[0] = __builtin_fmaf(pd, (float)pi, acc[0]);
@@ -499,7 +514,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
         }
     };
 
-    if constexpr (RPW == 4) {
+    if constexpr (NBUF == 1) {
         // one slice in flight while the parked one is decoded (past the
         // last item the last item again, as above)
         for (int it = 0; it < nitems; it++) {
@@ -524,12 +539,17 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
 
 template <int FMT, int MT>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
-    gemv_run<FMT, MT, 8>(p);
+    gemv_run<FMT, MT, 8, 2>(p);
 }
-// four workgroups of four waves per CU: at most 128 VGPRs
-template <int FMT>
-__global__ __launch_bounds__(256, 4) void k_gemv4(GemvArgs p) {
-    gemv_run<FMT, 1, 4>(p);
+// Four-row items.  NBUF = 1 (one slice in flight): four workgroups of four
+// waves per CU, at most 128 VGPRs, for grids that fill the GPU; NBUF = 2
+// (two slices in flight, up to 144 VGPRs) for grids of under two
+// workgroups per CU, whose waves have nothing to overlap with but their own
+// next slice (Q8_0 [4096 x 2048] 6.9 -> 6.3 us, [4096 x 4096] 9.8 -> 8.2 us;
+// [16384 x 2048] 11.3 against 13.0 us the other way round).
+template <int FMT, int NBUF>
+__global__ __launch_bounds__(256, NBUF == 1 ? 4 : 3) void k_gemv4(GemvArgs p) {
+    gemv_run<FMT, 1, 4, NBUF>(p);
 }
 
 struct DevLimits {
@@ -553,12 +573,12 @@ const DevLimits& limits() {
     return L;
 }
 
-template <int FMT, int MT, int RPW>
+template <int FMT, int MT, int RPW, int NBUF>
 const void* kfn() {
-    if constexpr (RPW == 4) return (const void*)k_gemv4<FMT>;
+    if constexpr (RPW == 4) return (const void*)k_gemv4<FMT, NBUF>;
     else return (const void*)k_gemv<FMT, MT>;
 }
-template <int FMT, int MT, int RPW = 8>
+template <int FMT, int MT, int RPW = 8, int NBUF = 2>
 hipError_t launch_t(GemvArgs args, hipStream_t s) {
     using G = GvGeom<FMT, RPW>;
     args.act_lds = act_lds_bytes<FMT, MT>(args.nu);
@@ -567,7 +587,7 @@ hipError_t launch_t(GemvArgs args, hipStream_t s) {
     const DevLimits& L = limits();
     if (lds > (size_t)L.lds_block) return hipErrorNotSupported;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(kfn<FMT, MT, RPW>(), hipFuncAttributeMaxDynamicSharedMemorySize,
+        hipError_t e = hipFuncSetAttribute(kfn<FMT, MT, RPW, NBUF>(), hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds);
         if (e != hipSuccess) {
             (void)hipGetLastError();
@@ -576,14 +596,14 @@ hipError_t launch_t(GemvArgs args, hipStream_t s) {
     }
     int per_cu = (int)(L.lds_cu / lds);
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn<FMT, MT, RPW>(), 256, lds) == hipSuccess &&
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn<FMT, MT, RPW, NBUF>(), 256, lds) == hipSuccess &&
         occ > 0 && occ < per_cu)
         per_cu = occ;
     (void)hipGetLastError();
     const int64_t wgs = ((int64_t)args.groups + 3) / 4;
     const int64_t cap = (int64_t)L.cus * (per_cu < 1 ? 1 : per_cu);
     dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)((args.m + MT - 1) / MT));
-    if constexpr (RPW == 4) hipLaunchKernelGGL((k_gemv4<FMT>), grid, dim3(256), lds, s, args);
+    if constexpr (RPW == 4) hipLaunchKernelGGL((k_gemv4<FMT, NBUF>), grid, dim3(256), lds, s, args);
     else hipLaunchKernelGGL((k_gemv<FMT, MT>), grid, dim3(256), lds, s, args);
     return hipGetLastError();
 }
@@ -599,9 +619,11 @@ hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
     const int mt_min = args.nu <= 16 ? 1 : 2;  // one-row tiles quantise at most 16 groups
     while (mt > mt_min && (int64_t)args.groups * ((m + mt - 1) / mt) < 2048) mt /= 2;
     switch (mt) {
-    case 1:
-        if constexpr (FMT != kQ8_0) return launch_t<FMT, 1, 4>(args, s);
-        else return launch_t<FMT, 1>(args, s);
+    case 1: {
+        const int64_t wgs = ((args.n + 3) / 4 + 3) / 4 * m;  // four-row items, one-row tiles
+        if (wgs < 2 * (int64_t)limits().cus) return launch_t<FMT, 1, 4, 2>(args, s);
+        return launch_t<FMT, 1, 4, 1>(args, s);
+    }
     case 2: return launch_t<FMT, 2>(args, s);
     case 4: return launch_t<FMT, 4>(args, s);
     default: return launch_t<FMT, 8>(args, s);
