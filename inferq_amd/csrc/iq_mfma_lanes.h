@@ -606,7 +606,9 @@ __device__ __forceinline__ void ml_product_sk(const MlOperands& op, ARow arow, B
     // the chains' hand-over [NH][64] reuses wave 0's stage: wave 0 writes it
     // after its own blocks, and the other waves' stages stay untouched
     static_assert(NH * 64 * 4 <= BPW * R::END, "hand-over fits wave 0's stage");
-    float (*hand)[64] = (float (*)[64])reg[0][0];
+    // [NH / 4][64] float4: one 16-byte LDS access per four chains, lanes
+    // 16 bytes apart (no bank conflicts)
+    f32x4 (*hand)[64] = (f32x4 (*)[64])reg[0][0];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, jj = lane & 15, h = q & 1;
@@ -678,19 +680,25 @@ __device__ __forceinline__ void ml_product_sk(const MlOperands& op, ARow arow, B
         if (wave == w2) {
             if (w2 > 0) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i >> 2][i & 3] = hand[i][lane];
+                for (int p = 0; p < 4; p++) {
+                    const f32x4 t = hand[p][lane];
+                    acc[p][0] = t.x; acc[p][1] = t.y; acc[p][2] = t.z; acc[p][3] = t.w;
+                }
                 if constexpr (F::kMins)
 #pragma unroll
-                    for (int i = 0; i < 16; i++) accm[i >> 2][i & 3] = hand[16 + i][lane];
+                    for (int p = 0; p < 4; p++) {
+                        const f32x4 t = hand[4 + p][lane];
+                        accm[p][0] = t.x; accm[p][1] = t.y; accm[p][2] = t.z; accm[p][3] = t.w;
+                    }
             }
 #pragma unroll
             for (int bi = 0; bi < BPW; bi++) ml_pk_chain<FMT>(o[bi], acc, accm);
             if (w2 < NW - 1) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) hand[i][lane] = acc[i >> 2][i & 3];
+                for (int p = 0; p < 4; p++) hand[p][lane] = f32x4{acc[p][0], acc[p][1], acc[p][2], acc[p][3]};
                 if constexpr (F::kMins)
 #pragma unroll
-                    for (int i = 0; i < 16; i++) hand[16 + i][lane] = accm[i >> 2][i & 3];
+                    for (int p = 0; p < 4; p++) hand[4 + p][lane] = f32x4{accm[p][0], accm[p][1], accm[p][2], accm[p][3]};
             }
         }
         if (w2 < NW - 1) lds_barrier();
