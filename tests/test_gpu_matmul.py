@@ -20,7 +20,8 @@ Q4, Q6, Q8 = S.Q4_K, S.Q6_K, S.Q8_0
 
 # (dtype, rows, cols): the reference test matrix shape [96 x 512] for each
 # format (src/gguf.rs:1630-1677), the BASELINE shapes, ragged row counts
-# (not a multiple of 8) and an odd number of Q6_K blocks per row.  Widths
+# (not a multiple of 8 or 4, down to matrices of fewer rows than one GEMV
+# row group) and an odd number of Q6_K blocks per row.  Widths
 # whose block count suits the GEMV kernel (iq_gemv.hip) run it, in tiles of
 # 8 rows past 8 input rows (up to 63 on matrices this small); the others run
 # the lane kernel (iq_lanes.hip).
@@ -29,6 +30,7 @@ SHAPES = [
     (Q4, 1024, 2048), (Q6, 2048, 512), (Q8, 4096, 2048),
     (Q4, 2048, 4096), (Q6, 37, 768), (Q8, 45, 96), (Q4, 13, 256),
     (Q6, 300, 2048), (Q6, 64, 4096), (Q4, 77, 2048), (Q8, 19, 1024), (Q6, 5, 6144), (Q8, 40, 4096),
+    (Q8, 3, 2048), (Q8, 1, 4096), (Q4, 2, 2048), (Q6, 3, 4096),
 ]
 ROWS = [1, 2, 3, 4, 7, 8, 9, 15, 16, 17, 33, 48, 63]
 
