@@ -32,6 +32,7 @@
 // groups.  Q6_K blocks at 2 (mod 4) bytes are read as aligned dword pairs and
 // funnel-shifted; the parity of every block in a slice is a compile-time
 // constant because slices hold a multiple of 8 blocks.
+#include <atomic>
 #include <type_traits>
 
 #include "iq_lanes.h"
@@ -578,6 +579,29 @@ const void* kfn() {
     if constexpr (RPW == 4) return (const void*)k_gemv4<FMT, NBUF>;
     else return (const void*)k_gemv<FMT, MT>;
 }
+// Workgroups per CU the kernel's registers allow at `lds` bytes of LDS,
+// queried once per LDS size (0: unknown).
+template <int FMT, int MT, int RPW, int NBUF>
+int occupancy(size_t lds) {
+    static std::atomic<long long> cache[8];  // (lds << 8) | blocks; 0 = empty
+    for (auto& c : cache) {
+        const long long v = c.load(std::memory_order_relaxed);
+        if (v == 0) break;
+        if ((size_t)(v >> 8) == lds) return (int)(v & 0xff);
+    }
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn<FMT, MT, RPW, NBUF>(), 256, lds) != hipSuccess) {
+        (void)hipGetLastError();  // clear this query's own error
+        return 0;
+    }
+    const long long v = ((long long)lds << 8) | (occ & 0xff);
+    for (auto& c : cache) {
+        long long z = 0;
+        if (c.compare_exchange_strong(z, v) || z == v) break;
+    }
+    return occ;
+}
+
 template <int FMT, int MT, int RPW = 8, int NBUF = 2>
 hipError_t launch_t(GemvArgs args, hipStream_t s) {
     using G = GvGeom<FMT, RPW>;
@@ -595,11 +619,8 @@ hipError_t launch_t(GemvArgs args, hipStream_t s) {
         }
     }
     int per_cu = (int)(L.lds_cu / lds);
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn<FMT, MT, RPW, NBUF>(), 256, lds) == hipSuccess &&
-        occ > 0 && occ < per_cu)
-        per_cu = occ;
-    (void)hipGetLastError();
+    const int occ = occupancy<FMT, MT, RPW, NBUF>(lds);
+    if (occ > 0 && occ < per_cu) per_cu = occ;
     const int64_t wgs = ((int64_t)args.groups + 3) / 4;
     const int64_t cap = (int64_t)L.cus * (per_cu < 1 ? 1 : per_cu);
     dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)((args.m + MT - 1) / MT));
