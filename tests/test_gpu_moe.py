@@ -71,8 +71,10 @@ def qwen_layer():
     return S.random_moe_layer(2048, 512, 256, Q4, Q6, rng, shared=True)
 
 
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 11, 12])
 def test_qwen_shaped_moe_matches_oracle(gpu, oracle, qwen_layer, m):
+    """Token-major widths: the one-token kernel (1), the 16-row gate/up
+    workgroups with their own top-k (2..11) and after a routing launch (12)."""
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     rng = np.random.default_rng(7 + m)
     x = S.normal((m, 2048), rng)
@@ -176,10 +178,10 @@ def test_routed_only_layer_matches_oracle(gpu, oracle, qwen_layer_routed_only, t
         assert_bitexact(got, singles, f"routed-only grouped vs per-token m={m}")
 
 
-@pytest.mark.parametrize("m", [24, 64])
+@pytest.mark.parametrize("m", [3, 12, 24, 64])
 def test_skewed_grouped_call_equals_single_token_calls(gpu, qwen_layer, m):
-    """m rows with skewed routing in one call (token-major at 24, grouped by
-    expert at 64) equal m one-row calls."""
+    """m rows with skewed routing in one call (token-major at 3, 12 and 24,
+    grouped by expert at 64) equal m one-row calls."""
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     rng = np.random.default_rng(98)
     x = torch.from_numpy(S.normal((m, 2048), rng)).to(gpu)
