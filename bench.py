@@ -363,19 +363,7 @@ def secondary(args, hip, stream, device, layers):
     extra["lm_head_q6k_m8"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1)}
     del lm
     # config 3: verify pass MoE at M = 4 and 8 (independent routing per row)
-    n = len(layers)
-    g = torch.Generator(device=device)
-    g.manual_seed(77)
-    for m in (4, 8):
-        xs = torch.randn(64, m, H, device=device, generator=g)
-        lg = torch.randn(64, m, E, device=device, generator=g)
-        out = torch.empty(m, H, device=device)
-        ms = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 64], lg[i % 64], out), 40, hip)
-        uniq = float(np.mean([len(torch.unique(torch.topk(lg[j], TOPK, dim=1).indices)) for j in range(64)]))
-        kb = moe_kernel_bytes(m, uniq)
-        tot = kb["gate_up"] + kb["down"] + kb["prep"]
-        extra[f"moe_layer_m{m}"] = {"us": round(ms * 1e3, 2), "unique_experts": round(uniq, 1),
-                                    "GB_s": round(tot / ms / 1e6, 1), "frac_hbm": round(tot / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    extra.update(moe_tokens(hip, device, layers, (4, 8)))
     # configs 2/3: dense projections beside the MoE (attention q/gate, k, v, o),
     # one call each per step, rotated over copies beyond the MALL
     shapes = (("q_gate", 8192, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 4096))
@@ -398,6 +386,29 @@ def secondary(args, hip, stream, device, layers):
                                             "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
     del proj
     return extra
+
+
+def moe_tokens(hip, device, layers, widths):
+    """the MoE layer at M tokens per call (verify
+    widths), each row routed independently, graph replay over the resident
+    layers; bytes counted over the distinct experts a call reads."""
+    import torch
+
+    n = len(layers)
+    g = torch.Generator(device=device)
+    g.manual_seed(77)
+    res = {}
+    for m in widths:
+        xs = torch.randn(64, m, H, device=device, generator=g)
+        lg = torch.randn(64, m, E, device=device, generator=g)
+        out = torch.empty(m, H, device=device)
+        ms = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 64], lg[i % 64], out), 40, hip)
+        uniq = float(np.mean([len(torch.unique(torch.topk(lg[j], TOPK, dim=1).indices)) for j in range(64)]))
+        kb = moe_kernel_bytes(m, uniq)
+        tot = kb["gate_up"] + kb["down"] + kb["prep"]
+        res[f"moe_layer_m{m}"] = {"us": round(ms * 1e3, 2), "unique_experts": round(uniq, 1),
+                                  "GB_s": round(tot / ms / 1e6, 1), "frac_hbm": round(tot / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    return res
 
 
 def prefill(args, hip, stream, device):
@@ -563,7 +574,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--no-parity", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "moe_prefill", "lm_head", "decode_sweep"), default=None,
+    ap.add_argument("--only", choices=("prefill", "moe_prefill", "moe_tokens", "lm_head", "decode_sweep"), default=None,
                     help="run one secondary config alone (for profiling) and print its JSON")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC byte-counter calibration)")
@@ -616,6 +627,9 @@ def main():
         return
     if args.only == "decode_sweep":
         print(json.dumps({"only": args.only, "result": decode_sweep(args, hip, device, layers)}), flush=True)
+        return
+    if args.only == "moe_tokens":
+        print(json.dumps({"only": args.only, "result": moe_tokens(hip, device, layers, (1, 4, 8))}), flush=True)
         return
 
     eager_ms, eager_per = time_moe(layers, xs, logits, out, args.steps, args.warmup, hip, stream)
