@@ -287,6 +287,10 @@ constexpr int kMoeRouteLaunchMin = 12;  // calls this wide route in a launch of 
 // 1, 2 and 4 measure 45.3 / 44.1 / 44.9 us at 8 tokens, 17.2 / 17.0 / 17.9
 // at 2 and 118 / 111 / 109 at 28
 constexpr int kMoe1RowGroups = 2;
+// calls this wide quantise their SwiGLU rows in a launch of their own: 16
+// tokens 71.8 -> 71.0 us, 28 tokens 113 -> 106.7 us; at 8 tokens the extra
+// launch costs 2 us more than the repeated quantisation
+constexpr int kMoe1ActqMin = 16;
 
 // Routing workgroup of token t's gate/up slice: wave 0 routes the token
 // (top-k, exact softmax weights), wave 1 computes the shared-expert gate.
@@ -520,7 +524,22 @@ __global__ __launch_bounds__(128) void k_moe1_route(MoeParams p) { moe1_route(p,
 // row into LDS while the weights fly, and forms the row products; the 8
 // rows are then combined in route order (multiply, then add) plus
 // shared * gate.
-template <int DFMT, int NG>
+// One wave per (token-major act row, 256-value block): Q8K for the down
+// waves of wide calls (quant_q8k_wave: the bytes, scale and 32-value sums of
+// from_float, as the down waves would form them).
+__global__ __launch_bounds__(256) void k_moe1_actq(MoeParams p, int P) {
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nb = p.aq.ng;
+    if (wid >= (int64_t)P * nb) return;  // uniform per wave
+    const int64_t row = wid / nb;
+    const int b = (int)(wid - row * nb);
+    quant_q8k_wave(p.act + row * p.I + (int64_t)b * 256, row, b, p.aq, nullptr);
+}
+
+// QA: the SwiGLU rows come quantised (k_moe1_actq); otherwise each wave
+// quantises its slot's row into LDS, which every workgroup of the token
+// repeats -- cheaper than a launch of its own below kMoe1ActqMin tokens.
+template <int DFMT, int NG, bool QA = false>
 __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
     constexpr int VPL = NG * 4;  // SwiGLU values per lane (I = NG * 256)
     static_assert(VPL == 8 || VPL == 16 || VPL == 32, "shape");
@@ -536,7 +555,7 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
     constexpr int LPB = 256 / VPL;
     const int gq = lane / LPB;
     float av[VPL];
-    q8k_vpl_load<VPL>(p.act + ((int64_t)t * nslots + wave) * p.I + (int64_t)gq * 256, av);
+    if constexpr (!QA) q8k_vpl_load<VPL>(p.act + ((int64_t)t * nslots + wave) * p.I + (int64_t)gq * 256, av);
     const int e = wave < K ? __builtin_amdgcn_readfirstlane(p.experts[t * K + wave]) : 0;
     const int64_t n = (int64_t)blockIdx.x * 8 + slot;
     const bool ok = n < p.H;
@@ -546,19 +565,25 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
     typename WT<DFMT>::T w[1][NG];
     lanes_load_exact<DFMT, 1, NG>(wrow, k, w);
     ActView a;
-    a.ng = NG;
-    a.ldq = NG * 256;
-    a.ldd = NG * 8;
-    a.m = nslots;
-    a.q = s_q;
-    a.d = s_d;
-    a.s8 = s_s8;
-    quant_q8k_vpl<VPL>(av, true, wave, gq, a);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int64_t ar0 = wave;
+    if constexpr (QA) {
+        a = p.aq;
+        ar0 = (int64_t)t * nslots + wave;
+    } else {
+        a.ng = NG;
+        a.ldq = NG * 256;
+        a.ldd = NG * 8;
+        a.m = nslots;
+        a.q = s_q;
+        a.d = s_d;
+        a.s8 = s_s8;
+        quant_q8k_vpl<VPL>(av, true, wave, gq, a);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
     float acc[1][1] = {{0.f}}, accm[1][1] = {{0.f}};
-    const int64_t arow[1][1] = {{wave}};
+    const int64_t arow[1][1] = {{ar0}};
     const int mc[1] = {1};
     lanes_accumulate<DFMT, 1, 1, NG>(w, wrow, 0, NG, p.d_nbw, a, arow, mc, k, acc, accm);
     float o[1][1];
@@ -607,7 +632,14 @@ hipError_t launch_moe1_stage(const MoeParams& p, int stage, hipStream_t s) {
                                s, p);
         }
     } else if (stage == 2) {
-        hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), m), dim3(64 * nslots), 0, s, p);
+        if (p.M >= kMoe1ActqMin) {
+            const int P = p.M * nslots;
+            const int64_t aw = (int64_t)P * p.aq.ng;
+            hipLaunchKernelGGL(k_moe1_actq, dim3((unsigned)((aw + 3) / 4)), dim3(256), 0, s, p, P);
+            hipLaunchKernelGGL((k_moe1_down<DFMT, 2, true>), dim3((unsigned)(p.H / 8), m), dim3(64 * nslots), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((k_moe1_down<DFMT, 2>), dim3((unsigned)(p.H / 8), m), dim3(64 * nslots), 0, s, p);
+        }
     } else {
         return hipErrorInvalidValue;
     }
