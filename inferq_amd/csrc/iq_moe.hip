@@ -278,10 +278,10 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeParams p) {
 // pass and have far less weight traffic in flight per CU.
 
 constexpr int kMoe1MaxSlots = 12;  // top-k routes plus the shared expert
-// widest call served token-major: since the grouped MFMA path took 16-row
-// chunks it is faster from about 32 tokens (32: 125 against 137 us, 48: 148
-// against 195 us in graph replays; 24: 105-108 either way)
-constexpr int kMoeTokenMajorMax = 28;
+// widest call served token-major (graph replays, grouped against
+// token-major: 32 tokens 121.4 against 118.9 us, 36: 127.9 against 130.7,
+// 48: 142.8 against 165.6)
+constexpr int kMoeTokenMajorMax = 32;
 constexpr int kMoeRouteLaunchMin = 12;  // calls this wide route in a launch of their own
 // 8-row groups of gate (and of up) per workgroup of the multi-token form:
 // 1, 2 and 4 measure 45.3 / 44.1 / 44.9 us at 8 tokens, 17.2 / 17.0 / 17.9

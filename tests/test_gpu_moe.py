@@ -104,7 +104,7 @@ def format_layers():
 @pytest.mark.parametrize("fmts", _FORMAT_PAIRS, ids=lambda f: f"{_NAMES[f[0]]}-{_NAMES[f[1]]}")
 def test_format_pairs_match_oracle(gpu, oracle, format_layers, fmts, m):
     """Every gate/down format pair at one row, a verify width and a prefill
-    width (K-quant pairs take the token-major kernels up to 28 rows and the
+    width (K-quant pairs take the token-major kernels up to 32 rows and the
     grouped MFMA kernels past that; Q8_0 the generic grouped path); a
     multi-row call equals one-row calls, bitwise."""
     layer = format_layers[fmts]
@@ -132,11 +132,11 @@ def _dirichlet_logits(m, n_experts, rng, alpha=0.3):
     return (S.normal((m, n_experts), rng) + np.log(np.maximum(p, 1e-30))).astype(np.float32)
 
 
-@pytest.mark.parametrize("m", [17, 28, 29, 48, 256])
+@pytest.mark.parametrize("m", [17, 28, 32, 33, 48, 256])
 def test_prefill_width_moe_matches_oracle(gpu, oracle, qwen_layer, m):
     """Wide calls with skewed routing (large groups on a few experts, most
-    experts idle): token-major calls (17, and 28, the widest), the narrowest
-    grouped MFMA call (29), 48 and the prefill width of 256."""
+    experts idle): token-major calls (17, 28, and 32, the widest), the
+    narrowest grouped MFMA call (33), 48 and the prefill width of 256."""
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     rng = np.random.default_rng(300 + m)
     x = S.normal((m, 2048), rng)
