@@ -410,3 +410,32 @@ def test_mixed_format_graph_replays_match_eager_calls(gpu, m):
             moe.forward_into(xs[(i + 1) % 3], ls[(i + 1) % 3], o)
             torch.cuda.synchronize()
             assert_bitexact(o.cpu().numpy(), eager[(i + 1) % 3], "eager between replays")
+
+
+@pytest.fixture(scope="module")
+def wide_router_layer():
+    """512 experts, top-10 plus the shared expert (eleven slots; the
+    Qwen3-Next routing shape at hidden 2048, intermediate 512)."""
+    return S.random_moe_layer(2048, 512, 512, Q4, Q6, np.random.default_rng(2026), shared=True)
+
+
+@pytest.mark.parametrize("m", [1, 5, 12, 32, 40])
+def test_512_experts_top10_matches_oracle(gpu, oracle, wide_router_layer, m):
+    """Eleven slots per token through every token-major form (1, 5, 12 and
+    32 tokens) and the grouped MFMA path (40): routes equal the oracle's,
+    outputs within 1e-4, and the call equals one call per token bitwise."""
+    moe, _ = _device_layer(wide_router_layer, 10, gpu)
+    rng = np.random.default_rng(3100 + m)
+    x = S.normal((m, 2048), rng)
+    logits = S.normal((m, 512), rng)
+    xg, lg = torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu)
+    out = moe.forward(xg, lg)
+    ref, ref_e, ref_w = oracle.moe_forward(_oracle_layer(wide_router_layer, 10), x, logits, mode=1,
+                                           impl=_impl(oracle), nthreads=8)
+    assert [r.experts for r in out.routes] == ref_e.tolist()
+    assert_close_normwise(np.array([r.weights for r in out.routes]), ref_w, 1e-6, "route weights")
+    got = out.hidden.cpu().numpy()
+    assert_close_normwise(got, ref, 1e-4, f"512-expert top-10 MoE m={m}")
+    if m > 1:
+        singles = np.concatenate([moe.forward(xg[i:i + 1], lg[i:i + 1]).hidden.cpu().numpy() for i in range(m)])
+        assert_bitexact(got, singles, f"512-expert top-10 m={m} vs per-token")
