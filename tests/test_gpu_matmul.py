@@ -231,3 +231,25 @@ def test_call_time_errors(gpu):
     other = Q.QuantizedMatrix.upload(np.zeros(34 * 8, np.uint8), Q8, 1, 256)
     with pytest.raises(Q.QgemmError, match="cannot concatenate quantized matrices with dtypes"):
         mat.concatenate_rows(other)
+
+
+def test_random_shapes_bitexact(gpu, oracle):
+    """A seeded sweep of shapes the named tests do not pin -- every format,
+    widths from one block to 24, row counts from 1 to about 20000 and input
+    rows from 1 to 70, whichever kernel the dispatch picks -- each output
+    bitwise the oracle's."""
+    rng = np.random.default_rng(4242)
+    impl = 1 if oracle.have_avx2() else 0
+    fmts = (Q4, S.Q5_K, Q6, Q8)
+    for case in range(64):
+        dtype = fmts[case % 4]
+        nb = int(rng.choice([1, 2, 3, 4, 8, 12, 16, 24]))
+        cols = 256 * nb
+        rows = int(rng.choice([int(rng.integers(1, 40)), int(rng.integers(40, 3000)), int(rng.integers(3000, 20000))]))
+        m = int(rng.choice([1, 2, int(rng.integers(3, 9)), int(rng.integers(9, 64)), int(rng.integers(64, 71))]))
+        w = S.random_matrix(dtype, rows, cols, rng)
+        x = S.normal((m, cols), rng)
+        mat = Q.QuantizedMatrix.upload(w, dtype, rows, cols)
+        got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+        expected = oracle.matmul(dtype, w, rows, cols, x, impl=impl, nthreads=8)
+        assert_bitexact(got, expected, f"case {case}: {S.NAMES[dtype]} [{rows}x{cols}] m={m}")
