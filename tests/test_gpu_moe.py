@@ -439,3 +439,25 @@ def test_512_experts_top10_matches_oracle(gpu, oracle, wide_router_layer, m):
     if m > 1:
         singles = np.concatenate([moe.forward(xg[i:i + 1], lg[i:i + 1]).hidden.cpu().numpy() for i in range(m)])
         assert_bitexact(got, singles, f"512-expert top-10 m={m} vs per-token")
+
+
+def test_random_layers_match_oracle(gpu, oracle):
+    """A seeded sweep over the token-major and grouped paths: expert counts
+    16-96, top-k 1-10, with or without the shared expert, Q4_K or Q6_K
+    experts, 1-40 tokens.  Routes equal the oracle's, outputs within 1e-4."""
+    rng = np.random.default_rng(777)
+    for case in range(12):
+        E = int(rng.choice([16, 40, 96]))
+        K = int(rng.integers(1, 11))
+        shared = bool(rng.integers(0, 2))
+        g, d = [(Q4, Q6), (Q4, Q4), (Q6, Q6), (Q6, Q4)][case % 4]
+        m = int(rng.choice([1, int(rng.integers(2, 9)), int(rng.integers(9, 33)), int(rng.integers(33, 41))]))
+        layer = S.random_moe_layer(2048, 512, E, g, d, rng, shared=shared)
+        moe, _ = _device_layer(layer, K, gpu)
+        x = S.normal((m, 2048), rng)
+        logits = S.normal((m, E), rng)
+        out = moe.forward(torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu))
+        ref, ref_e, _ = oracle.moe_forward(_oracle_layer(layer, K), x, logits, mode=1, impl=_impl(oracle), nthreads=8)
+        what = f"case {case}: E={E} K={K} shared={shared} {_NAMES[g]}/{_NAMES[d]} m={m}"
+        assert [r.experts for r in out.routes] == ref_e.tolist(), what
+        assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, what)
