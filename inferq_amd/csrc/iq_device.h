@@ -92,6 +92,20 @@ __device__ __forceinline__ float xor_lane(float v) {
     return __builtin_bit_cast(float, r);
 }
 
+// Maximum of v over the 64 lanes, in every lane: two lane-half swaps
+// (v_permlane32_swap, v_permlane16_swap) and four DPP steps inside rows.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = max(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(b[0], b[1]);
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));  // row half mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));  // row mirror
+    return v;
+}
+
 // hsum_f32_8 over the 8 lanes of a group: ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)).
 // Every lane of the group ends with the same value.
 __device__ __forceinline__ float hsum8(float v) {

@@ -39,34 +39,27 @@ struct Q8KLane {
     int bsum16, sum32;
 };
 __device__ __forceinline__ Q8KLane quant_q8k_core(const f32x4 v) {
-    const int lane = threadIdx.x & 63;
     // amax and the first index reaching it (the reference updates only on a
-    // strictly larger |x| while scanning upwards)
-    float am = 0.f;
-    int idx = 1 << 20;
+    // strictly larger |x| while scanning upwards): the lane's first largest
+    // |x| (never NaN, never negative, so its bits order like the values),
+    // the wave maximum of those, and the lowest lane holding it, whose
+    // values come first in the block.
+    float am = 0.f, mine = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const float ax = fabsf(v[e]);
         if (am < ax) {
             am = ax;
-            idx = 4 * lane + e;
+            mine = v[e];
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float am2 = __shfl_xor(am, off);
-        const int idx2 = __shfl_xor(idx, off);
-        if (am2 > am || (am2 == am && idx2 < idx)) {
-            am = am2;
-            idx = idx2;
-        }
-    }
+    const uint32_t amb = __builtin_bit_cast(uint32_t, am);
+    const uint32_t top = wave_max_u32(amb);
     int q[4] = {0, 0, 0, 0};
     float dval = 0.f;
-    if (am != 0.f) {  // uniform
-        const int e = idx & 3;
-        const float mine = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
-        const float maxv = __shfl(mine, idx >> 2);
+    if (top != 0u) {  // uniform
+        const int first = (int)__builtin_ctzll(__ballot(amb == top));
+        const float maxv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first));
         const float iscale = __fdiv_rn(-128.f, maxv);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -78,10 +71,10 @@ __device__ __forceinline__ Q8KLane quant_q8k_core(const f32x4 v) {
     Q8KLane r;
     r.packed = pack4(q[0], q[1], q[2], q[3]);
     int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    s += __builtin_amdgcn_mov_dpp(s, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+    s += __builtin_amdgcn_mov_dpp(s, 0x4E, 0xF, 0xF, false);  // lane ^ 2
     r.bsum16 = s;
-    s += __shfl_xor(s, 4);
+    s += __builtin_amdgcn_ds_swizzle(s, 0x101F);  // lane ^ 4
     r.sum32 = s;
     r.d = dval;
     return r;

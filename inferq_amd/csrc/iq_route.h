@@ -32,20 +32,6 @@ __device__ __forceinline__ uint32_t route_ukey(float x) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Maximum of v over the 64 lanes, in every lane: two lane-half swaps
-// (v_permlane32_swap, v_permlane16_swap) and four DPP steps inside rows.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    v = max(a[0], a[1]);
-    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    v = max(b[0], b[1]);
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));  // row half mirror
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));  // row mirror
-    return v;
-}
-
 // The lane's logits (-inf past E), 16-byte loads when E is 256 or 512 and
 // the row is aligned.
 __device__ __forceinline__ void route_load(const float* lg, int E, float (&lv)[kRoutePer]) {
