@@ -15,8 +15,10 @@
 // (18 KiB), the bsums and the block scales in LDS, double buffered, the next
 // block's loads in flight while the current one is multiplied.  Each wave
 // dequantises its B fragments in registers (nibbles, then one packed 16-bit
-// multiply per dword and stream).  Narrow outputs are split over K, with
-// partial tiles summed in a fixed order by a second pass.
+// multiply per dword and stream).  Calls too small to fill the GPU with
+// such tiles take 32 x 64 tiles (4 waves, two row tiles each) and, only if
+// those are still too few, a split over K, with partial tiles summed in a
+// fixed order by a second pass.
 #include "iq_lanes.h"
 #include "iq_pf_q4k.h"
 #include "iq_quant.h"
@@ -29,9 +31,16 @@ namespace {
 // Tile shape: ROWS input rows x COLS output columns per workgroup, one
 // wave per 16 columns, each wave all ROWS rows (RT = ROWS / 16 row tiles
 // share every decoded B fragment).  64 x 128 on 8 waves (two per SIMD)
-// measured fastest: 128 x 64 on 4 waves, 128 x 128 on 8 waves with split K,
-// and a smaller stage with two workgroups per CU were all slower.
-constexpr int kPfRows = 64, kPfCols = 128;
+// measured fastest where 256 such tiles fill the GPU ([256 x 2048] ->
+// 8192: kernel 16.5-17.0 us): 128 x 64 on 4 waves, 128 x 128 on 8 waves
+// with split K, 64 x 64 on 4 waves at two workgroups per CU (17.0-18.4 us)
+// and 32 x 64 (20.9 us) were all slower.  Fewer tiles than that take 32 x 64
+// on 4 waves, which fill the GPU without the split over K and its reduce
+// launch: [256 x 4096] -> 2048 per call 24.1-32.6 us as 64 x 128 tiles in
+// four K splits, 22.7 us as 256 unsplit 32 x 64 tiles.
+constexpr int kPfRows = 64, kPfCols = 128;      // large calls
+constexpr int kPfRowsS = 32, kPfColsS = 64;     // calls with fewer than 256 large tiles
+constexpr int kPfMinTiles = 256;
 
 // ---- activation quantisation --------------------------------------------------
 // Q8K (bit-exact from_float) into the layouts the MFMA kernel reads:
@@ -226,12 +235,13 @@ struct PfPlan {
 PfPlan plan(const WeightView& w, int64_t m) {
     PfPlan P;
     P.nb = (int)(w.cols / 256);
-    P.rows = kPfRows;
-    P.cols = kPfCols;
+    const int64_t large = (w.rows + kPfCols - 1) / kPfCols * ((m + kPfRows - 1) / kPfRows);
+    P.rows = large >= kPfMinTiles ? kPfRows : kPfRowsS;
+    P.cols = large >= kPfMinTiles ? kPfCols : kPfColsS;
     P.mp = (int)((m + P.rows - 1) / P.rows * P.rows);
     const int64_t tiles = ((w.rows + P.cols - 1) / P.cols) * (P.mp / P.rows);  // real tiles (padding aside)
     int splits = 1;
-    while (tiles * splits < 256 && splits * 2 <= P.nb && splits < 8) splits *= 2;
+    while (tiles * splits < kPfMinTiles && splits * 2 <= P.nb && splits < 8) splits *= 2;
     P.bps = (P.nb + splits - 1) / splits;
     P.splits = (P.nb + P.bps - 1) / P.bps;
     P.q_bytes = align256((size_t)P.mp * P.nb * 256);
@@ -278,9 +288,15 @@ hipError_t launch_prefill(const WeightView& w, const float* x, int64_t ldx, int6
     if (e != hipSuccess) return e;
     const int64_t ntiles = (w.rows + P.cols - 1) / P.cols;
     dim3 grid((unsigned)((ntiles + 7) / 8 * 8 * (P.mp / P.rows)), 1, (unsigned)P.splits);
-    constexpr int TH = PfTile<kPfRows, kPfCols>::kThreads;
-    if (dbg_isum) hipLaunchKernelGGL((k_prefill_q4k<kPfRows, kPfCols, true>), grid, dim3(TH), 0, s, a);
-    else hipLaunchKernelGGL((k_prefill_q4k<kPfRows, kPfCols, false>), grid, dim3(TH), 0, s, a);
+    if (P.rows == kPfRows) {
+        constexpr int TH = PfTile<kPfRows, kPfCols>::kThreads;
+        if (dbg_isum) hipLaunchKernelGGL((k_prefill_q4k<kPfRows, kPfCols, true>), grid, dim3(TH), 0, s, a);
+        else hipLaunchKernelGGL((k_prefill_q4k<kPfRows, kPfCols, false>), grid, dim3(TH), 0, s, a);
+    } else {
+        constexpr int TH = PfTile<kPfRowsS, kPfColsS>::kThreads;
+        if (dbg_isum) hipLaunchKernelGGL((k_prefill_q4k<kPfRowsS, kPfColsS, true>), grid, dim3(TH), 0, s, a);
+        else hipLaunchKernelGGL((k_prefill_q4k<kPfRowsS, kPfColsS, false>), grid, dim3(TH), 0, s, a);
+    }
     e = hipGetLastError();
     if (e != hipSuccess || P.splits == 1) return e;
     const int64_t tot = m * w.rows;

@@ -27,31 +27,38 @@ def _rowwise_close(got, ref, tol, what):
         assert_close_normwise(got[r], ref[r], tol, f"{what} row {r}")
 
 
-def test_prefill_block_integers_exact(gpu, oracle):
-    """Ragged rows (70, not a multiple of 16) and columns (40, not a
-    multiple of 32): every (row, column, block) integer pair equals the
-    oracle's textbook integers."""
-    rng = np.random.default_rng(61)
-    rows, cols, m = 40, 512, 70
+@pytest.mark.parametrize("rows,cols,m,sample", [(40, 512, 70, None), (8192, 512, 256, 4000)])
+def test_prefill_block_integers_exact(gpu, oracle, rows, cols, m, sample):
+    """Every (row, column, block) integer pair of a ragged call on the
+    small 32 x 64 tiles (70 rows, not a multiple of 16; 40 columns, not a
+    multiple of 32), and a seeded sample of the pairs of a call that fills
+    the GPU with the large 64 x 128 tiles, equal the oracle's textbook
+    integers."""
+    rng = np.random.default_rng(61 + rows)
     w = S.random_matrix(Q4, rows, cols, rng)
     x = S.normal((m, cols), rng)
     mat = Q.QuantizedMatrix.upload(w, Q4, rows, cols)
     y, isum, msum = mat.prefill_block_sums(torch.from_numpy(x).to(gpu))
     isum, msum = isum.cpu().numpy(), msum.cpu().numpy()
     wb = w.view(oracle.BLOCK[Q4]).reshape(rows, cols // 256)
-    for t in range(m):
-        q = oracle.quantize_q8k(x[t])
-        for n in range(rows):
-            for b in range(cols // 256):
-                ti, tm = oracle.block_textbook(Q4, wb[n, b], q[b])
-                assert isum[t, n, b] == ti and msum[t, n, b] == tm, (t, n, b)
-    _rowwise_close(y.cpu().numpy(), oracle.matmul(Q4, w, rows, cols, x), 1e-4, "prefill product")
+    if sample is None:
+        picks = [(t, n, b) for t in range(m) for n in range(rows) for b in range(cols // 256)]
+    else:
+        picks = list(zip(rng.integers(0, m, sample), rng.integers(0, rows, sample), rng.integers(0, cols // 256, sample)))
+    qs = {}
+    for t, n, b in picks:
+        if t not in qs:
+            qs[t] = oracle.quantize_q8k(x[t])
+        ti, tm = oracle.block_textbook(Q4, wb[n, b], qs[t][b])
+        assert isum[t, n, b] == ti and msum[t, n, b] == tm, (t, n, b)
+    _rowwise_close(y.cpu().numpy(), oracle.matmul(Q4, w, rows, cols, x, nthreads=8), 1e-4, "prefill product")
 
 
 @pytest.mark.parametrize("rows,cols,m", [(1024, 2048, 256), (2048, 4096, 256), (300, 2048, 100), (64, 256, 64)])
 def test_prefill_matches_oracle(gpu, oracle, rows, cols, m):
     """BASELINE configs[3] shapes scaled to what the oracle computes in
-    seconds, a split-K shape (narrow output, wide input), ragged sizes."""
+    seconds ([2048 x 4096] at 256 rows: 256 unsplit small tiles; [1024 x
+    2048]: small tiles split over K), ragged sizes."""
     rng = np.random.default_rng(rows + cols + m)
     w = S.random_matrix(Q4, rows, cols, rng)
     x = S.normal((m, cols), rng)
