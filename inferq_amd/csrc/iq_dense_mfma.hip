@@ -229,8 +229,13 @@ bool dm_layout_ok(const WeightView& w) {
 //    needs (src/gguf.rs:493-520 tiles prefill rows under the same guarantee).
 // Smaller or narrower matrices keep the GEMV, whose latency is lower there
 // (a [512 x 2048] matrix: 4.1 against 7.9 us at 8 rows).
+// The tiles address activation rows with 32-bit byte offsets (MlOperands).
+static bool dm_rows_ok(const WeightView& w, int64_t m) {
+    return m >= 1 && m <= (int64_t)1 << 20 && (uint64_t)m * (uint64_t)w.cols <= 0xffffffffull;
+}
+
 bool dense_mfma_supported(const WeightView& w, int64_t m) {
-    if (m < 2 || !dm_layout_ok(w)) return false;
+    if (m < 2 || !dm_layout_ok(w) || !dm_rows_ok(w, m)) return false;
     if (m >= kPrefillMinRows) return true;
     const int64_t bytes = w.rows * w.row_bytes, MiB = (int64_t)1 << 20;
     if (bytes >= 64 * MiB) return true;
@@ -239,7 +244,7 @@ bool dense_mfma_supported(const WeightView& w, int64_t m) {
 }
 
 size_t dense_mfma_workspace_any(const WeightView& w, int64_t m) {
-    return m >= 1 && dm_layout_ok(w) ? dm_plan(w, m).total() : 0;
+    return dm_layout_ok(w) && dm_rows_ok(w, m) ? dm_plan(w, m).total() : 0;
 }
 
 hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
@@ -253,7 +258,7 @@ hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, i
 
 hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                                  void* ws, hipStream_t s) {
-    if (m < 1 || !dm_layout_ok(w) || m > (int64_t)1 << 20) return hipErrorNotSupported;
+    if (!dm_layout_ok(w) || !dm_rows_ok(w, m)) return hipErrorNotSupported;
     const DmPlan P = dm_plan(w, m);
     uint8_t* base = (uint8_t*)ws;
     DmArgs a;
