@@ -40,6 +40,16 @@ FLAGS = [
 ]
 
 
+# Per-source additions.  The token-major MoE kernels (iq_moe.hip) are
+# chains of dependent loads; the scheduler that keeps memory clauses
+# together measured MoE M=4 26.9 -> 25.2 us, M=8 44.3 -> 43.2 us and the
+# one-token gate/up launch 7.28 -> 7.17 us, bitwise the same results (the
+# other sources were neutral or slower with it).
+SOURCE_FLAGS = {
+    "iq_moe.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
+}
+
+
 def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
 
@@ -47,7 +57,7 @@ def sources() -> list[str]:
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
     lang = ["-x", "hip"]
-    cmd = [HIPCC, *lang, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *lang, *FLAGS, *SOURCE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
