@@ -413,9 +413,9 @@ def moe_tokens(hip, device, layers, widths):
 
 def prefill(args, hip, stream, device):
     """BASELINE configs[3], dense part: Q4_K [256 x 2048] -> 8192 and
-    [256 x 4096] -> 2048 (and Q6_K [256 x 2048] -> 8192) on int8 MFMA (activation quantisation, MFMA kernel
-    and, for the narrow output, the split-K reduction all inside the timed
-    call), on both MFMA paths: the dispatch's exact lane order (bitwise the
+    [256 x 4096] -> 2048 (and Q6_K [256 x 2048] -> 8192) on int8 MFMA (activation quantisation and the MFMA
+    kernel, and any split-K reduction, all inside the timed call), on both
+    MFMA paths: the dispatch's exact lane order (bitwise the
     reference) and the prefill tiles a caller requests explicitly (tile
     order, within 1e-4).  TOPS = 2 M N K / time; peak = 5.0 POPS dense
     int8."""
