@@ -11,30 +11,34 @@ constexpr int kMoeMaxAssign = 4096;   // tokens * top_k per call
 constexpr int kMoePrefillMinTokens = 17;  // the MFMA path serves calls of this many tokens or more
 
 struct MoeParams {
-    // layer (device pointers, GGUF native layout)
+    // The fields the one-token kernels read first share the first three
+    // 64-byte lines of the kernel arguments, so that one scalar-cache fill
+    // brings them in (a kernel argument on a line of its own costs its
+    // kernel a dependent memory round trip before the loads that need it).
     int64_t H = 0, I = 0, E = 0, K = 0;
-    int normalize = 1;
+    int32_t* experts = nullptr;     // [M][K] (workspace)
+    float* act = nullptr;           // [P][I] SwiGLU output (workspace)
+    const float* x = nullptr;       // [M][H]
+    const float* logits = nullptr;  // [M][E] (given, or computed from router into logits_ws)
+    // layer (device pointers, GGUF native layout)
     const uint8_t* gate = nullptr;  // [E][I][H]
     const uint8_t* up = nullptr;    // [E][I][H]
     const uint8_t* down = nullptr;  // [E][H][I]
     const uint8_t* sgate_w = nullptr;  // shared expert [I][H], or null
     const uint8_t* sup_w = nullptr;    // [I][H]
     const uint8_t* sdown_w = nullptr;  // [H][I]
-    const float* selector = nullptr;   // [H]
     int64_t g_row_bytes = 0, d_row_bytes = 0, g_exp_bytes = 0, d_exp_bytes = 0;
     int g_nbw = 0, d_nbw = 0;  // weight blocks per row of gate/up and of down
-    const float* router = nullptr;  // f32 [E][H] (blk.N.ffn_gate_inp.weight), or null
-    // call
-    const float* x = nullptr;       // [M][H]
-    const float* logits = nullptr;  // [M][E] (given, or computed from router into logits_ws)
-    float* logits_ws = nullptr;     // [M][E] workspace for the router's logits
+    float* weights = nullptr;  // [M][K] (workspace)
+    float* sgate = nullptr;    // [M] sigmoid(x . selector) (workspace)
     const float* residual = nullptr;  // [M][H] added to the output, or null
+    float* out = nullptr;             // [M][H]
     int M = 0;
-    float* out = nullptr;  // [M][H]
+    int normalize = 1;
+    const float* selector = nullptr;  // [H]
+    const float* router = nullptr;  // f32 [E][H] (blk.N.ffn_gate_inp.weight), or null
+    float* logits_ws = nullptr;     // [M][E] workspace for the router's logits
     // workspace
-    int32_t* experts = nullptr;  // [M][K]
-    float* weights = nullptr;    // [M][K]
-    float* sgate = nullptr;      // [M] sigmoid(x . selector)
     int32_t* meta = nullptr;     // [0] number of groups
     int32_t* group_expert = nullptr;
     int32_t* group_start = nullptr;
@@ -43,7 +47,6 @@ struct MoeParams {
     int32_t* slot_pos = nullptr;    // [M][K] grouped position of (token, route)
     int32_t* counters = nullptr;    // [M*K+1][ceil(I/256)], zero between calls
     ActView xq;                     // x quantised, M rows of width H
-    float* act = nullptr;           // [P][I] SwiGLU output
     ActView aq;                     // act quantised, P rows of width I
     float* vals = nullptr;          // [P][H] expert outputs before the combine
     // MFMA (prefill) path
