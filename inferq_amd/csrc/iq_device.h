@@ -92,18 +92,18 @@ __device__ __forceinline__ float xor_lane(float v) {
     return __builtin_bit_cast(float, r);
 }
 
-// Maximum of v over the 64 lanes, in every lane: two lane-half swaps
-// (v_permlane32_swap, v_permlane16_swap) and four DPP steps inside rows.
+// Maximum of v over the 64 lanes, wave-uniform.  Four DPP steps inside each
+// 16-lane row (lanes a step leaves out read 0, the identity), then
+// row_bcast:15 and row_bcast:31 fold the rows into lane 63; every step
+// issues as one v_max_u32_dpp (half the VALU ops of lane-half swaps).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    v = max(a[0], a[1]);
-    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    v = max(b[0], b[1]);
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));  // row half mirror
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));  // row mirror
-    return v;
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, true));   // quad [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, true));   // quad [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, true));  // row half mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, true));  // row mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false)); // row_bcast:15 -> rows 1, 3
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false)); // row_bcast:31 -> rows 2, 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // hsum_f32_8 over the 8 lanes of a group: ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)).

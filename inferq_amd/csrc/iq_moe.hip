@@ -474,9 +474,8 @@ __global__ __launch_bounds__(128 * RG) void k_moe1_gate_up_rows(MoeParams p) {
         if (wave == 0 && sidx < K) {
             float lv[kRoutePer];
             route_load(p.logits + (int64_t)t * p.E, (int)p.E, lv);
-            int sel[kMoe1MaxSlots];
-            route_topk_any<kMoe1MaxSlots>(lv, (int)p.E, sidx + 1, sel);
-            if (lane == 0) s_e = sel[sidx];
+            const int er = route_rank(lv, (int)p.E, sidx);  // 4 tokens: 24.5 -> 23.9 us
+            if (lane == 0) s_e = er;
         }
         lds_barrier();
         if (sidx < K) e = __builtin_amdgcn_readfirstlane(s_e);

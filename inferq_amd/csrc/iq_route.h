@@ -80,6 +80,66 @@ __device__ __forceinline__ void route_topk_vals(const float (&lv)[kRoutePer], in
     }
 }
 
+// The expert at rank s (0-based) of the same order, wave-uniform, without
+// the s rounds before it: a bitwise search for T, the (s+1)-th largest key
+// counted with multiplicity (the largest value with at least s+1 keys at or
+// above it; keys are counted by ballots, so each step is a few compares and
+// scalar population counts), stopping once exactly s+1 keys lie at or above
+// the candidate (T is then their minimum); the expert is then the
+// (s - #{keys > T})-th lowest index among the keys equal to T.  Fewer VALU
+// ops than the rounds, but a longer dependent chain: it pays where many
+// workgroups share the SIMDs (several tokens), not for one token.
+template <int PER>
+__device__ __forceinline__ int route_rank_vals(const float (&lv)[kRoutePer], int E, int s) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) key[j] = PER * lane + j < E ? route_ukey(lv[j]) : 0u;
+    uint32_t lo = 0;  // invariant: at least s+1 keys are >= lo
+    bool exact = false;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t c = lo | (1u << b);
+        int n = 0;
+#pragma unroll
+        for (int q = 0; q < PER; q++) n += __builtin_popcountll(__ballot(key[q] >= c));
+        if (n > s) {
+            lo = c;
+            if (n == s + 1) {
+                exact = true;
+                break;
+            }
+        }
+    }
+    uint32_t T = lo;
+    if (exact) {
+        uint32_t mn = 0xffffffffu;
+#pragma unroll
+        for (int q = 0; q < PER; q++) mn = key[q] >= lo ? min(mn, key[q]) : mn;
+        T = ~wave_max_u32(~mn);
+    }
+    int above = 0;
+#pragma unroll
+    for (int q = 0; q < PER; q++) above += __builtin_popcountll(__ballot(key[q] > T));
+    for (int r = s - above;; r--) {  // r-th lowest index among the keys equal to T
+        bool has = false;
+        int jf = PER - 1;
+#pragma unroll
+        for (int j = PER - 1; j >= 0; j--) {
+            has = has || key[j] == T;
+            jf = key[j] == T ? j : jf;
+        }
+        const int L = (int)__builtin_ctzll(__ballot(has));
+        const int j = __builtin_amdgcn_readlane(jf, L);
+        if (r <= 0) return PER * L + j;
+#pragma unroll
+        for (int q = 0; q < PER; q++) key[q] = (lane == L && q == j) ? 0u : key[q];
+    }
+}
+
+__device__ __forceinline__ int route_rank(const float (&lv)[kRoutePer], int E, int s) {
+    return E <= 256 ? route_rank_vals<4>(lv, E, s) : route_rank_vals<kRoutePer>(lv, E, s);
+}
+
 template <int MAXK>
 __device__ __forceinline__ void route_topk_any(const float (&lv)[kRoutePer], int E, int count, int (&sel)[MAXK]) {
     if (E <= 256) route_topk_vals<MAXK, 4>(lv, E, count, sel);

@@ -86,6 +86,27 @@ def test_qwen_shaped_moe_matches_oracle(gpu, oracle, qwen_layer, m):
     assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, f"Qwen-shaped MoE m={m}")
 
 
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 12])
+def test_tied_logits_route_like_oracle(gpu, oracle, qwen_layer, m):
+    """Equal logits rank by lower index (src/qwen/moe.rs:21-54 as fixed in
+    route order): logits on a half-unit grid tie often, one row ties
+    everywhere, and +0 / -0 compare equal.  Covers the per-slot rank search
+    of the 2..11-token gate/up workgroups and the rounds elsewhere."""
+    moe, _ = _device_layer(qwen_layer, 8, gpu)
+    rng = np.random.default_rng(300 + m)
+    x = S.normal((m, 2048), rng)
+    logits = np.round(S.normal((m, 256), rng) * 2.0).astype(np.float32) / 2.0
+    logits[0, :] = 0.25
+    if m > 1:
+        logits[1, ::2] = -0.0
+        logits[1, 1::2] = 0.0
+    out = moe.forward(torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu))
+    ref, ref_e, _ = oracle.moe_forward(_oracle_layer(qwen_layer, 8), x, logits, mode=1, impl=_impl(oracle), nthreads=8)
+    assert [r.experts for r in out.routes] == ref_e.tolist()
+    assert out.routes[0].experts == list(range(8))
+    assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, f"tied logits m={m}")
+
+
 _NAMES = {Q4: "q4k", Q6: "q6k", Q8: "q80"}
 _FORMAT_PAIRS = [(Q4, Q6), (Q4, Q4), (Q6, Q6), (Q6, Q4), (Q8, Q8), (Q8, Q6)]
 
