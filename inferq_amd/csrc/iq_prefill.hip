@@ -12,8 +12,8 @@
 // output columns; each wave all 64 rows of 16 columns as four 16 x 16 tiles
 // of the double-rate v_mfma_i32_16x16x64_i8.  Per block the workgroup
 // stages the int8 activation tile (16 KiB), the 128 raw Q4_K blocks
-// (18 KiB), the bsums and the block scales in LDS, double buffered, the next
-// block's loads in flight while the current one is multiplied.  Each wave
+// (18 KiB), the bsums and the block scales in LDS, in three stages: the
+// next two blocks' loads in flight while the current one is multiplied.  Each wave
 // dequantises its B fragments in registers (nibbles, then one packed 16-bit
 // multiply per dword and stream).  Calls too small to fill the GPU with
 // such tiles take 32 x 64 tiles (4 waves, two row tiles each) and, only if
@@ -91,7 +91,21 @@ struct PfTile {
     static constexpr int kRT = ROWS / 16;
     static constexpr int kStA = 0, kStB = kStA + ROWS * kAS, kStH = kStB + COLS * kBS, kStD = kStH + ROWS * 32;
     static constexpr int kStage = kStD + ROWS * 4;
+    // Three stages, two blocks' loads in flight behind the one being
+    // multiplied ([256 x 4096] -> 2048: 20.4 -> 19.3 us per call, [256 x
+    // 2048] -> 8192: 19.2 -> 19.1 us against two stages).  Each stage is
+    // followed by 1 KiB that takes the loads of lanes and of whole
+    // instructions past the stage, so that every wave issues the same number
+    // of loads per stage and a wait can count them.
+    static constexpr int kNst = 3;
+    static constexpr int kStagePad = kStage + 1024;
 };
+
+// Workgroup barrier once this wave's LDS reads have returned, without the
+// release fence of lds_barrier: at workgroup scope that fence also waits for
+// every LDS DMA load in flight (vmcnt(0)), which would drain the stages
+// loading ahead.  Stage arrival is counted by explicit vmcnt waits.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Wave w owns all ROWS rows and columns 16w .. 16w+15 of the tile as RT
 // 16 x 16 tiles of v_mfma_i32_16x16x64_i8 (one decoded B fragment serves
@@ -105,7 +119,8 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
     constexpr int kThreads = T::kThreads;
     constexpr int kStA = T::kStA, kStB = T::kStB, kStH = T::kStH, kStD = T::kStD, kStage = T::kStage;
     constexpr int RT = T::kRT;
-    __shared__ __align__(16) uint8_t st[2][kStage];
+    constexpr int NST = T::kNst, kSP = T::kStagePad;
+    __shared__ __align__(16) uint8_t st[NST][kSP];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, jj = lane & 15;
@@ -126,27 +141,25 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
     // wave w of W fills the 64 consecutive 16-byte granules (W i + w) * 64 .. +63
     // of a stage, each lane the granule at base + 16 lane.  The stage keeps
     // its padded layout (A rows of 18 granules, B columns of 10, then H and
-    // D); pad granules and those past the stage load nothing.
+    // D).  Every lane loads, so that each wave issues the same count per
+    // stage: pad granules land in the row padding, granules past the stage
+    // (from clamped addresses) in the 1 KiB behind it.
     constexpr int kGA = ROWS * 18, kGB = COLS * 10, kGH = ROWS * 2, kGD = ROWS / 4;
     constexpr int kG = kGA + kGB + kGH + kGD;
     constexpr int kWaves = kThreads / 64, kIPer = (kG + kThreads - 1) / kThreads;
     static_assert(kStB == kGA * 16 && kStH == kStB + kGB * 16 && kStD == kStH + kGH * 16, "stage layout");
     const uint8_t* gsrc[kIPer];
     uint32_t gstr[kIPer];
-    bool gok[kIPer];
 #pragma unroll
     for (int i = 0; i < kIPer; i++) {
         int t = (i * kWaves + wave) * 64 + lane;
-        gok[i] = t < kG;
         t = min(t, kG - 1);
         if (t < kGA) {
             const int r = t / 18, gr = t - 18 * r;
-            gok[i] = gok[i] && gr < 16;
             gsrc[i] = (const uint8_t*)p.q + (int64_t)(row0 + r) * K + 16 * min(gr, 15);
             gstr[i] = 256;
         } else if ((t -= kGA) < kGB) {
             const int col = t / 10, gr = t - 10 * col;
-            gok[i] = gok[i] && gr < 9;
             const int64_t gc = min((int64_t)n0 + col, p.n - 1);
             gsrc[i] = p.w + gc * p.row_bytes + 16 * min(gr, 8);
             gstr[i] = 144;
@@ -162,13 +175,12 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
     auto issue = [&](int b, uint8_t* s) {
         b = min(b, b1 - 1);
 #pragma unroll
-        for (int i = 0; i < kIPer; i++) {
-            if (gok[i])
-                __builtin_amdgcn_global_load_lds(
-                    (const void __attribute__((address_space(1)))*)(gsrc[i] + (int64_t)b * gstr[i]),
-                    (void __attribute__((address_space(3)))*)(s + (i * kWaves + wave) * 1024), 16, 0, 0);
-        }
+        for (int i = 0; i < kIPer; i++)
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)(gsrc[i] + (int64_t)b * gstr[i]),
+                (void __attribute__((address_space(3)))*)(s + min((i * kWaves + wave) * 1024, kStage)), 16, 0, 0);
     };
+    static_assert(kIPer <= 15, "vmcnt field");
 
     float out[RT][4];  // [row tile][r]
 #pragma unroll
@@ -177,12 +189,23 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
         for (int r = 0; r < 4; r++) out[rt][r] = 0.f;
 
     issue(b0, st[0]);
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's granules are in LDS
-    lds_barrier();
+    if (!DBG && b0 + 1 < b1) {
+        issue(b0 + 1, st[1]);
+        __builtin_amdgcn_s_waitcnt(0x0f70 | kIPer);  // vmcnt(kIPer): stage 0 is in LDS
+    } else {
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    }
+    stage_barrier();
 
+    int cur = 0;
     for (int b = b0; b < b1; b++) {
-        const uint8_t* S = st[(b - b0) & 1];
-        if (b + 1 < b1) issue(b + 1, st[(b - b0 + 1) & 1]);
+        const uint8_t* S = st[cur];
+        const int nx = cur + 1 == NST ? 0 : cur + 1, nx2 = nx + 1 == NST ? 0 : nx + 1;
+        if constexpr (DBG) {  // the debug stores share vmcnt: one block ahead, drained each block
+            if (b + 1 < b1) issue(b + 1, st[nx]);
+        } else {
+            if (b + 2 < b1) issue(b + 2, st[nx2]);
+        }
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* bcol = S + kStB + (16 * wave + jj) * kBS;
         pf_q4k_block<RT, kAS>(S + kStA, bcol, S + kStH, (const float*)(S + kStD), g, jj, out,
@@ -196,8 +219,12 @@ __global__ __launch_bounds__((PfTile<ROWS, COLS>::kThreads)) void k_prefill_q4k(
                                  }
                              });
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-        lds_barrier();
+        if (!DBG && b + 2 < b1)
+            __builtin_amdgcn_s_waitcnt(0x0f70 | kIPer);  // vmcnt(kIPer): stage b + 1 is in LDS
+        else
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        stage_barrier();
+        cur = nx;
     }
 
     float* dst = p.splits == 1 ? p.y : p.part + (int64_t)blockIdx.z * p.m * p.n;
