@@ -100,8 +100,11 @@ def make_layers(n_layers, device, seed):
         g = torch.Generator(device=device)
         g.manual_seed(s + 7)
         t["selector"] = torch.randn(H, device=device, generator=g) / float(np.sqrt(H))
+        # the f32 router (blk.N.ffn_gate_inp.weight), used by the from-x line
+        t["router"] = torch.randn(E, H, device=device, generator=g) / float(np.sqrt(H))
         m = moe.QuantizedMoeLayer(H, I, E, TOPK, synth.Q4_K, synth.Q6_K, t["gate"], t["up"], t["down"],
-                                  t["shared_gate"], t["shared_up"], t["shared_down"], t["selector"])
+                                  t["shared_gate"], t["shared_up"], t["shared_down"], t["selector"],
+                                  router=t["router"])
         layers.append((m, t))
     return layers
 
@@ -215,34 +218,54 @@ class GraphSet:
         return {k: {"best_ms": min(v), "median_ms": float(np.median(v)), "reps": len(v)} for k, v in times.items()}
 
 
-def moe_protocol(layers, xs, logits, out, steps, reps, hip, kernel_bytes):
-    """The headline's timed graphs.
+def protocol_plan(steps, n_layers, kernel_bytes):
+    """Layer indices every headline graph captures, in capture order.
 
-    * layer_a/b/c: three graphs of exactly `steps` layer calls each, over
-      disjoint ranges of the rotated layers with fresh inputs per call;
-      replayed round-robin, so a graph's bytes were last touched two other
-      graphs ago (>= 2x the MALL for any steps >= 14) and no replay reads
-      its weights from the Infinity Cache.
-    * gate_up / down: each kernel alone (iq_moe_forward_stage re-runs a
-      layer's last call), one launch per layer over as many layers as make
-      >= 512 MiB of distinct weight bytes.
-    * mall_resident: `steps` calls of one layer on one input (every replay
-      after the first reads its 18 MB from the Infinity Cache), reported
-      separately.
+    * layer_a/b/c: `steps` layer calls each over disjoint ranges of the
+      rotated layers (call s of graph j is layer (j * steps + s) mod
+      n_layers, on input j * steps + s of the 3 * steps timed inputs).
+    * gate_up / down: one launch of that kernel per layer (the layer's last
+      call re-launched), over as many layers as make >= 512 MiB of distinct
+      weight bytes, and at least `steps`.
+    * mall_resident: `steps` calls of layer 0 on one input.
+    """
+    plan = {name: [(j * steps + s_) % n_layers for s_ in range(steps)]
+            for j, name in enumerate(("layer_a", "layer_b", "layer_c"))}
+    for name in ("gate_up", "down"):
+        launches = max(steps, -(-MIN_STREAM_BYTES // kernel_bytes[name]))
+        plan[name] = [i % n_layers for i in range(launches)]
+    plan["mall_resident"] = [0] * steps
+    return plan
+
+
+def moe_protocol(layers, xs, logits, out, steps, reps, hip, kernel_bytes, graphset=None):
+    """The headline's timed graphs (protocol_plan names what each captures).
+
+    The layer graphs are replayed round-robin with the others, so a graph's
+    bytes were last touched two other graphs ago (>= 2x the MALL for any
+    steps >= 14) and no replay reads its weights from the Infinity Cache;
+    the MALL-resident graph (every replay after the first reads its 18 MB
+    from the Infinity Cache) is reported separately.  Before any capture,
+    every layer a graph captures makes one eager call, so each handle has a
+    workspace and a last call (which the per-kernel graphs re-launch).
+    `xs` / `logits` hold the 3 * steps timed inputs.
     """
     n = len(layers)
-    gs = GraphSet(hip)
+    plan = protocol_plan(steps, n, kernel_bytes)
+    for li in sorted({li for v in plan.values() for li in v}):
+        layers[li][0].forward_into(xs[li % len(xs)], logits[li % len(logits)], out)
+    gs = graphset if graphset is not None else GraphSet(hip)
     for j, name in enumerate(("layer_a", "layer_b", "layer_c")):
-        def cap(j=j):
-            for s_ in range(steps):
+        def cap(j=j, seq=plan[name]):
+            for s_, li in enumerate(seq):
                 i = j * steps + s_
-                layers[i % n][0].forward_into(xs[i % len(xs)], logits[i % len(logits)], out)
+                layers[li][0].forward_into(xs[i % len(xs)], logits[i % len(logits)], out)
         gs.add(name, cap, steps)
     per_kernel = {}
     for stage, name in ((1, "gate_up"), (2, "down")):
-        launches = max(steps, -(-MIN_STREAM_BYTES // kernel_bytes[name]))
-        per_kernel[name] = launches
-        gs.add(name, lambda st=stage, L_=launches: [layers[i % n][0].forward_stage(st) for i in range(L_)], launches)
+        seq = plan[name]
+        per_kernel[name] = len(seq)
+        gs.add(name, lambda st=stage, seq=seq: [layers[li][0].forward_stage(st) for li in seq], len(seq))
     gs.add("mall_resident", lambda: [layers[0][0].forward_into(xs[0], logits[0], out) for _ in range(steps)], steps)
     res = gs.run(reps)
     return res, per_kernel
@@ -250,13 +273,14 @@ def moe_protocol(layers, xs, logits, out, steps, reps, hip, kernel_bytes):
 
 def time_graph(fn, iters, hip, warmup=3, reps=5, settle_ms=SETTLE_MS):
     """`iters` calls of fn(i) captured once in a HIP graph and replayed: GPU
-    time per call without host submission gaps, the median of `reps` timed
-    replays.  Every captured call runs once eagerly first, which grows the
-    library's per-layer workspaces, so the capture itself allocates
-    nothing.  Before the timed replays the graph runs untimed for about
-    `settle_ms`: a large stream (the LM head) measures 10-20% slower in its
-    first few milliseconds on an idle MI355X than once the clocks have
-    settled, which is the state of a decode loop."""
+    time per call without host submission gaps, the median and best of
+    `reps` timed replays (dict of median_ms / best_ms).  Every captured call
+    runs once eagerly first, which grows the library's workspaces, so the
+    capture itself allocates nothing.  Before the timed replays the graph
+    runs untimed for about `settle_ms`: a large stream (the LM head)
+    measures 10-20% slower in its first few milliseconds on an idle MI355X
+    than once the clocks have settled, which is the state of a decode
+    loop."""
     import torch
 
     cap = torch.cuda.Stream()
@@ -284,11 +308,11 @@ def time_graph(fn, iters, hip, warmup=3, reps=5, settle_ms=SETTLE_MS):
             torch.cuda.synchronize()
             times.append(hip.ms(t0, t1) / iters)
     hip.destroy([t0, t1])
-    return float(np.median(times))
+    return {"median_ms": float(np.median(times)), "best_ms": float(min(times)), "reps": reps}
 
 
 def host_layer(t):
-    d = {k: v.cpu().numpy() for k, v in t.items()}
+    d = {k: v.cpu().numpy() for k, v in t.items() if k != "router"}
     from inferq_amd import synth
 
     d.update(hidden=H, inter=I, n_experts=E, top_k=TOPK, normalize=True, gate_dtype=synth.Q4_K,
@@ -331,8 +355,114 @@ def cpu_model():
     return "unknown"
 
 
-def secondary(args, hip, stream, device, layers):
-    """Other BASELINE configs, reported beside the headline (not the value)."""
+class CpuLegs:
+    """The CPU figure beside each GPU line: the oracle's AVX2 restatement of
+    the reference's kernels (fused_forward over output rows, the MoE over
+    experts), one pool thread pinned per physical core, timed on a bounded
+    sample after one untimed call.  Also the checker each line's
+    max_abs_diff_vs_oracle comes from.  Imported only after the GPU timing
+    of a line is done."""
+
+    def __init__(self, seconds):
+        from oracle import oracle as O
+
+        self.O = O
+        self.phys, self.allowed = physical_cpus()
+        self.nt = len(self.phys)
+        self.impl = 1 if O.have_avx2() else 0
+        self.seconds = seconds
+
+    def _pinned(self, fn):
+        saved = os.sched_getaffinity(0)
+        self.O.pool_pin(self.phys)
+        os.sched_setaffinity(0, {self.phys[0]})
+        try:
+            return fn()
+        finally:
+            os.sched_setaffinity(0, saved)
+            self.O.pool_pin([])
+
+    def time(self, fn, max_reps=7):
+        """fn() once untimed, then up to max_reps timed calls within the
+        sample budget (at least one): best and median seconds."""
+        def run():
+            fn()
+            ts, t_end = [], time.perf_counter() + self.seconds
+            while len(ts) < max_reps and (not ts or time.perf_counter() < t_end):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            return ts
+        ts = self._pinned(run)
+        return {"best_seconds": min(ts), "median_seconds": float(np.median(ts)), "reps": len(ts),
+                "threads": self.nt, "kind": "port",
+                "impl": "AVX2 restatement" if self.impl else "scalar restatement"}
+
+    def matmul(self, dtype, wbytes, rows, cols, x, tiled=False):
+        return self._pinned(lambda: self.O.matmul(dtype, wbytes, rows, cols, x, impl=self.impl, nthreads=self.nt,
+                                                  tiled=tiled))
+
+    def time_matmul(self, dtype, wbytes, rows, cols, x, tiled=False):
+        return self.time(lambda: self.O.matmul(dtype, wbytes, rows, cols, x, impl=self.impl, nthreads=self.nt,
+                                               tiled=tiled))
+
+    def moe(self, hl, x, logits, mode):
+        return self._pinned(lambda: self.O.moe_forward(hl, x, logits, mode=mode, impl=self.impl,
+                                                       nthreads=self.nt)[0])
+
+    def time_moe(self, hl, x, logits, mode):
+        return self.time(lambda: self.O.moe_forward(hl, x, logits, mode=mode, impl=self.impl, nthreads=self.nt))
+
+
+def max_abs_diff(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max())
+
+
+def normwise(got, ref):
+    """max_i |g - r| / max_i |r|: the path's stated f32 tolerance measure."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def measurement(tensor, dtype, rows, cols, storage, input_rows, t, path, moved=None, peak=HBM_PEAK_GBS,
+                diff=None, cpu=None, bitexact=None, rel=None):
+    """One line in the reference's Measurement shape
+    (src/bin/gguf_matmul_bench.rs:62-84): best and median seconds, ns per
+    input row, effective GB/s of the weight bytes, the largest absolute
+    difference against the checker (the oracle, in place of candle) and the
+    speed-up over the CPU leg; plus us, algorithmic GB/s (`moved` bytes,
+    default the weight bytes) and its fraction of HBM peak."""
+    med, best = t["median_ms"] * 1e-3, t["best_ms"] * 1e-3
+    moved = storage if moved is None else moved
+    d = {"tensor": tensor, "dtype": dtype, "rows": rows, "columns": cols, "storage_bytes": storage, "path": path,
+         "input_rows": input_rows, "best_seconds": best, "median_seconds": med,
+         "nanoseconds_per_input_row": round(med * 1e9 / input_rows, 1),
+         "effective_gigabytes_per_second": round(storage / med / 1e9, 1),
+         "us": round(med * 1e6, 3), "GB_s": round(moved / med / 1e9, 1),
+         "frac_hbm": round(moved / med / 1e9 / peak, 4), "max_abs_diff_vs_oracle": diff}
+    if rel is not None:
+        d["normwise_rel_err_vs_oracle"] = rel
+    if bitexact is not None:
+        d["bitexact_fraction_vs_oracle"] = bitexact
+    if cpu is not None:
+        d["cpu"] = cpu
+        d["speedup_vs_cpu"] = round(cpu["median_seconds"] / med, 1)
+    return d
+
+
+def bit_fraction(got, ref):
+    got = np.ascontiguousarray(got, np.float32)
+    ref = np.ascontiguousarray(ref, np.float32)
+    return float((got.view(np.uint32) == ref.view(np.uint32)).mean())
+
+
+def secondary(args, hip, stream, device, layers, cpu=None, chk=None):
+    """Other BASELINE configs, reported beside the headline (not the
+    value).  Every line: GPU graph timing (median / best), then the
+    checker's output on the same input and a bounded CPU-leg sample."""
     import torch
 
     from inferq_amd import qgemm, synth
@@ -340,37 +470,37 @@ def secondary(args, hip, stream, device, layers):
     extra = {}
     # config 1: Q8_0 [4096 x 2048] matvec, rotated over copies beyond 2x the MALL
     copies = -(-MIN_STREAM_BYTES // (4096 * 2048 // 32 * 34))
-    mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q8_0, 4096, 2048, device, 50 + c),
-                                       synth.Q8_0, 4096, 2048) for c in range(copies)]
+    raw = [synth.random_matrix_device(synth.Q8_0, 4096, 2048, device, 50 + c) for c in range(copies)]
+    mats = [qgemm.QuantizedMatrix.view(r, synth.Q8_0, 4096, 2048) for r in raw]
     x = torch.randn(2048, 2048, device=device).reshape(-1, 1, 2048)
     y = torch.empty(1, 4096, device=device)
-    ms = time_graph(lambda i: mats[i % copies].forward_into(x[i % 2048], y), args.steps, hip)
-    b = mats[0].storage_bytes() + 2048 * 4 + 4096 * 4
-    extra["q8_0_matvec_4096x2048"] = {"us": round(ms * 1e3, 3), "GB_s": round(b / ms / 1e6, 1),
-                                      "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    del mats
-    # LM head [248320 x 2048] Q6_K, M=1 (417 MB: larger than the MALL)
-    lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 60),
-                                    synth.Q6_K, 248320, 2048)
-    yl = torch.empty(1, 248320, device=device)
-    ms = time_graph(lambda i: lm.forward_into(x[i % 2048], yl), max(10, args.steps // 10), hip)
-    b = lm.storage_bytes() + 2048 * 4 + 248320 * 4
-    extra["lm_head_q6k_248320x2048_m1"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1),
-                                           "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    x8 = torch.randn(8, 2048, device=device)
-    y8 = torch.empty(8, 248320, device=device)
-    ms = time_graph(lambda i: lm.forward_into(x8, y8), 10, hip, warmup=2)
-    extra["lm_head_q6k_m8"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1)}
-    del lm
+    t = time_graph(lambda i: mats[i % copies].forward_into(x[i % 2048], y), args.steps, hip)
+    st = mats[0].storage_bytes()
+    kw = {}
+    if cpu is not None:
+        got = mats[0].forward(x[0]).cpu().numpy()
+        wh, xh = raw[0].cpu().numpy(), x[0].cpu().numpy()
+        ref = cpu.matmul(synth.Q8_0, wh, 4096, 2048, xh)
+        kw = dict(diff=max_abs_diff(got, ref), rel=normwise(got, ref), bitexact=bit_fraction(got, ref),
+                  cpu=cpu.time_matmul(synth.Q8_0, wh, 4096, 2048, xh))
+    extra["q8_0_matvec_4096x2048"] = measurement("q8_0 [4096x2048]", "Q8_0", 4096, 2048, st, 1, t, "gpu:auto",
+                                                 moved=st + 2048 * 4 + 4096 * 4, **kw)
+    del mats, raw
+    # LM head [248320 x 2048] Q6_K at M = 1 and 8 (417 MB: larger than the MALL)
+    extra.update(lm_head_lines(args, hip, device, cpu))
     # config 3: verify pass MoE at M = 4 and 8 (independent routing per row)
-    extra.update(moe_tokens(hip, device, layers, (4, 8)))
+    extra.update(moe_tokens(hip, device, layers, (4, 8), cpu, chk))
+    # the whole sublayer from x (router on the GPU, residual add) at M = 1
+    extra["moe_from_x_m1"] = moe_from_x(hip, device, layers, cpu, chk)
     # configs 2/3: dense projections beside the MoE (attention q/gate, k, v, o),
     # one call each per step, rotated over copies beyond the MALL
     shapes = (("q_gate", 8192, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 4096))
     copies = -(-MIN_STREAM_BYTES // sum(r * c // 256 * 144 for _, r, c in shapes))
-    proj = [[qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q4_K, n, k, device, 700 + 10 * c + j),
-                                        synth.Q4_K, n, k) for j, (_, n, k) in enumerate(shapes)] for c in range(copies)]
+    raw = [[synth.random_matrix_device(synth.Q4_K, n, k, device, 700 + 10 * c + j) for j, (_, n, k) in
+            enumerate(shapes)] for c in range(copies)]
+    proj = [[qgemm.QuantizedMatrix.view(r, synth.Q4_K, n, k) for r, (_, n, k) in zip(rc, shapes)] for rc in raw]
     pbytes = sum(p.storage_bytes() for p in proj[0])
+    wh = [r.cpu().numpy() for r in raw[0]] if cpu is not None else None
     for m in (1, 4, 8):
         xin = {k: torch.randn(m, k, device=device) for k in (2048, 4096)}
         yout = [torch.empty(m, n, device=device) for _, n, _ in shapes]
@@ -380,45 +510,132 @@ def secondary(args, hip, stream, device, layers):
             for j, (_, n, k) in enumerate(shapes):
                 mats[j].forward_into(xin[k], yout[j])
 
-        ms = time_graph(step, 50, hip)
-        b = pbytes + m * 4 * sum(n + k for _, n, k in shapes)
-        extra[f"dense_projections_m{m}"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1),
-                                            "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    del proj
+        t = time_graph(step, 50, hip)
+        kw = {}
+        if cpu is not None:
+            xh = {k: v.cpu().numpy() for k, v in xin.items()}
+            diff, rel, bits = 0.0, 0.0, []
+            for j, (_, n, k) in enumerate(shapes):
+                got = proj[0][j].forward(xin[k]).cpu().numpy()
+                ref = cpu.matmul(synth.Q4_K, wh[j], n, k, xh[k])
+                diff = max(diff, max_abs_diff(got, ref))
+                rel = max(rel, normwise(got, ref))
+                bits.append(bit_fraction(got, ref))
+            ct = cpu.time(lambda: [cpu.O.matmul(synth.Q4_K, wh[j], n, k, xh[k], impl=cpu.impl, nthreads=cpu.nt)
+                                   for j, (_, n, k) in enumerate(shapes)])
+            kw = dict(diff=diff, rel=rel, bitexact=float(np.mean(bits)), cpu=ct)
+        extra[f"dense_projections_m{m}"] = measurement(
+            "attention q/gate [8192x2048] + k, v [512x2048] + o [2048x4096]", "Q4_K", 11264, 2048, pbytes, m, t,
+            "gpu:auto", moved=pbytes + m * 4 * sum(n + k for _, n, k in shapes), **kw)
+    del proj, raw
     return extra
 
 
-def moe_tokens(hip, device, layers, widths):
+def lm_head_lines(args, hip, device, cpu=None):
+    """The LM head [248320 x 2048] Q6_K at M = 1 and 8 (one 417 MB matrix
+    per launch: larger than the Infinity Cache)."""
+    import torch
+
+    from inferq_amd import qgemm, synth
+
+    raw = synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 60)
+    lm = qgemm.QuantizedMatrix.view(raw, synth.Q6_K, 248320, 2048)
+    st = lm.storage_bytes()
+    wh = raw.cpu().numpy() if cpu is not None else None
+    res = {}
+    for m in (1, 8):
+        x = torch.randn(m, 2048, device=device)
+        y = torch.empty(m, 248320, device=device)
+        t = time_graph(lambda i: lm.forward_into(x, y), max(10, args.steps // 10), hip, warmup=2)
+        kw = {}
+        if cpu is not None:
+            got = lm.forward(x).cpu().numpy()
+            xh = x.cpu().numpy()
+            ref = cpu.matmul(synth.Q6_K, wh, 248320, 2048, xh)
+            kw = dict(diff=max_abs_diff(got, ref), rel=normwise(got, ref), bitexact=bit_fraction(got, ref),
+                      cpu=cpu.time_matmul(synth.Q6_K, wh, 248320, 2048, xh))
+        res["lm_head_q6k_248320x2048_m1" if m == 1 else "lm_head_q6k_m8"] = measurement(
+            "lm_head [248320x2048]", "Q6_K", 248320, 2048, st, m, t, "gpu:auto",
+            moved=st + m * (2048 + 248320) * 4, **kw)
+    del lm, raw
+    return res
+
+
+def moe_tokens(hip, device, layers, widths, cpu=None, chk=None):
     """the MoE layer at M tokens per call (verify
     widths), each row routed independently, graph replay over the resident
-    layers; bytes counted over the distinct experts a call reads."""
+    layers; bytes counted over the distinct experts a call reads.  The
+    checker runs layer chk[0] (whose host copy is chk[1]) on the first
+    input."""
     import torch
 
     n = len(layers)
     g = torch.Generator(device=device)
     g.manual_seed(77)
     res = {}
+    gu, dn = expert_bytes()
     for m in widths:
         xs = torch.randn(64, m, H, device=device, generator=g)
         lg = torch.randn(64, m, E, device=device, generator=g)
         out = torch.empty(m, H, device=device)
-        ms = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 64], lg[i % 64], out), 40, hip)
+        t = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 64], lg[i % 64], out), 40, hip)
         uniq = float(np.mean([len(torch.unique(torch.topk(lg[j], TOPK, dim=1).indices)) for j in range(64)]))
         kb = moe_kernel_bytes(m, uniq)
         tot = kb["gate_up"] + kb["down"] + kb["prep"]
-        res[f"moe_layer_m{m}"] = {"us": round(ms * 1e3, 2), "unique_experts": round(uniq, 1),
-                                  "GB_s": round(tot / ms / 1e6, 1), "frac_hbm": round(tot / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        kw = {}
+        if cpu is not None and chk is not None:
+            ci, hl = chk
+            got = layers[ci][0].forward(xs[0], lg[0]).hidden.cpu().numpy()
+            xh, lh = xs[0].cpu().numpy(), lg[0].cpu().numpy()
+            ref = cpu.moe(hl, xh, lh, 1)
+            kw = dict(diff=max_abs_diff(got, ref), rel=normwise(got, ref), bitexact=bit_fraction(got, ref), cpu=cpu.time_moe(hl, xh, lh, 1))
+        line = measurement(f"MoE layer ({E} experts, top-{TOPK} + shared)", "Q4_K gate/up, Q6_K down", E * I,
+                           H, int((uniq + 1) * (gu + dn)), m, t, "gpu:token-major", moved=tot, **kw)
+        line["unique_experts"] = round(uniq, 1)
+        res[f"moe_layer_m{m}"] = line
     return res
 
 
-def prefill(args, hip, stream, device):
+def moe_from_x(hip, device, layers, cpu=None, chk=None):
+    """The whole sublayer from x at M = 1 (iq_moe_forward_x): the router
+    matmul [256 x 2048] f32 on the GPU, routing, experts, shared expert and
+    out = residual + MoE(x) -- the entry a decoder-layer binding calls --
+    graph replay over the rotated layers.  The checker takes the router
+    logits from the oracle's restatement (the router's f32 order is fixed
+    here, the reference's is candle's, so this line is compared within
+    1e-4, not bitwise)."""
+    import torch
+
+    n = len(layers)
+    g = torch.Generator(device=device)
+    g.manual_seed(78)
+    xs = torch.randn(64, 1, H, device=device, generator=g)
+    res_in = torch.randn(64, 1, H, device=device, generator=g)
+    out = torch.empty(1, H, device=device)
+    t = time_graph(lambda i: layers[i % n][0].forward_x_into(xs[i % 64], out, res_in[i % 64]), 40, hip)
+    gu, dn = expert_bytes()
+    moved = 9 * (gu + dn) + E * H * 4 + H * 4 + 3 * H * 4  # experts, router, selector, x, residual, out
+    diff = nre = None
+    if cpu is not None and chk is not None:
+        ci, hl = chk
+        got = layers[ci][0].forward(xs[0], residual=res_in[0]).hidden.cpu().numpy().astype(np.float64)
+        xh = xs[0].cpu().numpy()
+        lh = cpu.O.router_logits(xh, layers[ci][1]["router"].cpu().numpy())
+        ref = res_in[0].cpu().numpy().astype(np.float64) + cpu.moe(hl, xh, lh, 0)
+        diff, nre = max_abs_diff(got, ref), normwise(got, ref)
+    return measurement("MoE layer from x (router + experts + residual)", "Q4_K gate/up, Q6_K down, f32 router",
+                       E * I, H, 9 * (gu + dn), 1, t, "gpu:forward_x", moved=moved, diff=diff, rel=nre)
+
+
+def prefill(args, hip, stream, device, cpu=None):
     """BASELINE configs[3], dense part: Q4_K [256 x 2048] -> 8192 and
-    [256 x 4096] -> 2048 (and Q6_K [256 x 2048] -> 8192) on int8 MFMA (activation quantisation and the MFMA
-    kernel, and any split-K reduction, all inside the timed call), on both
-    MFMA paths: the dispatch's exact lane order (bitwise the
-    reference) and the prefill tiles a caller requests explicitly (tile
-    order, within 1e-4).  TOPS = 2 M N K / time; peak = 5.0 POPS dense
-    int8."""
+    [256 x 4096] -> 2048 (and Q6_K [256 x 2048] -> 8192) on int8 MFMA
+    (activation quantisation and the MFMA kernel, and any split-K
+    reduction, all inside the timed call), on both MFMA paths: the
+    dispatch's exact lane order (bitwise the reference) and the prefill
+    tiles a caller requests explicitly (tile order, within 1e-4).  TOPS =
+    2 M N K / time; peak = 5.0 POPS dense int8.  The CPU leg is the
+    reference's 16-row tiled fused_forward (src/gguf.rs:493-520)."""
     import torch
 
     from inferq_amd import _lib, qgemm, synth
@@ -429,38 +646,29 @@ def prefill(args, hip, stream, device):
     paths = {"tiles": _lib.PATH_PREFILL_TILES, "exact": _lib.PATH_AUTO}
     for dt, n, k, labels in cases:
         copies = -(-MIN_STREAM_BYTES // synth.matrix_bytes(dt, n, k))
-        mats = [qgemm.QuantizedMatrix.view(synth.random_matrix_device(dt, n, k, device, 90 + c), dt, n, k)
-                for c in range(copies)]
+        raw = [synth.random_matrix_device(dt, n, k, device, 90 + c) for c in range(copies)]
+        mats = [qgemm.QuantizedMatrix.view(r, dt, n, k) for r in raw]
         x = torch.randn(256, k, device=device)
         y = torch.empty(256, n, device=device)
+        name = "q4k" if dt == synth.Q4_K else "q6k"
+        ref = ct = None
+        if cpu is not None:
+            wh, xh = raw[0].cpu().numpy(), x.cpu().numpy()
+            ref = cpu.matmul(dt, wh, n, k, xh, tiled=True)
+            ct = cpu.time_matmul(dt, wh, n, k, xh, tiled=True)
         for label in labels:
             path = paths[label]
-            ms = time_graph(lambda i: mats[i % copies].forward_into(x, y, path), max(20, args.steps // 4), hip)
-            tops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
-            name = "q4k" if dt == synth.Q4_K else "q6k"
-            res[f"{name}_256x{k}_to_{n}_{label}"] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
-                                                     "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-        del mats
-    return res
-
-
-def lm_head_only(args, hip, device):
-    """The LM head [248320 x 2048] Q6_K alone at M = 1 and 8 (one 417 MB
-    matrix per launch: larger than the Infinity Cache)."""
-    import torch
-
-    from inferq_amd import qgemm, synth
-
-    lm = qgemm.QuantizedMatrix.view(synth.random_matrix_device(synth.Q6_K, 248320, 2048, device, 60),
-                                    synth.Q6_K, 248320, 2048)
-    b = lm.storage_bytes() + 2048 * 4 + 248320 * 4
-    res = {}
-    for m in (1, 8):
-        x = torch.randn(m, 2048, device=device)
-        y = torch.empty(m, 248320, device=device)
-        ms = time_graph(lambda i: lm.forward_into(x, y), max(10, args.steps // 10), hip)
-        res[f"m{m}"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1),
-                        "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4)}
+            t = time_graph(lambda i: mats[i % copies].forward_into(x, y, path), max(20, args.steps // 4), hip)
+            tops = 2 * 256 * n * k / (t["median_ms"] * 1e-3) / 1e12
+            kw = {}
+            if ref is not None:
+                got = mats[0].forward_via(x, path).cpu().numpy()
+                kw = dict(diff=max_abs_diff(got, ref), rel=normwise(got, ref), bitexact=bit_fraction(got, ref), cpu=ct)
+            line = measurement(f"{name} [{n}x{k}]", "Q4_K" if dt == synth.Q4_K else "Q6_K", n, k,
+                               mats[0].storage_bytes(), 256, t, f"gpu:{label}", **kw)
+            line.update(TOPS=round(tops, 1), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
+            res[f"{name}_256x{k}_to_{n}_{label}"] = line
+        del mats, raw
     return res
 
 
@@ -474,15 +682,15 @@ def decode_sweep(args, hip, device, layers):
     [2048 x 4096] (src/qwen/quantized_deltanet.rs:419-434, 537-563, 699) --
     all Q4_K, each followed by its MoE layer; then the LM head [248320 x
     2048] Q6_K; at M = 1 and M = 8 rows.  Every call of a step is launched
-    in order on one stream (graph replay); reported: matmul time per step,
-    tokens per second of matmul time, and the step's algorithmic HBM bytes
-    over that time.  The *_qkv_rows lines also join the attention layers'
-    q/gate, k and v into one [9216 x 2048] matrix (QuantizedMatrix::
-    concatenate_rows, src/gguf.rs:379-404): one launch instead of three, the
-    same bytes and bitwise the same outputs; likewise the DeltaNet layers'
-    qkvz and ba, which the reference computes from the same input
-    (src/qwen/quantized_deltanet.rs:537-563), as one [12352 x 2048]
-    matrix."""
+    in order on one stream (graph replay of 10 steps); reported: matmul time
+    per step, tokens per second of matmul time, and the step's algorithmic
+    HBM bytes over that time.  The *_qkv_rows lines also join the attention
+    layers' q/gate, k and v into one [9216 x 2048] matrix
+    (QuantizedMatrix::concatenate_rows, src/gguf.rs:379-404): one launch
+    instead of three, the same bytes and bitwise the same outputs; likewise
+    the DeltaNet layers' qkvz and ba, which the reference computes from the
+    same input (src/qwen/quantized_deltanet.rs:537-563), as one
+    [12352 x 2048] matrix."""
     import torch
 
     from inferq_amd import qgemm, synth
@@ -506,7 +714,7 @@ def decode_sweep(args, hip, device, layers):
     gu, dn = expert_bytes()
     g = torch.Generator(device=device)
     g.manual_seed(args.seed + 9)
-    res = {"layers": n, "attention_layers": sum(is_attn), "deltanet_layers": n - sum(is_attn)}
+    res = {"layers": n, "attention_layers": sum(is_attn), "deltanet_layers": n - sum(is_attn), "steps_per_graph": 10}
     for m in (1, 8):
         xin = {c: torch.randn(m, c, device=device, generator=g) for c in (2048, 4096)}
         lg = torch.randn(n, m, E, device=device, generator=g)
@@ -530,18 +738,22 @@ def decode_sweep(args, hip, device, layers):
         uniq = float(np.mean([len(torch.unique(torch.topk(lg[li], TOPK, dim=1).indices)) for li in range(n)]))
         total = n * (uniq + 1) * (gu + dn) + dense_bytes + lm.storage_bytes()
         for name, fn in ((f"m{m}", step), (f"m{m}_qkv_rows", lambda i: step(i, True))):
-            ms = time_graph(fn, 2, hip, warmup=1)
-            res[name] = {"us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(m / (ms * 1e-3), 1),
+            t = time_graph(fn, 10, hip, warmup=1, reps=3)
+            ms = t["median_ms"]
+            res[name] = {"us_per_step": round(ms * 1e3, 1), "us_per_step_best": round(t["best_ms"] * 1e3, 1),
+                         "tokens_per_s": round(m / (ms * 1e-3), 1),
                          "unique_experts_per_layer": round(uniq, 1), "GB_per_step": round(total / 1e9, 3),
                          "GB_s": round(total / ms / 1e6, 1), "frac_hbm": round(total / ms / 1e6 / HBM_PEAK_GBS, 4)}
     del dense, qkv, lm
     return res
 
 
-def prefill_moe(args, hip, stream, device, layers):
+def prefill_moe(args, hip, stream, device, layers, cpu=None, chk=None):
     """BASELINE configs[3], MoE part: 256 tokens, top-8 of 256 experts with
     Dirichlet(0.3) router skew, plus the shared expert.  TOPS counts the
-    expert products actually routed: 2 * (rows routed + 256 shared) * 3 * I * H."""
+    expert products actually routed: 2 * (rows routed + 256 shared) * 3 * I
+    * H.  The checker and the CPU leg run layer chk[0] grouped by expert
+    (routed_grouped_by_expert, src/qwen/quantized_moe.rs:336-406)."""
     import torch
 
     n = len(layers)
@@ -554,12 +766,23 @@ def prefill_moe(args, hip, stream, device, layers):
                    .to(device))
         xs.append(torch.randn(m, H, device=device))
     out = torch.empty(m, H, device=device)
-    ms = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 8], lgs[i % 8], out), 20, hip)
+    t = time_graph(lambda i: layers[i % n][0].forward_into(xs[i % 8], lgs[i % 8], out), 20, hip)
     ops = 2 * (m * TOPK + m) * 3 * I * H
     uniq = float(np.mean([len(torch.unique(torch.topk(lg, TOPK, dim=1).indices)) for lg in lgs]))
-    tops = ops / (ms * 1e-3) / 1e12
-    return {"us": round(ms * 1e3, 2), "unique_experts": round(uniq, 1), "TOPS": round(tops, 1),
-            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+    tops = ops / (t["median_ms"] * 1e-3) / 1e12
+    gu, dn = expert_bytes()
+    kw = {}
+    if cpu is not None and chk is not None:
+        ci, hl = chk
+        got = layers[ci][0].forward(xs[0], lgs[0]).hidden.cpu().numpy()
+        xh, lh = xs[0].cpu().numpy(), lgs[0].cpu().numpy()
+        ref = cpu.moe(hl, xh, lh, 1)
+        kw = dict(diff=max_abs_diff(got, ref), rel=normwise(got, ref), bitexact=bit_fraction(got, ref), cpu=cpu.time_moe(hl, xh, lh, 1))
+    line = measurement(f"MoE layer ({E} experts, top-{TOPK} + shared), Dirichlet(0.3) routing",
+                       "Q4_K gate/up, Q6_K down", E * I, H, int((uniq + 1) * (gu + dn)), m, t, "gpu:grouped",
+                       **kw)
+    line.update(unique_experts=round(uniq, 1), TOPS=round(tops, 1), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
+    return line
 
 
 def main():
@@ -572,9 +795,12 @@ def main():
                          ">= 2x the 256 MB Infinity Cache of distinct weights")
     ap.add_argument("--reps", type=int, default=7, help="interleaved timed replays of every graph (best and median)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-line-seconds", type=float, default=2.0,
+                    help="bounded CPU sample beside each secondary line (0 = no CPU legs or checker diffs)")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--no-parity", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "moe_prefill", "moe_tokens", "lm_head", "decode_sweep"), default=None,
+    ap.add_argument("--only", choices=("prefill", "moe_prefill", "moe_tokens", "lm_head", "decode_sweep", "moe_x"),
+                    default=None,
                     help="run one secondary config alone (for profiling) and print its JSON")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC byte-counter calibration)")
@@ -606,7 +832,7 @@ def main():
         if args.only == "prefill":
             out_only = prefill(args, hip, stream, device)
         else:
-            out_only = lm_head_only(args, hip, device)
+            out_only = lm_head_lines(args, hip, device)
         print(json.dumps({"only": args.only, "result": out_only}), flush=True)
         return
 
@@ -630,6 +856,9 @@ def main():
         return
     if args.only == "moe_tokens":
         print(json.dumps({"only": args.only, "result": moe_tokens(hip, device, layers, (1, 4, 8))}), flush=True)
+        return
+    if args.only == "moe_x":
+        print(json.dumps({"only": args.only, "result": moe_from_x(hip, device, layers)}), flush=True)
         return
 
     eager_ms, eager_per = time_moe(layers, xs, logits, out, args.steps, args.warmup, hip, stream)
@@ -689,11 +918,15 @@ def main():
                      "algorithmic_bytes": kb[dom], "avg_us": round(avg[dom] * 1e3, 3)},
     }
 
+    chk = cpu = None
     if not args.no_parity:
         from oracle import oracle as O
 
         li = (args.warmup + args.steps - 1) % args.layers
         hl = host_layer(layers[li][1])
+        chk = (li, hl)
+        if args.cpu_line_seconds > 0:
+            cpu = CpuLegs(args.cpu_line_seconds)
         xi, li_ = xs[-1].cpu().numpy(), logits[-1].cpu().numpy()
         got = layers[li][0].forward(xs[-1], logits[-1])
         ref, re, _ = O.moe_forward(hl, xi, li_, mode=0, impl=1 if O.have_avx2() else 0, nthreads=cpu_threads())
@@ -735,9 +968,9 @@ def main():
             log(f"cpu baseline: {result['cpu_baseline']}")
 
     if not args.no_secondary:
-        result["extra"] = secondary(args, hip, stream, device, layers)
-        result["extra"]["prefill_int8_tops"] = prefill(args, hip, stream, device)
-        result["extra"]["prefill_moe_m256_dirichlet"] = prefill_moe(args, hip, stream, device, layers)
+        result["extra"] = secondary(args, hip, stream, device, layers, cpu, chk)
+        result["extra"]["prefill_int8_tops"] = prefill(args, hip, stream, device, cpu)
+        result["extra"]["prefill_moe_m256_dirichlet"] = prefill_moe(args, hip, stream, device, layers, cpu, chk)
         result["extra"]["decode_step_sweep"] = decode_sweep(args, hip, device, layers)
         log(f"secondary: {result['extra']}")
 

@@ -14,10 +14,20 @@
  *     pointers are ordinary process memory.
  *   - Every function returns IQ_OK (0) or a negative IQ_ERR_* code;
  *     iq_last_error() returns this thread's message for the last failure.
- *   - Results are deterministic and bit-identical to the reference's CPU
- *     kernels for the same inputs, whatever the row count, on every entry
- *     except iq_matmul_via(..., IQ_PATH_PREFILL_TILES, ...), which a caller
- *     must request explicitly (its f32 order differs; within 1e-4).
+ *   - Results are deterministic and do not depend on the row count.  For
+ *     Q4_K, Q6_K and Q8_0 matrices they are bit-identical to the
+ *     reference's CPU kernels for the same inputs, on every entry except
+ *     iq_matmul_via(..., IQ_PATH_PREFILL_TILES, ...), which a caller must
+ *     request explicitly (its f32 order differs; within 1e-4).  Three f32
+ *     orders follow a published or fixed order that the reference's own
+ *     code (candle's, absent here) could not be checked against, so they
+ *     are bit-identical to this library's CPU restatement and within 1e-4
+ *     of the reference: Q5_K products (ggml's vec_dot_q5_K_q8_K order), the
+ *     router logits of iq_moe_forward_x, and the shared-expert selector dot.
+ *   - Workspaces: library-owned device memory grows on the first call that
+ *     needs more and is never freed under a graph that may still use it.
+ *     Growth is refused during graph capture; the *_reserve entries size a
+ *     workspace ahead of a capture.
  *   - stream is a hipStream_t (NULL = the default stream).
  */
 #ifndef IQ_QGEMM_H
@@ -119,9 +129,11 @@ int iq_weights_leading_rows(iq_weight_t a, int64_t rows, iq_weight_t *out);
  * bitwise what a one-row call gives.  Uses a library workspace per (device,
  * stream): calls on different streams or threads never share memory, and
  * the library lock is held while a call enqueues its launches.  A workspace
- * grows on the first call that needs more (synchronising that stream); such
- * a call fails during graph capture, so capture after one eager call of the
- * same size, or use iq_matmul_ws.
+ * grows on the first call that needs more; such a call fails during graph
+ * capture, so call iq_matmul_reserve for the widest call first (or make one
+ * eager call of that size, or use iq_matmul_ws).  A grown workspace's old
+ * buffer stays allocated until iq_workspace_release, so a graph captured
+ * before a wider eager call on the same stream stays valid.
  * Replaces: QuantizedMatrix::forward / forward_spread / forward_rows /
  * multi_row_forward / fused_forward (src/gguf.rs:406-456, :558-690) and the
  * per-row kernels q4k_q8k_row / q6k_q8k_row / q80_q80_row they call
@@ -132,6 +144,22 @@ int iq_matmul(iq_weight_t w, const float *x, int64_t m, float *y, iq_stream_t st
  * kernel does not cover the dtype, shape or row count.
  * Replaces: QuantizedMatrix::forward_via (src/gguf.rs:522-556). */
 int iq_matmul_via(iq_weight_t w, const float *x, int64_t m, float *y, int path, iq_stream_t stream);
+
+/* Size the library workspace of `stream` (current device) for calls of up
+ * to m input rows of W through iq_matmul, iq_matmul_via and
+ * iq_matmul_argmax, so that such calls can be captured into a graph
+ * without an eager call first.  Not during capture.
+ * Replaces: the reference's load-time allocation of the per-call buffers
+ * fused_forward otherwise allocates per call (src/gguf.rs:608-690). */
+int iq_matmul_reserve(iq_weight_t w, int64_t m, iq_stream_t stream);
+
+/* Free the library workspace of `stream` on the current device (its live
+ * buffer and every buffer it outgrew), after synchronising the stream.  A
+ * graph captured with entries on that stream must not be replayed after
+ * this call.  For callers that create and destroy many streams; the next
+ * call on the stream allocates again.
+ * No counterpart in the reference (its per-call buffers are Rust Vecs). */
+int iq_workspace_release(iq_stream_t stream);
 
 /* Device workspace bytes iq_matmul_ws needs for m input rows of W (any
  * path). */
@@ -259,18 +287,32 @@ typedef struct {
 int iq_moe_create(const iq_moe_desc *desc, iq_moe_t *out);
 int iq_moe_destroy(iq_moe_t moe);
 
+/* Size the handle's workspace for calls of up to max_tokens tokens (one
+ * slice at most), so that they can be captured into a graph without an
+ * eager call first.  Not during capture.
+ * Replaces: the buffers QuantizedMoeLayer::load prepares for the layer
+ * (src/qwen/quantized_moe.rs:141-225); the reference allocates the rest per
+ * call. */
+int iq_moe_reserve(iq_moe_t moe, int64_t max_tokens, iq_stream_t stream);
+
+/* Tokens one set of the layer's launches serves (wider calls are sliced):
+ * 4096 / top_k, and at most 32 * (8192 / n_experts). */
+int64_t iq_moe_slice_tokens(iq_moe_t moe);
+
 /* out[m x hidden] = MoE(x[m x hidden]) for device x, router logits
  * [m x n_experts] and out.  Routing is softmax, top-k by probability,
  * renormalised (src/qwen/moe.rs:21-54); routed experts run grouped by
  * expert (src/qwen/quantized_moe.rs:336-406), SwiGLU between gate/up and
  * down, ordered combine, then routed + shared * sigmoid(x . selector)
  * (:266-273).  experts_out [m x top_k] i32 and weights_out [m x top_k] f32
- * (device, may be NULL) receive the routes.  m * top_k <= 4096.
- * The handle owns a workspace sized by the widest call so far; a wider call
- * regrows it (synchronising the device), which is refused during graph
- * capture.  A captured graph keeps the workspace address it was captured
- * with, so after capturing a call, make no wider call on the same handle
- * while the graph may still be replayed.  Calls on one handle must not
+ * (device, may be NULL) receive the routes.  Any m: a call wider than
+ * iq_moe_slice_tokens runs as consecutive slices of that many tokens on
+ * `stream`, which gives every token the same bits as one call would.
+ * The handle owns a workspace, sized for one token at create and grown by
+ * iq_moe_reserve or by the widest call so far (up to one slice); growth is
+ * refused during graph capture, so reserve before capturing wider calls.
+ * A grown workspace's old buffer stays allocated until iq_moe_destroy, so
+ * graphs captured earlier stay valid.  Calls on one handle must not
  * overlap in time (they share the workspace); use one handle per stream.
  * Replaces: QuantizedMoeLayer::forward (src/qwen/quantized_moe.rs:227-281)
  * minus the router matmul, whose logits are the input here. */
@@ -292,7 +334,7 @@ int iq_moe_forward_x(iq_moe_t moe, const float *x, int64_t m, const float *resid
 /* iq_moe_forward, also recording events[0..3] (hipEvent_t handles created by
  * the caller) on `stream`: before the routing launch, then after the
  * routing, gate/up and down launches.  Consecutive event pairs time the
- * three kernels.
+ * three kernels.  At most iq_moe_slice_tokens tokens.
  * Replaces: the per-stage QuantizedMoeTimings the reference collects
  * (src/qwen/quantized_moe.rs:67-96, :252-275). */
 int iq_moe_forward_timed(iq_moe_t moe, const float *x, const float *router_logits, int64_t m, float *out,

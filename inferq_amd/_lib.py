@@ -49,6 +49,8 @@ _SIGNATURES = {
     "iq_matmul_noalloc": ([P, P, I64, P, P], INT),
     "iq_matmul_noalloc_max_bytes": ([], SZ),
     "iq_matmul_workspace_size": ([P, I64], SZ),
+    "iq_matmul_reserve": ([P, I64, P], INT),
+    "iq_workspace_release": ([P], INT),
     "iq_matmul_ws": ([P, P, I64, P, P, SZ, P], INT),
     "iq_matmul_host": ([P, P, I64, P], INT),
     "iq_argmax_rows": ([P, I64, I64, P, P, P], INT),
@@ -77,6 +79,8 @@ _SIGNATURES = {
     "iq_experts_layer": ([P, I64, P], INT),
     "iq_moe_create": ([P, ctypes.POINTER(P)], INT),
     "iq_moe_destroy": ([P], INT),
+    "iq_moe_reserve": ([P, I64, P], INT),
+    "iq_moe_slice_tokens": ([P], I64),
     "iq_moe_forward": ([P, P, P, I64, P, P, P, P], INT),
     "iq_moe_forward_x": ([P, P, I64, P, P, P, P, P], INT),
     "iq_moe_forward_timed": ([P, P, P, I64, P, P, P, ctypes.POINTER(P), P], INT),

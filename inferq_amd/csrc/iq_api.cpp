@@ -3,7 +3,9 @@
 // dispatch to the kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
+#include <cstddef>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -58,6 +60,9 @@ struct Workspace {
     hipStream_t stream = nullptr;
     void* p = nullptr;
     size_t bytes = 0;
+    // Buffers this workspace outgrew.  Graphs captured on the stream keep
+    // their addresses, so they stay allocated until iq_workspace_release.
+    std::vector<void*> retired;
 };
 std::vector<Workspace> g_ws;
 
@@ -77,7 +82,7 @@ int WsLease::acquire(size_t bytes, hipStream_t stream) {
     for (Workspace& c : g_ws)
         if (c.device == dev && c.stream == stream) w = &c;
     if (!w) {
-        g_ws.push_back(Workspace{dev, stream, nullptr, 0});
+        g_ws.push_back(Workspace{dev, stream, nullptr, 0, {}});
         w = &g_ws.back();
     }
     if (w->bytes < bytes) {
@@ -87,26 +92,54 @@ int WsLease::acquire(size_t bytes, hipStream_t stream) {
         if (cs != hipStreamCaptureStatusNone)
             return fail(IQ_ERR_INVALID,
                         "the library workspace of this stream must grow to %zu bytes, which cannot happen during "
-                        "graph capture: make one eager call of the same size on the stream first, or pass a "
-                        "workspace (iq_matmul_ws)",
+                        "graph capture: call iq_matmul_reserve (or make one eager call of the same size) on the "
+                        "stream first, or pass a workspace (iq_matmul_ws)",
                         bytes);
-        if (w->p) {
-            e = hipStreamSynchronize(stream);  // earlier work on the stream may still read the old buffer
-            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-            (void)hipFree(w->p);
-            w->p = nullptr;
-            w->bytes = 0;
-        }
+        // at least 1 MiB, and at least double the old size, so that a run of
+        // growing calls retires few buffers
         size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-        e = hipMalloc(&w->p, want);
+        if (w->bytes && want < 2 * w->bytes) want = 2 * w->bytes;
+        void* np = nullptr;
+        e = hipMalloc(&np, want);
         if (e != hipSuccess) {
             (void)hipGetLastError();
-            w->p = nullptr;
-            return fail(IQ_ERR_OOM, "workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+            if (want > bytes) e = hipMalloc(&np, want = bytes);  // doubling may not fit where the need does
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                return fail(IQ_ERR_OOM, "workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+            }
         }
+        // earlier launches (and captured graphs) may still read the old
+        // buffer: it is retired, not freed
+        if (w->p) w->retired.push_back(w->p);
+        w->p = np;
         w->bytes = want;
     }
     p_ = w->p;
+    return IQ_OK;
+}
+
+// Free the workspaces of `stream` on the current device (the live one and
+// every retired one), after the stream's work has finished.
+int release_workspace(hipStream_t stream) {
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    for (size_t i = 0; i < g_ws.size(); i++) {
+        Workspace& w = g_ws[i];
+        if (w.device != dev || w.stream != stream) continue;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(IQ_ERR_INVALID, "a stream's workspace cannot be released during graph capture");
+        e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        if (w.p) (void)hipFree(w.p);
+        for (void* r : w.retired) (void)hipFree(r);
+        g_ws.erase(g_ws.begin() + (std::ptrdiff_t)i);
+        return IQ_OK;
+    }
     return IQ_OK;
 }
 
@@ -220,6 +253,14 @@ size_t matmul_ws_bytes(const iq_weight* w, int64_t m) {
     const size_t d = dense_mfma_workspace_any(view_of(w), m);
     const size_t ap = a > p ? a : p;
     return ap > d ? ap : d;
+}
+
+// Workspace of iq_matmul_argmax: the logits, the argmax partials and the
+// product's own workspace.
+size_t argmax_call_bytes(const iq_weight* w, int64_t m) {
+    const size_t yb = ((size_t)(m * w->rows) * 4 + 255) & ~(size_t)255;
+    const size_t ab = (argmax_workspace_size(m, w->rows) + 255) & ~(size_t)255;
+    return yb + ab + matmul_ws_bytes(w, m);
 }
 
 // Kernel choice of a product (iq_matmul_via's path argument).  Every path
@@ -431,6 +472,18 @@ IQ_API int iq_matmul_noalloc(iq_weight_t w, const float* x, int64_t m, float* y,
 
 IQ_API size_t iq_matmul_noalloc_max_bytes(void) { return kScratchBytes; }
 
+IQ_API int iq_matmul_reserve(iq_weight_t w, int64_t m, iq_stream_t stream) {
+    if (int rc = check_weight(w)) return rc;
+    if (m < 0) return fail(IQ_ERR_SHAPE, "negative input row count %lld", (long long)m);
+    if (m == 0) return IQ_OK;
+    // the widest of the entries that use the stream's workspace for W
+    const size_t need = std::max(matmul_ws_bytes(w, m), m <= 65535 ? argmax_call_bytes(w, m) : 0);
+    WsLease lease;
+    return lease.acquire(need, (hipStream_t)stream);
+}
+
+IQ_API int iq_workspace_release(iq_stream_t stream) { return release_workspace((hipStream_t)stream); }
+
 IQ_API size_t iq_matmul_workspace_size(iq_weight_t w, int64_t m) {
     if (!w || m <= 0) return 0;
     return matmul_ws_bytes(w, m);
@@ -526,7 +579,7 @@ IQ_API int iq_matmul_argmax(iq_weight_t w, const float* x, int64_t m, int32_t* i
     const size_t yb = ((size_t)(m * w->rows) * 4 + 255) & ~(size_t)255;
     const size_t ab = (argmax_workspace_size(m, w->rows) + 255) & ~(size_t)255;
     WsLease lease;
-    if (int rc = lease.acquire(yb + ab + matmul_ws_bytes(w, m), s)) return rc;
+    if (int rc = lease.acquire(argmax_call_bytes(w, m), s)) return rc;
     uint8_t* base = (uint8_t*)lease.ptr();
     float* y = (float*)base;
     hipError_t e = launch_path(w, x, m, y, base + yb + ab, IQ_PATH_AUTO, nullptr, nullptr, s);

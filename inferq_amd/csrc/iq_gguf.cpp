@@ -237,7 +237,8 @@ int parse(iq_gguf* g) {
         if (ti.offset % g->alignment)
             return fail(IQ_ERR_SHAPE, "GGUF tensor %s is not aligned to %llu bytes", ti.name.c_str(),
                         (unsigned long long)g->alignment);
-        ti.offset += g->data_offset;
+        if (__builtin_add_overflow(ti.offset, g->data_offset, &ti.offset))
+            return fail(IQ_ERR_SHAPE, "GGUF tensor %s offset overflows", ti.name.c_str());
         if (ti.offset > g->file_size || ti.nbytes > g->file_size - ti.offset)
             return fail(IQ_ERR_SHAPE, "GGUF tensor %s extends past the end of the file", ti.name.c_str());
     }

@@ -2,7 +2,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <mutex>
+#include <vector>
 
 #include "../../include/iq_qgemm.h"
 #include "iq_api_internal.h"
@@ -25,6 +27,10 @@ struct iq_moe {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     int ws_m = 0;
+    // Workspaces replaced by a larger one.  A graph captured earlier still
+    // holds their addresses, so they stay allocated until the handle is
+    // destroyed.
+    std::vector<void*> retired;
 };
 
 namespace {
@@ -109,6 +115,50 @@ size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
     }
     (void)ctr;
     return off;
+}
+
+// Tokens one set of launches serves: the grouping kernels keep every
+// (token, route) pair of a call on chip (kMoeMaxAssign of them), and the
+// many-token path keeps a bitmask of tokens per expert in 32 KiB of LDS.
+// A wider call runs as consecutive slices of this many tokens; every
+// token's output is independent of the others in its call, so the slices
+// give the same bits as one call would.
+int slice_tokens(const iq_moe* L) {
+    const int64_t by_assign = kMoeMaxAssign / L->layer.K;
+    const int64_t by_mask = 32 * (8192 / std::max<int64_t>(L->layer.E, 1));
+    return (int)std::max<int64_t>(1, std::min(by_assign, by_mask));
+}
+
+// Make the handle's workspace serve calls of m tokens (m <= slice_tokens).
+// Refused during graph capture.  The buffer it replaces is kept until the
+// handle is destroyed, so graphs captured on it stay valid.
+int grow_workspace(iq_moe* L, int m, hipStream_t s, bool at_create = false) {
+    if (L->ws_m >= m) return IQ_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = at_create ? hipSuccess : hipStreamIsCapturing(s, &cs);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(IQ_ERR_INVALID,
+                    "the MoE workspace must grow to %d tokens, which cannot happen during graph capture: call "
+                    "iq_moe_reserve (or make one eager call of at least this many tokens) on the handle first",
+                    m);
+    const size_t bytes = carve(L, m, nullptr, nullptr);
+    void* ws = nullptr;
+    e = hipMalloc(&ws, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(IQ_ERR_OOM, "MoE workspace of %zu bytes: %s", bytes, hipGetErrorString(e));
+    }
+    e = hipMemset(ws, 0, bytes);  // the completion counters start at zero
+    if (e != hipSuccess) {
+        (void)hipFree(ws);
+        return hip_fail(e, "hipMemset");
+    }
+    if (L->ws) L->retired.push_back(L->ws);
+    L->ws = ws;
+    L->ws_bytes = bytes;
+    L->ws_m = m;
+    return IQ_OK;
 }
 
 }  // namespace
@@ -196,64 +246,38 @@ IQ_API int iq_moe_create(const iq_moe_desc* d, iq_moe_t* out) {
     p.d_nbw = (int)(I / block_elems(d->down_dtype));
     L->gfmt = d->gate_dtype;
     L->dfmt = d->down_dtype;
+    // a one-token (decode) call can be captured without an eager call first
+    if (int rc = grow_workspace(L, 1, nullptr, true)) {
+        delete L;
+        return rc;
+    }
     *out = L;
     return IQ_OK;
 }
 
 IQ_API int iq_moe_destroy(iq_moe_t L) {
     if (!L) return IQ_OK;
+    if (L->ws || !L->retired.empty()) (void)hipDeviceSynchronize();  // launches may still read them
     if (L->ws) (void)hipFree(L->ws);
+    for (void* p : L->retired) (void)hipFree(p);
     delete L;
     return IQ_OK;
 }
 
-// logits == nullptr: the layer's router computes them from x.
-static int moe_forward(iq_moe_t L, const float* x, const float* logits, const float* residual, int64_t m,
-                       float* out, int32_t* experts_out, float* weights_out, void* const* events,
-                       iq_stream_t stream) {
+IQ_API int iq_moe_reserve(iq_moe_t L, int64_t max_tokens, iq_stream_t stream) {
     if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
-    if (m < 0) return fail(IQ_ERR_SHAPE, "negative token count");
-    if (m == 0) return IQ_OK;
-    if (!logits && !L->layer.router)
-        return fail(IQ_ERR_INVALID, "this MoE layer has no router: pass router logits (iq_moe_forward)");
-    if (!x || !out) return fail(IQ_ERR_INVALID, "null input or output pointer");
-    if (residual && ((uintptr_t)residual & 15u))
-        return fail(IQ_ERR_INVALID, "the residual must be 16-byte aligned");
-    if (m * L->layer.K > kMoeMaxAssign)
-        return fail(IQ_ERR_RANGE, "%lld tokens x top-%lld exceeds %d assignments per call", (long long)m,
-                    (long long)L->layer.K, kMoeMaxAssign);
-    hipStream_t s = (hipStream_t)stream;
+    if (max_tokens < 0) return fail(IQ_ERR_SHAPE, "negative token count");
     std::lock_guard<std::mutex> lock(L->mu);
-    if (L->ws_m < m) {
-        const size_t bytes = carve(L, (int)m, nullptr, nullptr);
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        hipError_t ce = hipStreamIsCapturing(s, &cs);
-        if (ce != hipSuccess) return hip_fail(ce, "hipStreamIsCapturing");
-        if (cs != hipStreamCaptureStatusNone)
-            return fail(IQ_ERR_INVALID,
-                        "the MoE workspace must grow to %lld tokens, which cannot happen during graph capture: make "
-                        "one eager call of at least this many tokens on the handle first",
-                        (long long)m);
-        if (L->ws) {
-            // the old buffer goes away: the stage hooks must not launch on it
-            L->has_last = false;
-            hipError_t e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-            (void)hipFree(L->ws);
-            L->ws = nullptr;
-            L->ws_m = 0;
-        }
-        hipError_t e = hipMalloc(&L->ws, bytes);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            L->ws = nullptr;
-            return fail(IQ_ERR_OOM, "MoE workspace of %zu bytes: %s", bytes, hipGetErrorString(e));
-        }
-        e = hipMemset(L->ws, 0, bytes);  // the completion counters start at zero
-        if (e != hipSuccess) return hip_fail(e, "hipMemset");
-        L->ws_bytes = bytes;
-        L->ws_m = (int)m;
-    }
+    return grow_workspace(L, (int)std::min<int64_t>(max_tokens, slice_tokens(L)), (hipStream_t)stream);
+}
+
+IQ_API int64_t iq_moe_slice_tokens(iq_moe_t L) { return L ? slice_tokens(L) : 0; }
+
+// One set of launches for m <= slice_tokens(L) tokens (the caller holds
+// L->mu).  logits == nullptr: the layer's router computes them from x.
+static int moe_slice(iq_moe_t L, const float* x, const float* logits, const float* residual, int64_t m, float* out,
+                     int32_t* experts_out, float* weights_out, void* const* events, hipStream_t s) {
+    if (int rc = grow_workspace(L, (int)m, s)) return rc;
     MoeParams p = L->layer;
     carve(L, L->ws_m, (uint8_t*)L->ws, &p);
     // carve() sized the views for ws_m tokens; the call uses m
@@ -299,6 +323,38 @@ static int moe_forward(iq_moe_t L, const float* x, const float* logits, const fl
         return hip_fail(e, "hipMemcpyAsync (experts)");
     if (weights_out && (e = hipMemcpyAsync(weights_out, p.weights, rb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
         return hip_fail(e, "hipMemcpyAsync (weights)");
+    return IQ_OK;
+}
+
+// A call of any width: consecutive slices of at most slice_tokens(L)
+// tokens, each a complete set of launches on `stream`.
+static int moe_forward(iq_moe_t L, const float* x, const float* logits, const float* residual, int64_t m,
+                       float* out, int32_t* experts_out, float* weights_out, void* const* events,
+                       iq_stream_t stream) {
+    if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
+    if (m < 0) return fail(IQ_ERR_SHAPE, "negative token count");
+    if (m == 0) return IQ_OK;
+    if (!logits && !L->layer.router)
+        return fail(IQ_ERR_INVALID, "this MoE layer has no router: pass router logits (iq_moe_forward)");
+    if (!x || !out) return fail(IQ_ERR_INVALID, "null input or output pointer");
+    if (residual && ((uintptr_t)residual & 15u))
+        return fail(IQ_ERR_INVALID, "the residual must be 16-byte aligned");
+    if (m > INT32_MAX / std::max<int64_t>(L->layer.K, 1))
+        return fail(IQ_ERR_RANGE, "%lld tokens is more than a call can route", (long long)m);
+    const int64_t slice = slice_tokens(L);
+    if (events && m > slice)
+        return fail(IQ_ERR_RANGE, "timed MoE calls cover at most %lld tokens (got %lld)", (long long)slice,
+                    (long long)m);
+    hipStream_t s = (hipStream_t)stream;
+    std::lock_guard<std::mutex> lock(L->mu);
+    const int64_t H = L->layer.H, E = L->layer.E, K = L->layer.K;
+    for (int64_t t0 = 0; t0 < m; t0 += slice) {
+        const int64_t n = std::min(slice, m - t0);
+        if (int rc = moe_slice(L, x + t0 * H, logits ? logits + t0 * E : nullptr, residual ? residual + t0 * H : nullptr,
+                               n, out + t0 * H, experts_out ? experts_out + t0 * K : nullptr,
+                               weights_out ? weights_out + t0 * K : nullptr, events, s))
+            return rc;
+    }
     return IQ_OK;
 }
 

@@ -119,6 +119,17 @@ class QuantizedMoeLayer:
                 raise QgemmError(_lib.IQ_ERR_INVALID, f"MoE {name} must be a tensor on cuda:{self.device} "
                                                       f"(got {t.device})")
 
+    def reserve(self, max_tokens: int) -> None:
+        """Size the layer's workspace for calls of up to max_tokens tokens
+        (iq_moe_reserve): such calls can then be captured into a graph
+        without an eager call first."""
+        check(lib().iq_moe_reserve(self._h, int(max_tokens), _stream()))
+
+    def slice_tokens(self) -> int:
+        """Tokens one set of the layer's launches serves (iq_moe_slice_tokens);
+        wider calls run as consecutive slices."""
+        return int(lib().iq_moe_slice_tokens(self._h))
+
     def forward_into(self, xs, router_logits, out, experts=None, weights=None) -> None:
         """Raw call: device f32 xs [m, hidden], logits [m, n_experts], out [m, hidden]."""
         self._check_device(xs=xs, router_logits=router_logits, out=out, experts=experts, weights=weights)

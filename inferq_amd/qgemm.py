@@ -171,6 +171,13 @@ class QuantizedMatrix:
         check(lib().iq_matmul_argmax(self._h, xs.data_ptr(), m, idx.data_ptr(), val.data_ptr(), _stream()))
         return idx, val
 
+    def reserve(self, input_rows: int) -> None:
+        """Size the current stream's library workspace for products of up to
+        `input_rows` rows of this matrix (iq_matmul_reserve), so that they
+        can be captured into a graph without an eager call first."""
+        _ensure_init()
+        check(lib().iq_matmul_reserve(self._h, int(input_rows), _stream()))
+
     def forward_into(self, x, y, path: int = 0) -> None:
         """Raw call: contiguous device f32 x [m, cols] into y [m, rows]
         (`path` as forward_via; 0 = the dispatch)."""
@@ -250,6 +257,12 @@ def row_kernel(dtype: int, weight_row, inputs_block_major, rows: int) -> np.ndar
     check(getattr(lib(), fn)(w.ctypes.data, w.size // BLOCK_BYTES[dtype], x.ctypes.data, x.size // ib, rows,
                              out.ctypes.data, rows))
     return out
+
+
+def release_workspace() -> None:
+    """Free the current stream's library workspace (iq_workspace_release)."""
+    _ensure_init()
+    check(lib().iq_workspace_release(_stream()))
 
 
 def argmax(logits):

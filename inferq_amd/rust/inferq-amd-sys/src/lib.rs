@@ -97,6 +97,8 @@ extern "C" {
     pub fn iq_matmul_noalloc(w: iq_weight_t, x: *const f32, m: i64, y: *mut f32, stream: iq_stream_t) -> c_int;
     pub fn iq_matmul_noalloc_max_bytes() -> usize;
     pub fn iq_matmul_workspace_size(w: iq_weight_t, m: i64) -> usize;
+    pub fn iq_matmul_reserve(w: iq_weight_t, m: i64, stream: iq_stream_t) -> c_int;
+    pub fn iq_workspace_release(stream: iq_stream_t) -> c_int;
     pub fn iq_matmul_ws(w: iq_weight_t, x: *const f32, m: i64, y: *mut f32, ws: *mut c_void, ws_bytes: usize,
                         stream: iq_stream_t) -> c_int;
     pub fn iq_matmul_host(w: iq_weight_t, x: *const f32, m: i64, y: *mut f32) -> c_int;
@@ -121,6 +123,8 @@ extern "C" {
 
     pub fn iq_moe_create(d: *const iq_moe_desc, out: *mut iq_moe_t) -> c_int;
     pub fn iq_moe_destroy(l: iq_moe_t) -> c_int;
+    pub fn iq_moe_reserve(l: iq_moe_t, max_tokens: i64, stream: iq_stream_t) -> c_int;
+    pub fn iq_moe_slice_tokens(l: iq_moe_t) -> i64;
     pub fn iq_moe_forward(l: iq_moe_t, x: *const f32, logits: *const f32, m: i64, out: *mut f32,
                           experts: *mut i32, weights: *mut f32, stream: iq_stream_t) -> c_int;
     pub fn iq_moe_forward_x(l: iq_moe_t, x: *const f32, m: i64, residual: *const f32, out: *mut f32,
@@ -226,6 +230,13 @@ impl GpuMatrix {
         check(iq_matmul(self.0, x, m as i64, y, stream))
     }
 
+    /// Size the library workspace of `stream` for up to `m` input rows of
+    /// this matrix, so that a graph can capture such calls without an eager
+    /// call first.
+    pub fn reserve(&self, m: usize, stream: iq_stream_t) -> anyhow::Result<()> {
+        check(unsafe { iq_matmul_reserve(self.0, m as i64, stream) })
+    }
+
     /// concatenate_rows (src/gguf.rs:379-404).
     pub fn concatenate_rows(&self, other: &GpuMatrix) -> anyhow::Result<Self> {
         let mut h: iq_weight_t = std::ptr::null_mut();
@@ -314,6 +325,12 @@ impl Moe {
         let mut h: iq_moe_t = std::ptr::null_mut();
         check(unsafe { iq_moe_create(desc, &mut h) })?;
         Ok(Self(h))
+    }
+
+    /// Size the workspace for calls of up to `max_tokens` tokens, so that a
+    /// graph can capture them without an eager call first.
+    pub fn reserve(&self, max_tokens: usize, stream: iq_stream_t) -> anyhow::Result<()> {
+        check(unsafe { iq_moe_reserve(self.0, max_tokens as i64, stream) })
     }
 
     /// forward (src/qwen/quantized_moe.rs:227-281) with the router on the GPU

@@ -100,6 +100,13 @@ def test_malformed_files_are_refused(tmp_path):
     raw[i:i + 8] = struct.pack("<Q", 256 * 64)  # tensor runs past the end of the file
     open(p, "wb").write(bytes(raw))
     _expect_refused(p, "past the end of the file")
+    raw[i:i + 8] = struct.pack("<Q", 256)
+    # an aligned offset that wraps past 2^64 onto the header once the data
+    # start is added: refused, not read as tensor bytes
+    data_start = W.write_gguf(p, [("t", W.GGML_Q4_K, [2, 256], blocks)])["t"]
+    raw[i + 20:i + 28] = struct.pack("<Q", (1 << 64) - data_start)  # after the u32 type: the u64 offset
+    open(p, "wb").write(bytes(raw))
+    _expect_refused(p, "offset overflows")
 
 
 def test_library_exports_the_gguf_entries():

@@ -482,3 +482,27 @@ def test_random_layers_match_oracle(gpu, oracle):
         what = f"case {case}: E={E} K={K} shared={shared} {_NAMES[g]}/{_NAMES[d]} m={m}"
         assert [r.experts for r in out.routes] == ref_e.tolist(), what
         assert_close_normwise(out.hidden.cpu().numpy(), ref, 1e-4, what)
+
+
+def test_reference_prefill_pass_512_tokens_top10(gpu, oracle, wide_router_layer):
+    """The reference's prefill pass on its first model: 512 rows
+    (src/runtime.rs:44) routed top-10 of 512 experts (Qwen3-Coder-Next,
+    docs/execution-path.md:20), 5,120 assignments in one call.  The call
+    runs as slices of iq_moe_slice_tokens tokens; routes equal the
+    oracle's, outputs within 1e-4 (shared expert), and the 512-token call
+    equals two 256-token calls bitwise."""
+    moe, _ = _device_layer(wide_router_layer, 10, gpu)
+    assert moe.slice_tokens() < 512
+    rng = np.random.default_rng(5120)
+    x = S.normal((512, 2048), rng)
+    logits = S.normal((512, 512), rng)
+    xg, lg = torch.from_numpy(x).to(gpu), torch.from_numpy(logits).to(gpu)
+    out = moe.forward(xg, lg)
+    ref, ref_e, ref_w = oracle.moe_forward(_oracle_layer(wide_router_layer, 10), x, logits, mode=1,
+                                           impl=_impl(oracle), nthreads=8)
+    assert [r.experts for r in out.routes] == ref_e.tolist()
+    assert_close_normwise(np.array([r.weights for r in out.routes]), ref_w, 1e-6, "route weights")
+    got = out.hidden.cpu().numpy()
+    assert_close_normwise(got, ref, 1e-4, "512-token top-10 prefill pass")
+    halves = np.concatenate([moe.forward(xg[i:i + 256], lg[i:i + 256]).hidden.cpu().numpy() for i in (0, 256)])
+    assert_bitexact(got, halves, "512-token call vs two 256-token calls")
