@@ -45,6 +45,22 @@ def test_prefill_widths_bitexact_by_default(gpu, oracle, dtype, rows, cols):
         assert_bitexact(got, expected, f"{S.NAMES[dtype]} [{rows}x{cols}] m={m}")
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [(Q4, 8192, 2048), (Q4, 2048, 4096), (Q6, 8192, 2048)],
+                         ids=["q4k_8192x2048", "q4k_2048x4096", "q6k_8192x2048"])
+def test_prefill_full_size_bitexact_by_default(gpu, oracle, dtype, rows, cols):
+    """The BASELINE prefill shapes at full size through the dispatch: [256 x
+    2048] -> 8192 and [256 x 4096] -> 2048 (Q4_K), and the Q6_K [256 x 2048]
+    -> 8192, on the grid the default call launches, against the threaded
+    oracle, bit for bit."""
+    rng = np.random.default_rng(rows + cols + dtype)
+    w = S.random_matrix(dtype, rows, cols, rng)
+    mat = Q.QuantizedMatrix.upload(w, dtype, rows, cols)
+    x = S.normal((256, cols), np.random.default_rng(4096 + rows))
+    expected = oracle.matmul(dtype, w, rows, cols, x, impl=1 if oracle.have_avx2() else 0, nthreads=8)
+    got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    assert_bitexact(got, expected, f"{S.NAMES[dtype]} [256 x {cols}] -> {rows}")
+
+
 @pytest.mark.parametrize("dtype", [Q4, Q6, Q8], ids=["q4k", "q6k", "q80"])
 def test_prefill_rows_equal_one_row_calls(gpu, dtype):
     """256 rows in one call equal 256 one-row calls bitwise: prefill never

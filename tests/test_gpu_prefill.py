@@ -54,11 +54,12 @@ def test_prefill_block_integers_exact(gpu, oracle, rows, cols, m, sample):
     _rowwise_close(y.cpu().numpy(), oracle.matmul(Q4, w, rows, cols, x, nthreads=8), 1e-4, "prefill product")
 
 
-@pytest.mark.parametrize("rows,cols,m", [(1024, 2048, 256), (2048, 4096, 256), (300, 2048, 100), (64, 256, 64)])
+@pytest.mark.parametrize("rows,cols,m", [(8192, 2048, 256), (1024, 2048, 256), (2048, 4096, 256), (300, 2048, 100),
+                                         (64, 256, 64)])
 def test_prefill_matches_oracle(gpu, oracle, rows, cols, m):
-    """BASELINE configs[3] shapes scaled to what the oracle computes in
-    seconds ([2048 x 4096] at 256 rows: 256 unsplit small tiles; [1024 x
-    2048]: small tiles split over K), ragged sizes."""
+    """BASELINE configs[3] shapes: [256 x 2048] -> 8192 at full size (256
+    large tiles) and [256 x 4096] -> 2048 (256 unsplit small tiles);
+    [1024 x 2048] (small tiles split over K) and ragged sizes."""
     rng = np.random.default_rng(rows + cols + m)
     w = S.random_matrix(Q4, rows, cols, rng)
     x = S.normal((m, cols), rng)
