@@ -92,6 +92,28 @@ __device__ __forceinline__ uint32_t ml_lds_win(const uint8_t* row, int sh, int o
     return __builtin_amdgcn_alignbyte(w1, w0, (uint32_t)sh);
 }
 
+// N consecutive windows of ml_lds_win: out[i] = the 4 bytes at byte offset
+// o + 4 i (o 16-byte aligned) of a block staged with shift sh, from N + 1
+// dwords read as 16-byte (and one 4-byte) LDS accesses, which spread the
+// lanes of a fragment over the banks where per-window 4-byte reads would
+// pile up to four lanes on a bank.
+template <int N>
+__device__ __forceinline__ void ml_lds_span(const uint8_t* row, int sh, int o, uint32_t (&out)[N]) {
+    static_assert(N % 4 == 0, "span of whole 16-byte groups");
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int i = 0; i < N / 4; i++) {
+        const u32x4a16 v = *(const u32x4a16*)(row + o + 16 * i);
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+    }
+    w[N] = *(const uint32_t*)(row + o + 4 * N);
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], (uint32_t)sh);
+}
+
 // Operands of one tile.  Activation row rr (0 .. 16 RT - 1) of the tile is
 // row arow(rr) of aq (Q8K in the lane-transposed layout, ldq bytes a row),
 // ad (block scales, ldd a row) and hs ([row][nb][16] f16 16-value sums,
@@ -217,6 +239,14 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
         uint32_t s6a = 0, s6b = 0;  // Q4_K: six-bit scales of sub-blocks 2q, 2q+1
         uint32_t q6s = 0;           // Q6_K: scale bytes 4q..4q+3
         Q4Scales sc{};
+        // Q4_K: the lane's qs bytes 32q .. 32q + 31 (dword k for reference
+        // lane k), read as two 16-byte LDS accesses per block: the
+        // columns' 144-byte stride puts 16 lanes' 16-byte groups on 16
+        // distinct bank groups, where eight 4-byte reads per block would
+        // put four lanes on each bank
+        u32x4a16 qs4[2] = {};
+        // Q6_K: the lane's ql and qh windows for reference lanes k = 0..7
+        uint32_t l0s[8] = {}, l1s[8] = {}, qhs[8] = {};
         if constexpr (FMT == kQ4_K) {
             const u32x4a16 hdr = *(const u32x4a16*)bcol;
             xd = f16_to_f32(hdr.x);
@@ -225,9 +255,14 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
             const uint32_t sw = q < 2 ? sc.sc_lo : sc.sc_hi;
             s6a = byte_of(sw, 2 * (q & 1));
             s6b = byte_of(sw, 2 * (q & 1) + 1);
+            qs4[0] = *(const u32x4a16*)(bcol + 16 + 32 * q);
+            qs4[1] = *(const u32x4a16*)(bcol + 32 + 32 * q);
         } else {
             xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
             q6s = ml_lds_win(bcol, sh, 192 + 4 * q);
+            ml_lds_span<8>(bcol, sh, 64 * (q >> 1), l0s);
+            ml_lds_span<8>(bcol, sh, 64 * (q >> 1) + 32, l1s);
+            ml_lds_span<8>(bcol, sh, 128 + 32 * (q >> 1), qhs);
         }
 #pragma unroll
         for (int r = 0; r < 4 * RT; r++) {
@@ -240,7 +275,7 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
             uint32_t w1[2], w2[2];
             int mul;  // isum = mul * (stream 1) + (stream 2)
             if constexpr (FMT == kQ4_K) {
-                const uint32_t qd = *(const uint32_t*)(bcol + 16 + 32 * q + 4 * k);
+                const uint32_t qd = qs4[k >> 2][k & 3];
                 const uint32_t lo = qd & 0x0f0f0f0fu, hi = (qd >> 4) & 0x0f0f0f0fu;
                 w1[0] = bytes_mul_small(lo, s6a >> 3);
                 w1[1] = bytes_mul_small(hi, s6b >> 3);
@@ -249,9 +284,7 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
                 mul = 8;
             } else {
                 const int hk = k >= 4;
-                const int qo = 64 * (q >> 1) + 4 * k;
-                const uint32_t l0 = ml_lds_win(bcol, sh, qo), l1 = ml_lds_win(bcol, sh, qo + 32);
-                const uint32_t qh = ml_lds_win(bcol, sh, 128 + 32 * (q >> 1) + 4 * k);
+                const uint32_t l0 = l0s[k], l1 = l1s[k], qh = qhs[k];
 #pragma unroll
                 for (int cc = 0; cc < 2; cc++) {
                     const uint32_t l = cc ? l1 : l0;
@@ -354,14 +387,25 @@ __device__ __forceinline__ void ml_pk_block(const uint8_t* bcol, int sh, const u
     Q4Scales sc{};
     uint32_t s6w = 0;         // Q4_K: six-bit scales of sub-blocks 4h .. 4h+3
     s16x2_ml q6m[4], q6c[4];  // Q6_K: (sc, sc), (128 - 32 sc, ...) of chunks 4h + cc
+    // Q4_K: the lane's qs dwords 4 upper + p (p = 0..3) of the 32-byte rows
+    // 2h and 2h + 1, as two 16-byte LDS reads per block (conflict-free over
+    // the 144-byte column stride; four-byte reads put four lanes per bank)
+    u32x4a16 qp[2] = {};
+    // Q6_K: the lane's ql (rows 64 h, 64 h + 32) and qh windows, p = 0..3
+    uint32_t las[4] = {}, lbs[4] = {}, qhs[4] = {};
     if constexpr (FMT == kQ4_K) {
         const u32x4a16 hdr = *(const u32x4a16*)bcol;
         xd = f16_to_f32(hdr.x);
         xdm = f16_to_f32(hdr.x >> 16);
         sc = q4_scales(hdr.y, hdr.z, hdr.w);
         s6w = h ? sc.sc_hi : sc.sc_lo;
+        qp[0] = *(const u32x4a16*)(bcol + 16 + 64 * h + 16 * upper);
+        qp[1] = *(const u32x4a16*)(bcol + 16 + 64 * h + 32 + 16 * upper);
     } else {
         xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
+        ml_lds_span<4>(bcol, sh, 64 * h + 16 * upper, las);
+        ml_lds_span<4>(bcol, sh, 64 * h + 32 + 16 * upper, lbs);
+        ml_lds_span<4>(bcol, sh, 128 + 32 * h + 16 * upper, qhs);
         // scales 2c + upper of chunks c = 4h + cc: bytes upper, 2 + upper of two dwords
         const uint32_t w0 = ml_lds_win(bcol, sh, 192 + 8 * h) >> (8 * upper);
         const uint32_t w1 = ml_lds_win(bcol, sh, 196 + 8 * h) >> (8 * upper);
@@ -385,8 +429,7 @@ __device__ __forceinline__ void ml_pk_block(const uint8_t* bcol, int sh, const u
         int mul;  // isum = mul * (stream 1) + (stream 2)
         if constexpr (FMT == kQ4_K) {
             // sub-blocks 4h + cc: qs dword at 16 + 32 (2h + cc / 2) + 4 kq, nibble cc % 2
-            const uint32_t qd0 = *(const uint32_t*)(bcol + 16 + 64 * h + 4 * kq);
-            const uint32_t qd1 = *(const uint32_t*)(bcol + 16 + 64 * h + 32 + 4 * kq);
+            const uint32_t qd0 = qp[0][p], qd1 = qp[1][p];
 #pragma unroll
             for (int cc = 0; cc < 4; cc++) {
                 const uint32_t qd = cc < 2 ? qd0 : qd1;
@@ -399,9 +442,7 @@ __device__ __forceinline__ void ml_pk_block(const uint8_t* bcol, int sh, const u
         } else {
             // chunk c = 4h + cc: ql dword at 64 h + 32 (cc % 2) + 4 kq, the high
             // nibbles for cc >= 2; qh dword at 128 + 32 h + 4 kq, bits 2 cc
-            const uint32_t la = ml_lds_win(bcol, sh, 64 * h + 4 * kq);
-            const uint32_t lb = ml_lds_win(bcol, sh, 64 * h + 32 + 4 * kq);
-            const uint32_t qh = ml_lds_win(bcol, sh, 128 + 32 * h + 4 * kq);
+            const uint32_t la = las[p], lb = lbs[p], qh = qhs[p];
 #pragma unroll
             for (int cc = 0; cc < 4; cc++) {
                 const uint32_t l = (cc & 1) ? lb : la;
