@@ -748,12 +748,30 @@ def decode_sweep(args, hip, device, layers):
     return res
 
 
-def prefill_moe(args, hip, stream, device, layers, cpu=None, chk=None):
+def prefill_moe(args, hip, stream, device, layers, cpu=None, chk=None, tiles=False):
     """BASELINE configs[3], MoE part: 256 tokens, top-8 of 256 experts with
     Dirichlet(0.3) router skew, plus the shared expert.  TOPS counts the
     expert products actually routed: 2 * (rows routed + 256 shared) * 3 * I
     * H.  The checker and the CPU leg run layer chk[0] grouped by expert
-    (routed_grouped_by_expert, src/qwen/quantized_moe.rs:336-406)."""
+    (routed_grouped_by_expert, src/qwen/quantized_moe.rs:336-406).
+    tiles: the handles' down products in tile order (iq_moe_set_path with
+    IQ_PATH_PREFILL_TILES; within 1e-4, not bitwise)."""
+    import torch
+
+    from inferq_amd import _lib
+
+    if tiles:
+        for lay in layers:
+            lay[0].set_path(_lib.PATH_PREFILL_TILES)
+    try:
+        return _prefill_moe(args, hip, device, layers, cpu, chk, tiles)
+    finally:
+        if tiles:
+            for lay in layers:
+                lay[0].set_path(_lib.PATH_AUTO)
+
+
+def _prefill_moe(args, hip, device, layers, cpu, chk, tiles):
     import torch
 
     n = len(layers)
@@ -779,8 +797,8 @@ def prefill_moe(args, hip, stream, device, layers, cpu=None, chk=None):
         ref = cpu.moe(hl, xh, lh, 1)
         kw = dict(diff=max_abs_diff(got, ref), rel=normwise(got, ref), bitexact=bit_fraction(got, ref), cpu=cpu.time_moe(hl, xh, lh, 1))
     line = measurement(f"MoE layer ({E} experts, top-{TOPK} + shared), Dirichlet(0.3) routing",
-                       "Q4_K gate/up, Q6_K down", E * I, H, int((uniq + 1) * (gu + dn)), m, t, "gpu:grouped",
-                       **kw)
+                       "Q4_K gate/up, Q6_K down", E * I, H, int((uniq + 1) * (gu + dn)), m, t,
+                       "gpu:grouped, down in tile order" if tiles else "gpu:grouped", **kw)
     line.update(unique_experts=round(uniq, 1), TOPS=round(tops, 1), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
     return line
 
@@ -849,7 +867,8 @@ def main():
     out = torch.empty(1, H, device=device)
 
     if args.only == "moe_prefill":
-        print(json.dumps({"only": args.only, "result": prefill_moe(args, hip, stream, device, layers)}), flush=True)
+        print(json.dumps({"only": args.only, "result": prefill_moe(args, hip, stream, device, layers),
+                          "tiles": prefill_moe(args, hip, stream, device, layers, tiles=True)}), flush=True)
         return
     if args.only == "decode_sweep":
         print(json.dumps({"only": args.only, "result": decode_sweep(args, hip, device, layers)}), flush=True)
@@ -971,6 +990,8 @@ def main():
         result["extra"] = secondary(args, hip, stream, device, layers, cpu, chk)
         result["extra"]["prefill_int8_tops"] = prefill(args, hip, stream, device, cpu)
         result["extra"]["prefill_moe_m256_dirichlet"] = prefill_moe(args, hip, stream, device, layers, cpu, chk)
+        result["extra"]["prefill_moe_m256_dirichlet_tiles"] = prefill_moe(args, hip, stream, device, layers, cpu, chk,
+                                                                           tiles=True)
         result["extra"]["decode_step_sweep"] = decode_sweep(args, hip, device, layers)
         log(f"secondary: {result['extra']}")
 

@@ -17,8 +17,9 @@
  *   - Results are deterministic and do not depend on the row count.  For
  *     Q4_K, Q6_K and Q8_0 matrices they are bit-identical to the
  *     reference's CPU kernels for the same inputs, on every entry except
- *     iq_matmul_via(..., IQ_PATH_PREFILL_TILES, ...), which a caller must
- *     request explicitly (its f32 order differs; within 1e-4).  Three f32
+ *     iq_matmul_via(..., IQ_PATH_PREFILL_TILES, ...) and MoE handles set to
+ *     IQ_PATH_PREFILL_TILES (iq_moe_set_path), which a caller must request
+ *     explicitly (their f32 order differs; within 1e-4).  Three f32
  *     orders follow a published or fixed order that the reference's own
  *     code (candle's, absent here) could not be checked against, so they
  *     are bit-identical to this library's CPU restatement and within 1e-4
@@ -298,6 +299,20 @@ int iq_moe_reserve(iq_moe_t moe, int64_t max_tokens, iq_stream_t stream);
 /* Tokens one set of the layer's launches serves (wider calls are sliced):
  * 4096 / top_k, and at most 32 * (8192 / n_experts). */
 int64_t iq_moe_slice_tokens(iq_moe_t moe);
+
+/* Choose how the handle's grouped (many-token) calls form the down
+ * products: IQ_PATH_AUTO (the default) keeps the reference's per-lane f32
+ * order, so every token's output is bit-identical to a one-token call and
+ * to the reference; IQ_PATH_PREFILL_TILES forms them in tile order on
+ * chunks of up to 32 rows of one expert (exact per-block integers, one f32
+ * step per output and block), within 1e-4 of the reference and NOT
+ * bitwise.  Gate/up stay in the exact order on both (their SwiGLU rows are
+ * quantised again), and so do calls on the token-major path (up to 32
+ * tokens at the reference's shapes).  Any other path is IQ_ERR_INVALID.
+ * Replaces: the path choice the reference offers for matrix products
+ * (MultiRowPath, src/gguf.rs:43-62), applied to the expert products of
+ * QuantizedMoeLayer::forward (src/qwen/quantized_moe.rs:336-406). */
+int iq_moe_set_path(iq_moe_t moe, int path);
 
 /* out[m x hidden] = MoE(x[m x hidden]) for device x, router logits
  * [m x n_experts] and out.  Routing is softmax, top-k by probability,

@@ -81,6 +81,7 @@ _SIGNATURES = {
     "iq_moe_destroy": ([P], INT),
     "iq_moe_reserve": ([P, I64, P], INT),
     "iq_moe_slice_tokens": ([P], I64),
+    "iq_moe_set_path": ([P, INT], INT),
     "iq_moe_forward": ([P, P, P, I64, P, P, P, P], INT),
     "iq_moe_forward_x": ([P, P, I64, P, P, P, P, P], INT),
     "iq_moe_forward_timed": ([P, P, P, I64, P, P, P, ctypes.POINTER(P), P], INT),

@@ -747,4 +747,226 @@ __device__ __forceinline__ void ml_product_sk(const MlOperands& op, ARow arow, B
     if (wave == NW - 1) ml_pk_finish<FMT>(acc, accm, v);
 }
 
+// ---- tile order: one f32 step per output and block ------------------------
+//
+// For products whose outputs are not quantised again (the grouped MoE down
+// products, on request): the block's whole integer isum (the sum of the
+// eight reference lanes' integers) on v_mfma_i32_16x16x64_i8, then one
+// step out += y.d (x.d isum - x.dmin msum) per output and block.  The
+// per-block integers are exact; the f32 order is one chain per output
+// instead of eight lane chains joined by hsum_f32_8, a few ulps apart.
+//
+// K chunk of step p (0..3) for lane group q (h = q & 1, upper = q >> 1):
+// the activation dwords (c, k), k = p + 4 upper, c = 4 h .. 4 h + 3, which
+// the activation layout keeps as the 16 bytes at 32 k + 16 h; B carries the
+// same four weight dwords with their scales folded in, decoded as in the
+// pair-lane tile (ml_pk_block).  Over the four steps and lane groups the
+// chunks cover the block once, and one decoded B fragment serves every
+// 16-row tile.
+
+// One block: o[t][r] += output (row 16 t + 4 q + r, column j) for the RT
+// tiles.  Operands in LDS: A the block's activation rows at stride kMlAS,
+// bcol this lane's weight row staged as in ml_product (Q6_K: the dword
+// window at shift sh), D the rows' block scales, H their 16-value sums
+// (Q4_K, 32 bytes a row).
+template <int FMT, int RT>
+__device__ __forceinline__ void ml_tile_block(const uint8_t* A, const uint8_t* bcol, const float* D,
+                                              const uint8_t* H, int sh, int q, int jj, float (&o)[RT][4]) {
+    const int h = q & 1, upper = q >> 1;
+    float xd, xdm = 0.f;
+    Q4Scales sc{};
+    uint32_t s6w = 0;
+    s16x2_ml q6m[4], q6c[4];
+    u32x4a16 qp[2] = {};
+    uint32_t las[4] = {}, lbs[4] = {}, qhs[4] = {};
+    if constexpr (FMT == kQ4_K) {
+        const u32x4a16 hdr = *(const u32x4a16*)bcol;
+        xd = f16_to_f32(hdr.x);
+        xdm = f16_to_f32(hdr.x >> 16);
+        sc = q4_scales(hdr.y, hdr.z, hdr.w);
+        s6w = h ? sc.sc_hi : sc.sc_lo;
+        qp[0] = *(const u32x4a16*)(bcol + 16 + 64 * h + 16 * upper);
+        qp[1] = *(const u32x4a16*)(bcol + 16 + 64 * h + 32 + 16 * upper);
+    } else {
+        xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
+        ml_lds_span<4>(bcol, sh, 64 * h + 16 * upper, las);
+        ml_lds_span<4>(bcol, sh, 64 * h + 32 + 16 * upper, lbs);
+        ml_lds_span<4>(bcol, sh, 128 + 32 * h + 16 * upper, qhs);
+        const uint32_t w0 = ml_lds_win(bcol, sh, 192 + 8 * h) >> (8 * upper);
+        const uint32_t w1 = ml_lds_win(bcol, sh, 196 + 8 * h) >> (8 * upper);
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const int scv = (int)(int8_t)(uint8_t)((cc < 2 ? w0 : w1) >> (16 * (cc & 1)));
+            q6m[cc] = s16x2_ml{(short)scv, (short)scv};
+            q6c[cc] = s16x2_ml{(short)(128 - 32 * scv), (short)(128 - 32 * scv)};
+        }
+    }
+    v4i_ml i1[RT], i2[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) i1[t] = i2[t] = v4i_ml{0, 0, 0, 0};
+    constexpr int mul = FMT == kQ4_K ? 8 : 256;  // isum = mul * (stream 1) + (stream 2)
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        uint32_t w1[4], w2[4];
+        if constexpr (FMT == kQ4_K) {
+            const uint32_t qd0 = qp[0][p], qd1 = qp[1][p];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const uint32_t qd = cc < 2 ? qd0 : qd1;
+                const uint32_t nib = (cc & 1) ? ((qd >> 4) & 0x0f0f0f0fu) : (qd & 0x0f0f0f0fu);
+                const uint32_t s6 = byte_of(s6w, cc);
+                w1[cc] = bytes_mul_small(nib, s6 >> 3);
+                w2[cc] = bytes_mul_small(nib, s6 & 7u);
+            }
+        } else {
+            const uint32_t la = las[p], lb = lbs[p], qh = qhs[p];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const uint32_t l = (cc & 1) ? lb : la;
+                const uint32_t lo4 = (cc & 2) ? ((l >> 4) & 0x0f0f0f0fu) : (l & 0x0f0f0f0fu);
+                const uint32_t u = lo4 | (((qh >> (2 * cc)) & 0x03030303u) << 4);
+                const s16x2_ml u02 = __builtin_bit_cast(s16x2_ml, u & 0x00ff00ffu);
+                const s16x2_ml u13 = __builtin_bit_cast(s16x2_ml, __builtin_amdgcn_perm(0u, u, 0x0c030c01u));
+                const uint32_t p02 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u02 * q6m[cc] + q6c[cc]));
+                const uint32_t p13 = __builtin_bit_cast(uint32_t, (s16x2_ml)(u13 * q6m[cc] + q6c[cc]));
+                w1[cc] = __builtin_amdgcn_perm(p13, p02, 0x07030501u);
+                w2[cc] = __builtin_amdgcn_perm(p13, p02, 0x06020400u) ^ 0x80808080u;
+            }
+        }
+        const v4i_ml b1 = {(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+        const v4i_ml b2 = {(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            const v4i_ml a = *(const v4i_ml*)(A + (16 * t + jj) * kMlAS + 32 * (p + 4 * upper) + 16 * h);
+            i1[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b1, i1[t], 0, 0, 0);
+            i2[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b2, i2[t], 0, 0, 0);
+        }
+    }
+    // Q4_K mins: msum = sum over the 16-value sums s of m_{s/2} bsum16_s
+    // (lane group q: sums 4 q .. 4 q + 3, mins m_2q, m_2q+1), integers
+    // below 2^24 in the f16 MFMA's f32 result
+    v4h_ml bm = {};
+    if constexpr (FMT == kQ4_K) {
+        const uint32_t mw = q < 2 ? sc.mn_lo : sc.mn_hi;
+        const _Float16 mA = (_Float16)(float)byte_of(mw, 2 * (q & 1));
+        const _Float16 mB = (_Float16)(float)byte_of(mw, 2 * (q & 1) + 1);
+        bm = v4h_ml{mA, mA, mB, mB};
+    }
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const f32x4 yd = *(const f32x4*)(D + 16 * t + 4 * q);
+        v4f_ml ms = {};
+        if constexpr (FMT == kQ4_K) {
+            const v4h_ml am = *(const v4h_ml*)(H + (16 * t + jj) * 32 + 8 * q);
+            ms = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, v4f_ml{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+        const float ydr[4] = {yd.x, yd.y, yd.z, yd.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float isum = (float)(i1[t][r] * mul + i2[t][r]);
+            if constexpr (FMT == kQ4_K)
+                o[t][r] = __builtin_fmaf(ydr[r], __builtin_fmaf(-xdm, ms[r], xd * isum), o[t][r]);
+            else
+                o[t][r] = __builtin_fmaf(ydr[r] * xd, isum, o[t][r]);
+        }
+    }
+}
+
+// NT 16-row tiles x 64 weight rows on a 256-thread workgroup, in a stage of
+// RT >= NT tiles staged as in ml_product (rows past 16 NT are not loaded);
+// lane (q, j) of wave w ends with v[4 t + r] = output (row 16 t + 4 q + r,
+// weight row 16 w + j), t < NT.
+template <int FMT, int RT, int NT, class ARow, class BRow>
+__device__ __forceinline__ void ml_product_tiles(const MlOperands& op, ARow arow, BRow brow,
+                                                 uint8_t (*st)[MlStage<FMT, RT>::END], float (&v)[4 * RT]) {
+    using F = MlFmt<FMT>;
+    using L = MlStage<FMT, RT>;
+    static_assert(NT <= RT, "live tiles");
+    constexpr int rt_used = NT;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15;
+    const int nb = op.nb;
+    static_assert(RT <= 4, "D and H staging threads");
+
+    constexpr int kAPer = RT;  // 16 RT rows x 16 chunks = 256 RT
+    constexpr int kB = kMlCols * F::NL;
+    constexpr int kBPer = (kB + 255) / 256;
+    uint32_t a_src[kAPer];
+    int a_off[kAPer];
+#pragma unroll
+    for (int i = 0; i < kAPer; i++) {
+        const int t = (int)threadIdx.x + 256 * i;
+        const int rr = t >> 4, part = t & 15;
+        a_src[i] = (uint32_t)(arow(rr) * op.ldq + 16 * part);
+        a_off[i] = rr < 16 * rt_used ? L::A + rr * kMlAS + 16 * part : -1;
+    }
+    uint32_t b_src[kBPer];
+    int b_off[kBPer];
+    bool b_hi[kBPer];
+#pragma unroll
+    for (int i = 0; i < kBPer; i++) {
+        const int t = min((int)threadIdx.x + 256 * i, kB - 1);
+        const int c2 = t / F::NL, part = t - c2 * F::NL;
+        const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
+        b_hi[i] = c2 >= op.bsplit;
+        b_src[i] = (uint32_t)(brow(c2) * op.brow_bytes + po);
+        b_off[i] = (int)threadIdx.x + 256 * i < kB ? L::B + c2 * F::BS + po : -1;
+    }
+    const int tD = threadIdx.x, tH = threadIdx.x - 64;
+    const int64_t d_row = arow(tD & (L::R - 1));
+    const int64_t h_row = arow((tH >> 1) & (L::R - 1));
+
+    v4i_ml sa[kAPer];
+    u32x4 sb[kBPer];
+    float sd = 0.f;
+    v4i_ml sh16 = {};
+    auto issue = [&](int b) {
+        const int8_t* abase = op.aq + (int64_t)b * 256;
+#pragma unroll
+        for (int i = 0; i < kAPer; i++)
+            if (a_off[i] >= 0) sa[i] = *(const v4i_ml*)(abase + a_src[i]);
+        const int64_t boff = FMT == kQ6_K ? ((int64_t)b * F::BB) & ~(int64_t)3 : (int64_t)b * F::BB;
+#pragma unroll
+        for (int i = 0; i < kBPer; i++) sb[i] = *(const u32x4*)((b_hi[i] ? op.b1 : op.b0) + boff + b_src[i]);
+        if (tD < L::R) sd = op.ad[d_row * op.ldd + b];
+        if constexpr (F::kMins)
+            if (tH >= 0 && tH < 2 * L::R) sh16 = *(const v4i_ml*)(op.hs + (h_row * nb + b) * 16 + 8 * (tH & 1));
+    };
+    auto park = [&](uint8_t* s) {
+#pragma unroll
+        for (int i = 0; i < kAPer; i++)
+            if (a_off[i] >= 0) *(v4i_ml*)(s + a_off[i]) = sa[i];
+#pragma unroll
+        for (int i = 0; i < kBPer; i++)
+            if (b_off[i] >= 0) *(u32x4*)(s + b_off[i]) = sb[i];
+        if (tD < L::R) *(float*)(s + L::D + 4 * tD) = sd;
+        if constexpr (F::kMins)
+            if (tH >= 0 && tH < 2 * L::R) *(v4i_ml*)(s + L::H + 32 * (tH >> 1) + 16 * (tH & 1)) = sh16;
+    };
+
+    const int col = 16 * wave + jj;
+    float o[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o[t][r] = 0.f;
+    issue(0);
+    park(st[0]);
+    lds_barrier();
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* S = st[b & 1];
+        if (b + 1 < nb) issue(b + 1);
+        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
+        ml_tile_block<FMT, NT>(S + L::A, S + L::B + col * F::BS, (const float*)(S + L::D), S + L::H, sh, q, jj, o);
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + 1 < nb) park(st[(b + 1) & 1]);
+        lds_barrier();
+    }
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[4 * t + r] = t < NT ? o[t][r] : 0.f;
+}
+
 }  // namespace iq

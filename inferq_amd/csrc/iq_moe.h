@@ -63,7 +63,20 @@ struct MoeParams {
     float* shared_out = nullptr;
     void* shared_ws = nullptr;
     size_t shared_ws_bytes = 0;
+    // the grouped path's down products in tile order (on request): chunks
+    // of up to kMpTileRows grouped rows, meta[2] of them
+    int down_tiles = 0;
+    int32_t* tchunk_group = nullptr;  // [max_tchunks]
+    int32_t* tchunk_r0 = nullptr;     // [max_tchunks]
+    int max_tchunks = 0;
 };
+
+constexpr int kMpRows = 16;  // grouped rows per chunk of the exact expert products
+#ifndef IQ_MP_TILE_ROWS
+#define IQ_MP_TILE_ROWS 32
+#endif
+constexpr int kMpTileRows = IQ_MP_TILE_ROWS;  // grouped rows per chunk of the tile-order down products
+static_assert(kMpTileRows % 16 == 0 && kMpTileRows <= 64, "tile-order chunk rows");
 
 // logits_ws[t][e] = x[t] . router[e] (the router matmul of
 // src/qwen/quantized_moe.rs:253) in a fixed order: lane l of a wave sums
@@ -86,8 +99,8 @@ hipError_t launch_moe(const MoeParams& p, int gate_dtype, int down_dtype, hipStr
 bool moep_supported(const MoeParams& p, int gate_dtype, int down_dtype);
 hipError_t launch_moe_prefill(const MoeParams& p, int gate_dtype, int down_dtype, hipStream_t s,
                               hipEvent_t const* events);
-// Upper bound of the row chunks a call of M tokens makes.
-int moep_max_chunks(int64_t M, int64_t K, int64_t E);
+// Upper bound of the chunks of `rows` grouped rows a call of M tokens makes.
+int moep_max_chunks(int64_t M, int64_t K, int64_t E, int rows);
 // One launch of a call already made with these parameters (stage 0 routing
 // of the grouped path, 1 gate/up, 2 down).
 hipError_t launch_moe_stage(const MoeParams& p, int gate_dtype, int down_dtype, int stage, hipStream_t s);

@@ -67,11 +67,14 @@ size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
     uint8_t* aq = take(act_bytes(P, I));
     uint8_t* vals = take(P * H * 4);
     const int64_t ngH = (H + 255) / 256;
-    const int maxch = moep_max_chunks(m, K, L->layer.E);
+    const int maxch = moep_max_chunks(m, K, L->layer.E, kMpRows);
+    const int maxtch = moep_max_chunks(m, K, L->layer.E, kMpTileRows);
     uint8_t* xhs = take(m * ngH * 32);
     uint8_t* ahs = take(P * ngI * 32);
     uint8_t* chg = take((size_t)maxch * 4);
     uint8_t* chr = take((size_t)maxch * 4);
+    uint8_t* tchg = take((size_t)maxtch * 4);
+    uint8_t* tchr = take((size_t)maxtch * 4);
     uint8_t* lgw = L->layer.router ? take((size_t)m * L->layer.E * 4) : nullptr;
     // the shared expert run apart: gate, up and SwiGLU rows [m x I], its
     // output [m x H] and the products' workspace
@@ -112,6 +115,9 @@ size_t carve(iq_moe* L, int m, uint8_t* base, MoeParams* p) {
         p->chunk_group = (int32_t*)chg;
         p->chunk_r0 = (int32_t*)chr;
         p->max_chunks = maxch;
+        p->tchunk_group = (int32_t*)tchg;
+        p->tchunk_r0 = (int32_t*)tchr;
+        p->max_tchunks = maxtch;
     }
     (void)ctr;
     return off;
@@ -272,6 +278,15 @@ IQ_API int iq_moe_reserve(iq_moe_t L, int64_t max_tokens, iq_stream_t stream) {
 }
 
 IQ_API int64_t iq_moe_slice_tokens(iq_moe_t L) { return L ? slice_tokens(L) : 0; }
+
+IQ_API int iq_moe_set_path(iq_moe_t L, int path) {
+    if (!L) return fail(IQ_ERR_INVALID, "null MoE handle");
+    if (path != IQ_PATH_AUTO && path != IQ_PATH_PREFILL_TILES)
+        return fail(IQ_ERR_INVALID, "MoE path %d: expected IQ_PATH_AUTO or IQ_PATH_PREFILL_TILES", path);
+    std::lock_guard<std::mutex> lock(L->mu);
+    L->layer.down_tiles = path == IQ_PATH_PREFILL_TILES ? 1 : 0;
+    return IQ_OK;
+}
 
 // One set of launches for m <= slice_tokens(L) tokens (the caller holds
 // L->mu).  logits == nullptr: the layer's router computes them from x.

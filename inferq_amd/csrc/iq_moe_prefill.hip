@@ -18,7 +18,10 @@
 //   k_mp_mm<0>    per (chunk, 32 intermediate rows): gate and up tiles of
 //                 the chunk's tokens, SwiGLU into act.
 //   k_mp_actq     act rows quantised (Q8K) for the down products.
-//   k_mp_mm<1>    per (chunk, 64 hidden rows): down products into vals.
+//   k_mp_mm<1>    per (chunk, 64 hidden rows): down products into vals;
+//                 on request k_mp_down_res (intermediate 512) or
+//                 k_mp_down_tiles instead, per (chunk of up to 32 rows, 128
+//                 or 64 hidden rows), in tile order (within 1e-4).
 //   k_mp_combine  routes in order (multiply, then add), then shared * gate.
 #include <type_traits>
 
@@ -43,8 +46,18 @@ constexpr int kMpRouteTok = 4;
 // 16 tokens or fewer), and the exact tile's work is mostly per output (the
 // eight lane chains), so 16-row chunks waste less on padding than 32-row
 // ones cost in repeated weight decode (the call: 184 -> 167 us).
-constexpr int kMpRT = 1;             // 16-row MFMA tiles per chunk
-constexpr int kMpRows = 16 * kMpRT;  // grouped rows per chunk
+constexpr int kMpRT = 1;  // 16-row MFMA tiles per chunk
+static_assert(kMpRows == 16 * kMpRT, "chunk rows");
+constexpr int kMpTileRT = kMpTileRows / 16;  // 16-row tiles per chunk of the tile-order down
+#ifndef IQ_MP_RES_CT
+#define IQ_MP_RES_CT 2
+#endif
+// Tiles of 64 hidden rows per workgroup of k_mp_down_res.  With chunks of
+// 32 rows and two tiles per workgroup (136 VGPRs, 48 KB of LDS: three
+// workgroups per CU) a 256-token call took 128.5 us, against 131.3-134.4 us
+// for 64-row chunks with 1-8 tiles (fewer decodes of each expert's weights,
+// but two workgroups per CU) and 131.7 us for 32-row chunks with 4 tiles.
+constexpr int kMpResCT = IQ_MP_RES_CT;
 
 // ------------------------------------------------------------ routing
 __global__ __launch_bounds__(kMpThreads) void k_mp_route(MoeParams p) {
@@ -86,47 +99,42 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_route(MoeParams p) {
 }
 
 // ----------------------------------------------------------- grouping
-// Exclusive prefix sums over the 1024 threads of three per-thread values.
-__device__ __forceinline__ void block_scan3(int& a, int& b, int& c, int* s_tmp /* [3][16] */, int& ta, int& tb,
-                                            int& tc) {
+// Exclusive prefix sums over the 1024 threads of N per-thread values; tot
+// receives the totals.
+template <int N>
+__device__ __forceinline__ void block_scan(int (&v)[N], int* s_tmp /* [N][16] */, int (&tot)[N]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int ia = a, ib = b, ic = c;
+    int inc[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) inc[i] = v[i];
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-        const int xa = __shfl_up(ia, off), xb = __shfl_up(ib, off), xc = __shfl_up(ic, off);
-        if (lane >= off) {
-            ia += xa;
-            ib += xb;
-            ic += xc;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const int x = __shfl_up(inc[i], off);
+            if (lane >= off) inc[i] += x;
         }
     }
-    if (lane == 63) {
-        s_tmp[wave] = ia;
-        s_tmp[16 + wave] = ib;
-        s_tmp[32 + wave] = ic;
-    }
+    if (lane == 63)
+#pragma unroll
+        for (int i = 0; i < N; i++) s_tmp[16 * i + wave] = inc[i];
     __syncthreads();
-    int ba = 0, bb = 0, bc = 0;
-    ta = tb = tc = 0;
-    for (int w = 0; w < kMpThreads / 64; w++) {
-        if (w < wave) {
-            ba += s_tmp[w];
-            bb += s_tmp[16 + w];
-            bc += s_tmp[32 + w];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        int base = 0;
+        tot[i] = 0;
+        for (int w = 0; w < kMpThreads / 64; w++) {
+            if (w < wave) base += s_tmp[16 * i + w];
+            tot[i] += s_tmp[16 * i + w];
         }
-        ta += s_tmp[w];
-        tb += s_tmp[16 + w];
-        tc += s_tmp[32 + w];
+        v[i] = base + inc[i] - v[i];
     }
-    a = ba + ia - a;
-    b = bb + ib - b;
-    c = bc + ic - c;
 }
 
 __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     extern __shared__ uint32_t s_mask[];  // [E][mw] token bitmask of each expert
     __shared__ int s_start[kMoeMaxExperts];
-    __shared__ int s_tmp[48];
+    __shared__ int s_tmp[64];
     const int tid = threadIdx.x;
     const int E = (int)p.E, K = (int)p.K, M = p.M, NA = M * K, mw = (M + 31) / 32;
     for (int i = tid; i < E * mw; i += kMpThreads) s_mask[i] = 0;
@@ -140,8 +148,12 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     if (tid < E)
         for (int w = 0; w < mw; w++) cnt += __popc(s_mask[tid * mw + w]);
     const int nch = (cnt + kMpRows - 1) / kMpRows;
-    int gid = cnt > 0, start = cnt, cst = nch, n_routed, total, routed_chunks;
-    block_scan3(gid, start, cst, s_tmp, n_routed, total, routed_chunks);
+    const int ntc = (cnt + kMpTileRows - 1) / kMpTileRows;
+    // group id, first grouped row, first chunk, first tile-order chunk
+    int sv[4] = {cnt > 0, cnt, nch, ntc}, tot[4];
+    block_scan<4>(sv, s_tmp, tot);
+    const int gid = sv[0], start = sv[1], cst = sv[2], tst = sv[3];
+    const int n_routed = tot[0], routed_chunks = tot[2], routed_tchunks = tot[3];
     if (tid < E) {
         s_start[tid] = start;
         if (cnt > 0) {
@@ -151,6 +163,10 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
             for (int j = 0; j < nch; j++) {
                 p.chunk_group[cst + j] = gid;
                 p.chunk_r0[cst + j] = kMpRows * j;
+            }
+            for (int j = 0; j < ntc; j++) {
+                p.tchunk_group[tst + j] = gid;
+                p.tchunk_r0[tst + j] = kMpTileRows * j;
             }
         }
     }
@@ -168,6 +184,7 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     }
     const bool has_shared = p.sgate_w != nullptr;
     const int sch = has_shared ? (M + kMpRows - 1) / kMpRows : 0;
+    const int stch = has_shared ? (M + kMpTileRows - 1) / kMpTileRows : 0;
     if (has_shared) {
         for (int t = tid; t < M; t += kMpThreads) p.assign_row[NA + t] = t;
         if (tid == 0) {
@@ -179,10 +196,15 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
             p.chunk_group[routed_chunks + j] = n_routed;
             p.chunk_r0[routed_chunks + j] = kMpRows * j;
         }
+        for (int j = tid; j < stch; j += kMpThreads) {
+            p.tchunk_group[routed_tchunks + j] = n_routed;
+            p.tchunk_r0[routed_tchunks + j] = kMpTileRows * j;
+        }
     }
     if (tid == 0) {
         p.meta[0] = n_routed + (has_shared ? 1 : 0);
         p.meta[1] = routed_chunks + sch;
+        p.meta[2] = routed_tchunks + stch;
     }
 }
 
@@ -289,6 +311,225 @@ __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
     }
 }
 
+// Down products in tile order (on request: the outputs are not quantised
+// again, so the per-lane f32 order is not needed for the rounding of a
+// later stage).  A workgroup owns one chunk of up to kMpTileRows grouped
+// rows of one group; each block of the expert's down rows is decoded once
+// for all of them.  The chunk's row count picks, once per workgroup, a body
+// compiled for that many 16-row tiles (NT), so no tile is skipped by a
+// branch inside the product.
+struct MpChunk {
+    int rows, pos0;
+    const uint8_t* w;  // the group's down matrix
+};
+
+__device__ __forceinline__ MpChunk mp_tile_chunk(const MoeParams& p, int c) {
+    const int g = __builtin_amdgcn_readfirstlane(p.tchunk_group[c]);
+    const int r0 = __builtin_amdgcn_readfirstlane(p.tchunk_r0[c]);
+    const int e = __builtin_amdgcn_readfirstlane(p.group_expert[g]);
+    MpChunk k;
+    k.rows = min(kMpTileRows, __builtin_amdgcn_readfirstlane(p.group_count[g]) - r0);
+    k.pos0 = __builtin_amdgcn_readfirstlane(p.group_start[g]) + r0;
+    k.w = e == (int)p.E ? p.sdown_w : p.down + (int64_t)e * p.d_exp_bytes;
+    return k;
+}
+
+// Grid (tiles of 64 hidden rows, tile-chunk bound), the activations staged
+// per block beside the weights (any intermediate width).
+template <int FMT, int NT>
+__device__ __forceinline__ void mp_down_tiles_body(const MoeParams& p, const MpChunk& k, uint8_t* lds) {
+    using L = MlStage<FMT, kMpTileRT>;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15;
+    MlOperands op;
+    op.aq = p.aq.q;
+    op.ldq = p.aq.ldq;
+    op.ad = p.aq.d;
+    op.ldd = p.aq.ldd;
+    op.hs = p.ahs;
+    op.nb = p.d_nbw;
+    op.brow_bytes = p.d_row_bytes;
+    op.b0 = op.b1 = k.w;
+    op.bsplit = kMlCols;
+    auto brow = [&](int t) -> int64_t { return min((int64_t)blockIdx.x * kMlCols + t, p.H - 1); };
+    auto arow = [&](int rr) -> int64_t { return (int64_t)(k.pos0 + min(rr, k.rows - 1)); };
+    float v[4 * kMpTileRT];
+    ml_product_tiles<FMT, kMpTileRT, NT>(op, arow, brow, (uint8_t (*)[L::END])lds, v);
+    const int64_t n = (int64_t)blockIdx.x * kMlCols + 16 * wave + jj;
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = 16 * t + 4 * q + r;
+            if (rr < k.rows && n < p.H) p.vals[(int64_t)(k.pos0 + rr) * p.H + n] = v[4 * t + r];
+        }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_mp_down_tiles(MoeParams p) {
+    using L = MlStage<FMT, kMpTileRT>;
+    __shared__ __align__(16) uint8_t lds[2 * L::END];
+    const int c = blockIdx.y;
+    if (c >= p.meta[2]) return;  // whole workgroup
+    const MpChunk k = mp_tile_chunk(p, c);
+    switch ((k.rows + 15) >> 4) {
+        case 1: mp_down_tiles_body<FMT, 1>(p, k, lds); break;
+        case 2: mp_down_tiles_body<FMT, (kMpTileRT < 2 ? kMpTileRT : 2)>(p, k, lds); break;
+        case 3: mp_down_tiles_body<FMT, (kMpTileRT < 3 ? kMpTileRT : 3)>(p, k, lds); break;
+        default: mp_down_tiles_body<FMT, kMpTileRT>(p, k, lds); break;
+    }
+}
+
+// The same products with the chunk's activations resident, for down
+// products of NB blocks (intermediate 256 NB): a workgroup owns one chunk
+// and NCT consecutive tiles of 64 hidden rows.  The chunk's activation rows,
+// scales and 16-value sums of every block are staged in LDS once; the
+// expert's weight blocks stream through two stages, column tile after
+// column tile, one stage loading while the other is decoded.
+template <int NB, int FMT>
+struct MpResident {
+    static constexpr int R = kMpTileRows;
+    static constexpr int A = 0;                                     // [NB][R][kMlAS] int8
+    static constexpr int D = A + NB * R * kMlAS;                    // [NB][R] f32
+    static constexpr int H = D + NB * R * 4;                        // [NB][R][16] f16 (Q4_K)
+    static constexpr int B = H + (FMT == kQ4_K ? NB * R * 32 : 0);  // [2][64][BS]
+    static constexpr int BST = kMlCols * MlFmt<FMT>::BS;
+    static constexpr int END = B + 2 * BST;
+};
+
+template <int FMT, int NB, int NCT, int NT>
+__device__ __forceinline__ void mp_down_res_body(const MoeParams& p, const MpChunk& k, uint8_t* lds) {
+    using F = MlFmt<FMT>;
+    using Lr = MpResident<NB, FMT>;
+    constexpr int R = kMpTileRows, rows_live = 16 * NT;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, jj = lane & 15;
+    const int64_t n0 = (int64_t)blockIdx.x * (kMlCols * NCT);
+
+    // ---- weight stages: stage s = (column tile s / NB, block s % NB)
+    constexpr int kB = kMlCols * F::NL, kBPer = (kB + 255) / 256;
+    uint32_t b_src[kBPer];
+    int b_off[kBPer];
+#pragma unroll
+    for (int i = 0; i < kBPer; i++) {
+        const int t = min((int)threadIdx.x + 256 * i, kB - 1);
+        const int c2 = t / F::NL, part = t - c2 * F::NL;
+        const int po = FMT == kQ6_K && part == F::NL - 1 ? 196 : 16 * part;
+        b_src[i] = (uint32_t)(c2 * p.d_row_bytes + po);
+        b_off[i] = (int)threadIdx.x + 256 * i < kB ? c2 * F::BS + po : -1;
+    }
+    u32x4 sb[2][kBPer];  // two stages of weight loads in flight
+    auto issue = [&](int s) {
+        const int ct = s / NB, b = s - ct * NB;
+        // the launch keeps every tile inside the matrix (H % (64 NCT) == 0)
+        const int64_t boff = FMT == kQ6_K ? ((int64_t)b * F::BB) & ~(int64_t)3 : (int64_t)b * F::BB;
+        const uint8_t* src = k.w + (n0 + (int64_t)kMlCols * ct) * p.d_row_bytes + boff;
+#pragma unroll
+        for (int i = 0; i < kBPer; i++) sb[s & 1][i] = *(const u32x4*)(src + b_src[i]);
+    };
+    auto park = [&](int s) {
+        uint8_t* st = lds + Lr::B + (s & 1) * Lr::BST;
+#pragma unroll
+        for (int i = 0; i < kBPer; i++)
+            if (b_off[i] >= 0) *(u32x4*)(st + b_off[i]) = sb[s & 1][i];
+    };
+    constexpr int NS = NCT * NB;
+    // ---- the chunk's activations, once: NB blocks x 16 NT rows x 16
+    // granules, the scales (threads 0 .. NB R - 1) and the 16-value sums
+    // (Q4_K: threads 0 .. 2 NB R - 1 over two passes); the first two weight
+    // stages are issued behind their loads, so that storing the activations
+    // waits for them alone
+    {
+        constexpr int kAG = NB * rows_live * 16, kAPer = (kAG + 255) / 256;
+        v4i_ml sa[kAPer];
+#pragma unroll
+        for (int i = 0; i < kAPer; i++) {
+            const int t = min((int)threadIdx.x + 256 * i, kAG - 1);
+            const int b = t / (rows_live * 16), rr = (t >> 4) % rows_live, part = t & 15;
+            sa[i] = *(const v4i_ml*)(p.aq.q + (int64_t)(k.pos0 + min(rr, k.rows - 1)) * p.aq.ldq + b * 256 + 16 * part);
+        }
+        float sd = 0.f;
+        const int tb = (int)threadIdx.x / R, tr = (int)threadIdx.x % R;
+        if ((int)threadIdx.x < NB * R) sd = p.aq.d[(int64_t)(k.pos0 + min(tr, k.rows - 1)) * p.aq.ldd + tb];
+        v4i_ml sh16[2] = {};
+        if constexpr (FMT == kQ4_K)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int t = (int)threadIdx.x + 256 * i;  // NB R rows x 2 halves
+                const int hb = t / (2 * R), hr = (t >> 1) % R;
+                if (t < 2 * NB * R)
+                    sh16[i] = *(const v4i_ml*)(p.ahs + ((int64_t)(k.pos0 + min(hr, k.rows - 1)) * NB + hb) * 16 +
+                                               8 * (t & 1));
+            }
+        issue(0);
+        if (NS > 1) issue(1);
+#pragma unroll
+        for (int i = 0; i < kAPer; i++) {
+            const int t = (int)threadIdx.x + 256 * i;
+            const int b = t / (rows_live * 16), rr = (t >> 4) % rows_live, part = t & 15;
+            if (t < kAG) *(v4i_ml*)(lds + Lr::A + (b * R + rr) * kMlAS + 16 * part) = sa[i];
+        }
+        if ((int)threadIdx.x < NB * R) *(float*)(lds + Lr::D + 4 * threadIdx.x) = sd;
+        if constexpr (FMT == kQ4_K)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int t = (int)threadIdx.x + 256 * i;
+                if (t < 2 * NB * R) *(v4i_ml*)(lds + Lr::H + 16 * t) = sh16[i];
+            }
+    }
+
+    park(0);
+    lds_barrier();
+    const int col = 16 * wave + jj;
+    float o[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o[t][r] = 0.f;
+    // stage s: its weights were parked at the end of stage s - 1; the loads
+    // of s + 1 and s + 2 are in flight while it is decoded
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        if (s + 2 < NS) issue(s + 2);
+        const int ct = s / NB, b = s - ct * NB;
+        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
+        ml_tile_block<FMT, NT>(lds + Lr::A + b * R * kMlAS, lds + Lr::B + (s & 1) * Lr::BST + col * F::BS,
+                               (const float*)(lds + Lr::D) + b * R, lds + Lr::H + b * R * 32, sh, q, jj, o);
+        if (b == NB - 1) {
+            const int64_t n = n0 + (int64_t)kMlCols * ct + col;
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int rr = 16 * t + 4 * q + r;
+                    if (rr < k.rows) p.vals[(int64_t)(k.pos0 + rr) * p.H + n] = o[t][r];
+                    o[t][r] = 0.f;
+                }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 1 < NS) park(s + 1);
+        lds_barrier();
+    }
+}
+
+template <int FMT, int NB, int NCT>
+__global__ __launch_bounds__(256) void k_mp_down_res(MoeParams p) {
+    using Lr = MpResident<NB, FMT>;
+    static_assert(Lr::END <= 160 * 1024, "LDS");
+    __shared__ __align__(16) uint8_t lds[Lr::END];
+    const int c = blockIdx.y;
+    if (c >= p.meta[2]) return;  // whole workgroup
+    const MpChunk k = mp_tile_chunk(p, c);
+    switch ((k.rows + 15) >> 4) {
+        case 1: mp_down_res_body<FMT, NB, NCT, 1>(p, k, lds); break;
+        case 2: mp_down_res_body<FMT, NB, NCT, (kMpTileRT < 2 ? kMpTileRT : 2)>(p, k, lds); break;
+        case 3: mp_down_res_body<FMT, NB, NCT, (kMpTileRT < 3 ? kMpTileRT : 3)>(p, k, lds); break;
+        default: mp_down_res_body<FMT, NB, NCT, kMpTileRT>(p, k, lds); break;
+    }
+}
+
 // ------------------------------------------- act quantisation, combine
 // One wave per (grouped row, 256-value block) of act.
 template <int DFMT>
@@ -373,8 +614,15 @@ hipError_t launch_p(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
     hipLaunchKernelGGL((k_mp_actq<DFMT>), dim3((unsigned)((aw + 3) / 4)), dim3(256), 0, s, p, P);
     if (hipError_t e = hipGetLastError()) return e;
     if (ev) (void)hipEventRecord(ev[2], s);
-    hipLaunchKernelGGL((k_mp_mm<DFMT, 1>), dim3((unsigned)((p.H + kMlCols - 1) / kMlCols), (unsigned)p.max_chunks),
-                       dim3(256), 0, s, p);
+    if (p.down_tiles && p.d_nbw == 2 && p.H % (kMlCols * kMpResCT) == 0)
+        hipLaunchKernelGGL((k_mp_down_res<DFMT, 2, kMpResCT>), dim3((unsigned)(p.H / (kMlCols * kMpResCT)),
+                           (unsigned)p.max_tchunks), dim3(256), 0, s, p);
+    else if (p.down_tiles)
+        hipLaunchKernelGGL((k_mp_down_tiles<DFMT>), dim3((unsigned)((p.H + kMlCols - 1) / kMlCols), (unsigned)p.max_tchunks),
+                           dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((k_mp_mm<DFMT, 1>), dim3((unsigned)((p.H + kMlCols - 1) / kMlCols), (unsigned)p.max_chunks),
+                           dim3(256), 0, s, p);
     if (hipError_t e = hipGetLastError()) return e;
     hipLaunchKernelGGL(k_mp_combine, dim3((unsigned)((p.H + 1023) / 1024), (unsigned)M), dim3(256), 0, s, p);
     if (hipError_t e = hipGetLastError()) return e;
@@ -384,10 +632,10 @@ hipError_t launch_p(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
 
 }  // namespace
 
-int moep_max_chunks(int64_t M, int64_t K, int64_t E) {
-    // sum over groups of ceil(count / 32) <= rows / 32 + groups
+int moep_max_chunks(int64_t M, int64_t K, int64_t E, int rows) {
+    // sum over groups of ceil(count / rows) <= grouped rows / rows + groups
     const int64_t P = M * K + M;
-    return (int)(P / kMpRows + std::min(E, M * K) + 2);
+    return (int)(P / rows + std::min(E, M * K) + 2);
 }
 
 bool moep_supported(const MoeParams& p, int gfmt, int dfmt) {

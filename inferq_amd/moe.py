@@ -130,6 +130,12 @@ class QuantizedMoeLayer:
         wider calls run as consecutive slices."""
         return int(lib().iq_moe_slice_tokens(self._h))
 
+    def set_path(self, path: int) -> None:
+        """How grouped calls form the down products (iq_moe_set_path):
+        _lib.PATH_AUTO keeps the reference's bits, _lib.PATH_PREFILL_TILES
+        takes tile order (within 1e-4, not bitwise)."""
+        check(lib().iq_moe_set_path(self._h, int(path)))
+
     def forward_into(self, xs, router_logits, out, experts=None, weights=None) -> None:
         """Raw call: device f32 xs [m, hidden], logits [m, n_experts], out [m, hidden]."""
         self._check_device(xs=xs, router_logits=router_logits, out=out, experts=experts, weights=weights)

@@ -125,6 +125,7 @@ extern "C" {
     pub fn iq_moe_destroy(l: iq_moe_t) -> c_int;
     pub fn iq_moe_reserve(l: iq_moe_t, max_tokens: i64, stream: iq_stream_t) -> c_int;
     pub fn iq_moe_slice_tokens(l: iq_moe_t) -> i64;
+    pub fn iq_moe_set_path(l: iq_moe_t, path: c_int) -> c_int;
     pub fn iq_moe_forward(l: iq_moe_t, x: *const f32, logits: *const f32, m: i64, out: *mut f32,
                           experts: *mut i32, weights: *mut f32, stream: iq_stream_t) -> c_int;
     pub fn iq_moe_forward_x(l: iq_moe_t, x: *const f32, m: i64, residual: *const f32, out: *mut f32,
@@ -331,6 +332,12 @@ impl Moe {
     /// graph can capture them without an eager call first.
     pub fn reserve(&self, max_tokens: usize, stream: iq_stream_t) -> anyhow::Result<()> {
         check(unsafe { iq_moe_reserve(self.0, max_tokens as i64, stream) })
+    }
+
+    /// Down products of grouped calls in tile order (`IQ_PATH_PREFILL_TILES`,
+    /// within 1e-4, not bitwise) or the reference's order (`IQ_PATH_AUTO`).
+    pub fn set_path(&self, path: c_int) -> anyhow::Result<()> {
+        check(unsafe { iq_moe_set_path(self.0, path) })
     }
 
     /// forward (src/qwen/quantized_moe.rs:227-281) with the router on the GPU
