@@ -309,6 +309,8 @@ int64_t iq_moe_slice_tokens(iq_moe_t moe);
  * bitwise.  Gate/up stay in the exact order on both (their SwiGLU rows are
  * quantised again), and so do calls on the token-major path (up to 32
  * tokens at the reference's shapes).  Any other path is IQ_ERR_INVALID.
+ * The choice applies to calls made after it; a graph captured earlier
+ * keeps the path it was captured with.
  * Replaces: the path choice the reference offers for matrix products
  * (MultiRowPath, src/gguf.rs:43-62), applied to the expert products of
  * QuantizedMoeLayer::forward (src/qwen/quantized_moe.rs:336-406). */

@@ -162,6 +162,66 @@ def test_tile_path_leaves_token_major_and_default_bitwise(gpu, qwen_layer):
                     "back on IQ_PATH_AUTO")
 
 
+def test_tile_path_from_x_with_residual(gpu, qwen_layer):
+    """The whole sublayer from x (router on the GPU, residual added last) on
+    a tile-order handle: routes equal the default handle's, the output
+    within 1e-6 of it, and the residual is added after the combine."""
+    rng = np.random.default_rng(4800)
+    layer = dict(qwen_layer)
+    router = (rng.standard_normal((256, 2048), dtype=np.float32) / np.float32(np.sqrt(2048)))
+    t = {k: torch.from_numpy(v).to(gpu) for k, v in layer.items() if isinstance(v, np.ndarray)}
+    rt = torch.from_numpy(router).to(gpu)
+
+    def make():
+        return MOE.QuantizedMoeLayer(2048, 512, 256, 8, Q4, Q6, t["gate"], t["up"], t["down"], t["shared_gate"],
+                                     t["shared_up"], t["shared_down"], t["selector"], router=rt)
+
+    exact, tiles = make(), make()
+    tiles.set_path(_lib.PATH_PREFILL_TILES)
+    x = torch.from_numpy(S.normal((96, 2048), rng)).to(gpu)
+    res = torch.from_numpy(S.normal((96, 2048), rng)).to(gpu)
+    a, b = tiles.forward(x, residual=res), exact.forward(x, residual=res)
+    assert [r.experts for r in a.routes] == [r.experts for r in b.routes]
+    assert_close_normwise(a.hidden.cpu().numpy(), b.hidden.cpu().numpy(), 1e-6, "from x, tiles vs exact")
+    plain = tiles.forward(x).hidden
+    assert_close_normwise((plain + res).cpu().numpy(), a.hidden.cpu().numpy(), 1e-6, "residual added last")
+
+
+def test_tile_path_graph_replays_match_eager_calls(gpu, qwen_layer):
+    """A tile-order call captured in a HIP graph (after iq_moe_reserve, no
+    eager call first) and replayed with fresh inputs and eager work between
+    replays gives the eager call's bits each time."""
+    _, tiles = _pair(qwen_layer, 8, gpu)
+    m = 96
+    tiles.reserve(m)
+    rng = np.random.default_rng(4900)
+    xs = [torch.from_numpy(S.normal((m, 2048), rng)).to(gpu) for _ in range(3)]
+    ls = [torch.from_numpy(_dirichlet_logits(m, 256, rng)).to(gpu) for _ in range(3)]
+    x_buf, l_buf, o_buf = torch.zeros(m, 2048, device=gpu), torch.zeros(m, 256, device=gpu), \
+        torch.empty(m, 2048, device=gpu)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        tiles.forward_into(x_buf, l_buf, o_buf)
+    eager = []
+    for x, lg in zip(xs, ls):
+        o = torch.empty(m, 2048, device=gpu)
+        tiles.forward_into(x, lg, o)
+        eager.append(o.cpu().numpy())
+    for rep in range(2):
+        for i in range(3):
+            x_buf.copy_(xs[i])
+            l_buf.copy_(ls[i])
+            graph.replay()
+            torch.cuda.synchronize()
+            assert_bitexact(o_buf.cpu().numpy(), eager[i], f"replay {rep}.{i}")
+            o = torch.empty(m, 2048, device=gpu)
+            tiles.forward_into(xs[(i + 1) % 3], ls[(i + 1) % 3], o)
+            torch.cuda.synchronize()
+            assert_bitexact(o.cpu().numpy(), eager[(i + 1) % 3], "eager between replays")
+
+
 def test_set_path_refuses_other_paths(gpu, qwen_layer):
     moe, _ = _device_layer(qwen_layer, 8, gpu)
     for path in (_lib.PATH_LANES, _lib.PATH_GEMV, _lib.PATH_LANE_MFMA, 99, -1):
