@@ -146,6 +146,9 @@ def test_forty_layer_step_in_one_graph(gpu, oracle, model):
     steps = []
     for m, seed in ((1, 41), (8, 48)):
         st = _Step(model, m, gpu, seed)
+        # the inputs were drawn on the default stream; the eager pass, which
+        # fixes the residual scales, must read them complete
+        torch.cuda.synchronize()
         with torch.cuda.stream(stream):
             st.run()  # sizes the stream's and the layers' workspaces outside the capture
         torch.cuda.synchronize()
