@@ -25,6 +25,8 @@
 // ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) plus (m0+m2) + (m1+m3).
 #pragma once
 
+#include <type_traits>
+
 #include "iq_lanes.h"
 
 namespace iq {
@@ -112,6 +114,32 @@ __device__ __forceinline__ void ml_lds_span(const uint8_t* row, int sh, int o, u
     w[N] = *(const uint32_t*)(row + o + 4 * N);
 #pragma unroll
     for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], (uint32_t)sh);
+}
+
+// The same reads for a shift known at compile time (a Q6_K block's shift is
+// 2 (b & 1) in rows whose byte length is a multiple of 4): at shift 0 the
+// window is the bytes themselves, with no realignment and no extra dword.
+template <int S>
+using MlShift = std::integral_constant<int, S>;
+template <int S>
+__device__ __forceinline__ uint32_t ml_lds_win(const uint8_t* row, MlShift<S>, int o) {
+    if constexpr (S == 0) return *(const uint32_t*)(row + o);
+    else return ml_lds_win(row, S, o);
+}
+template <int N, int S>
+__device__ __forceinline__ void ml_lds_span(const uint8_t* row, MlShift<S>, int o, uint32_t (&out)[N]) {
+    if constexpr (S == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 4; i++) {
+            const u32x4a16 v = *(const u32x4a16*)(row + o + 16 * i);
+            out[4 * i] = v.x;
+            out[4 * i + 1] = v.y;
+            out[4 * i + 2] = v.z;
+            out[4 * i + 3] = v.w;
+        }
+    } else {
+        ml_lds_span<N>(row, S, o, out);
+    }
 }
 
 // Operands of one tile.  Activation row rr (0 .. 16 RT - 1) of the tile is
@@ -379,8 +407,8 @@ struct MlPkBlock {
     float ms[4][4];
     float dm[4];
 };
-template <int FMT>
-__device__ __forceinline__ void ml_pk_block(const uint8_t* bcol, int sh, const uint8_t* arow, const float* D,
+template <int FMT, class SHT>
+__device__ __forceinline__ void ml_pk_block(const uint8_t* bcol, SHT sh, const uint8_t* arow, const float* D,
                                             const uint8_t* H, int q, int jj, MlPkBlock<FMT>& o) {
     const int h = q & 1, upper = q >> 1;
     float xd, xdm = 0.f;
@@ -602,10 +630,13 @@ __device__ __forceinline__ void ml_product_pk(const MlOperands& op, ARow arow, B
     for (int b = 0; b < nb; b++) {
         const uint8_t* S = st[b & 1];
         if (b + 1 < nb) issue(b + 1);
-        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
         const uint8_t* arowp = a_live ? S + L::A + (jj & 7) * kMlAS + 16 * h : zero + 16 * h;
         MlPkBlock<FMT> o;
-        ml_pk_block<FMT>(S + L::B + col * F::BS, sh, arowp, (const float*)(S + L::D), S + L::H, q, jj, o);
+        // Q6_K: block b of a row sits at shift 2 (b & 1) (rows of a multiple of 4 bytes)
+        if (FMT == kQ6_K && (b & 1))
+            ml_pk_block<FMT>(S + L::B + col * F::BS, MlShift<2>{}, arowp, (const float*)(S + L::D), S + L::H, q, jj, o);
+        else
+            ml_pk_block<FMT>(S + L::B + col * F::BS, MlShift<0>{}, arowp, (const float*)(S + L::D), S + L::H, q, jj, o);
         ml_pk_chain<FMT>(o, acc, accm);
         __builtin_amdgcn_sched_barrier(0);
         if (b + 1 < nb) park(st[(b + 1) & 1]);
@@ -769,9 +800,9 @@ __device__ __forceinline__ void ml_product_sk(const MlOperands& op, ARow arow, B
 // bcol this lane's weight row staged as in ml_product (Q6_K: the dword
 // window at shift sh), D the rows' block scales, H their 16-value sums
 // (Q4_K, 32 bytes a row).
-template <int FMT, int RT>
+template <int FMT, int RT, class SHT>
 __device__ __forceinline__ void ml_tile_block(const uint8_t* A, const uint8_t* bcol, const float* D,
-                                              const uint8_t* H, int sh, int q, int jj, float (&o)[RT][4]) {
+                                              const uint8_t* H, SHT sh, int q, int jj, float (&o)[RT][4]) {
     const int h = q & 1, upper = q >> 1;
     float xd, xdm = 0.f;
     Q4Scales sc{};
@@ -957,8 +988,12 @@ __device__ __forceinline__ void ml_product_tiles(const MlOperands& op, ARow arow
     for (int b = 0; b < nb; b++) {
         const uint8_t* S = st[b & 1];
         if (b + 1 < nb) issue(b + 1);
-        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
-        ml_tile_block<FMT, NT>(S + L::A, S + L::B + col * F::BS, (const float*)(S + L::D), S + L::H, sh, q, jj, o);
+        if (FMT == kQ6_K && (b & 1))  // block b of a row sits at shift 2 (b & 1)
+            ml_tile_block<FMT, NT>(S + L::A, S + L::B + col * F::BS, (const float*)(S + L::D), S + L::H, MlShift<2>{},
+                                   q, jj, o);
+        else
+            ml_tile_block<FMT, NT>(S + L::A, S + L::B + col * F::BS, (const float*)(S + L::D), S + L::H, MlShift<0>{},
+                                   q, jj, o);
         __builtin_amdgcn_sched_barrier(0);
         if (b + 1 < nb) park(st[(b + 1) & 1]);
         lds_barrier();

@@ -494,9 +494,14 @@ __device__ __forceinline__ void mp_down_res_body(const MoeParams& p, const MpChu
     for (int s = 0; s < NS; s++) {
         if (s + 2 < NS) issue(s + 2);
         const int ct = s / NB, b = s - ct * NB;
-        const int sh = FMT == kQ6_K ? (int)(((int64_t)b * F::BB) & 3) : 0;
-        ml_tile_block<FMT, NT>(lds + Lr::A + b * R * kMlAS, lds + Lr::B + (s & 1) * Lr::BST + col * F::BS,
-                               (const float*)(lds + Lr::D) + b * R, lds + Lr::H + b * R * 32, sh, q, jj, o);
+        const uint8_t* sa = lds + Lr::A + b * R * kMlAS;
+        const uint8_t* sb = lds + Lr::B + (s & 1) * Lr::BST + col * F::BS;
+        const float* sd = (const float*)(lds + Lr::D) + b * R;
+        const uint8_t* sh16 = lds + Lr::H + b * R * 32;
+        if (FMT == kQ6_K && (b & 1))  // block b of a row sits at shift 2 (b & 1)
+            ml_tile_block<FMT, NT>(sa, sb, sd, sh16, MlShift<2>{}, q, jj, o);
+        else
+            ml_tile_block<FMT, NT>(sa, sb, sd, sh16, MlShift<0>{}, q, jj, o);
         if (b == NB - 1) {
             const int64_t n = n0 + (int64_t)kMlCols * ct + col;
 #pragma unroll
