@@ -169,6 +169,23 @@ def test_large_matrix_rows_bitexact(gpu, oracle, large_matrices, dtype):
         assert_bitexact(got, expected, f"{S.NAMES[dtype]} [{rows}x2048] m={m}")
 
 
+@pytest.mark.parametrize("rows,cols", [(100001, 512), (70001, 2048)])
+def test_q6k_many_pair_lane_tiles_bitexact(gpu, oracle, rows, cols):
+    """Q6_K matrices of more 64-row pair-lane tiles than the GPU holds
+    workgroups at once (1563 and 1094 tiles) at 3 and 8 rows, with 2 and 8
+    blocks per row (block shifts 0 and 2) and a ragged last tile.  Bitwise
+    the oracle's."""
+    rng = np.random.default_rng(rows + cols)
+    w = S.random_matrix(Q6, rows, cols, rng)
+    mat = Q.QuantizedMatrix.upload(w, Q6, rows, cols)
+    impl = 1 if oracle.have_avx2() else 0
+    for m in (3, 8):
+        x = S.normal((m, cols), np.random.default_rng(2200 + m))
+        expected = oracle.matmul(Q6, w, rows, cols, x, impl=impl, nthreads=8)
+        got = mat.forward(torch.from_numpy(x).to(gpu)).cpu().numpy()
+        assert_bitexact(got, expected, f"Q6_K [{rows}x{cols}] m={m}")
+
+
 def test_large_wide_matrix_rows_bitexact(gpu, oracle):
     """Width 4096 past 64 MiB (Q4_K [30000 x 4096], 69 MB): one row takes the
     four-row GEMV items over two slices per row, 2..8 rows the pair-lane
