@@ -80,6 +80,38 @@ __device__ __forceinline__ void route_topk_vals(const float (&lv)[kRoutePer], in
     }
 }
 
+// route_topk_vals with each pick handed to store(s, expert) as it is found
+// (wave-uniform arguments) instead of written into an array indexed by the
+// round: kernels whose register budget is tight would otherwise keep that
+// array in scratch memory, on the routing's dependent chain.
+template <int PER, class Store>
+__device__ __forceinline__ void route_topk_each(const float (&lv)[kRoutePer], int E, int count, Store&& store) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) key[j] = PER * lane + j < E ? route_ukey(lv[j]) : 0u;
+    for (int s = 0; s < count; s++) {
+        uint32_t m = key[0];
+#pragma unroll
+        for (int j = 1; j < PER; j++) m = max(m, key[j]);
+        const uint32_t best = wave_max_u32(m);
+        const int L = (int)__builtin_ctzll(__ballot(m == best));
+        int jf = PER - 1;
+#pragma unroll
+        for (int j = PER - 2; j >= 0; j--) jf = key[j] == m ? j : jf;
+        const int j = __builtin_amdgcn_readlane(jf, L);
+#pragma unroll
+        for (int q = 0; q < PER; q++) key[q] = (lane == L && q == j) ? 0u : key[q];
+        store(s, PER * L + j);
+    }
+}
+
+template <class Store>
+__device__ __forceinline__ void route_topk_each_any(const float (&lv)[kRoutePer], int E, int count, Store&& store) {
+    if (E <= 256) route_topk_each<4>(lv, E, count, store);
+    else route_topk_each<kRoutePer>(lv, E, count, store);
+}
+
 // The expert at rank s (0-based) of the same order, wave-uniform, without
 // the s rounds before it: a bitwise search for T, the (s+1)-th largest key
 // counted with multiplicity (the largest value with at least s+1 keys at or
@@ -193,6 +225,53 @@ __device__ __forceinline__ void route_weights(const float (&lv)[kRoutePer], int 
     }
     if (normalize)
         for (int s = 0; s < K; s++) w[s] = __fdiv_rn(w[s], sum);
+}
+
+// route_weights in two parts that can run on different waves: the softmax
+// denominator (exp(x - max) of every logit into `scratch`, E floats of LDS,
+// and their sequential sum in index order; independent of the selection),
+// then the picks' weights from it with the picks read from LDS (sel[0..K))
+// and written to LDS (w[0..K), lane 0).  The same operations in the same
+// order as route_weights, and no per-lane array indexed by the rank.
+__device__ __forceinline__ float route_softmax_den(const float (&lv)[kRoutePer], int E, float* scratch) {
+    const int lane = threadIdx.x & 63;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kRoutePer; j++) mx = fmaxf(mx, lv[j]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const int per = route_per(E);
+#pragma unroll
+    for (int j = 0; j < kRoutePer; j++) {
+        const int i = per * lane + j;
+        if (j < per && i < E) scratch[i] = exp_f32(lv[j] - mx);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float den = 0.f;
+    int i = 0;
+    for (; i + 16 <= E; i += 16) {
+        const f32x4 t0 = *(const f32x4*)(scratch + i), t1 = *(const f32x4*)(scratch + i + 4);
+        const f32x4 t2 = *(const f32x4*)(scratch + i + 8), t3 = *(const f32x4*)(scratch + i + 12);
+        den = den + t0.x; den = den + t0.y; den = den + t0.z; den = den + t0.w;
+        den = den + t1.x; den = den + t1.y; den = den + t1.z; den = den + t1.w;
+        den = den + t2.x; den = den + t2.y; den = den + t2.z; den = den + t2.w;
+        den = den + t3.x; den = den + t3.y; den = den + t3.z; den = den + t3.w;
+    }
+    for (; i < E; i++) den = den + scratch[i];
+    return den;
+}
+
+__device__ __forceinline__ void route_pick_weights(float den, int K, const int* sel, int normalize,
+                                                   const float* scratch, float* w) {
+    const int lane = threadIdx.x & 63;
+    float sum = 0.f;
+    for (int s = 0; s < K; s++) sum = sum + __fdiv_rn(scratch[sel[s]], den);
+    for (int s = 0; s < K; s++) {
+        const float ws = __fdiv_rn(scratch[sel[s]], den);
+        if (lane == 0) w[s] = normalize ? __fdiv_rn(ws, sum) : ws;
+    }
 }
 
 }  // namespace iq
