@@ -543,8 +543,9 @@ __global__ __launch_bounds__(128 * RG) void k_moe1_gate_up_rows(MoeParams p) {
     }
 }
 
-// Routing of every token of a call (grid M, two waves each).
-__global__ __launch_bounds__(128) void k_moe1_route(MoeParams p) { moe1_route(p, (int)(threadIdx.x >> 6), blockIdx.x); }
+// Routing of every token of a call (grid M, three waves each: top-k, shared
+// gate, softmax denominator).
+__global__ __launch_bounds__(192) void k_moe1_route(MoeParams p) { moe1_route(p, (int)(threadIdx.x >> 6), blockIdx.x); }
 
 // Grid (H/8, M); one wave per route slot of token t = blockIdx.y (blockDim
 // 64 * slots), all on the same 8 hidden rows.  Each wave loads its slot's
@@ -650,7 +651,7 @@ hipError_t launch_moe1_stage(const MoeParams& p, int stage, hipStream_t s) {
         constexpr int RG = kMoe1RowGroups;
         const unsigned rows_g = (unsigned)(p.I / (8 * RG));
         if (p.M >= kMoeRouteLaunchMin) {
-            hipLaunchKernelGGL(k_moe1_route, dim3(m), dim3(128), 0, s, p);
+            hipLaunchKernelGGL(k_moe1_route, dim3(m), dim3(192), 0, s, p);
             hipLaunchKernelGGL((k_moe1_gate_up_rows<GFMT, 8, true, RG>), dim3(rows_g, nslots, m), dim3(128 * RG), 0, s,
                                p);
         } else if (m == 1) {
