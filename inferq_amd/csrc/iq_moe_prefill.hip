@@ -9,7 +9,8 @@
 // reference's per-lane FMA chains.
 //
 // Six launches per call:
-//   k_mp_route    two waves per token: top-k and routing weights, shared gate;
+//   k_mp_route    three waves per token: top-k and routing weights, shared
+//                 gate, softmax denominator;
 //                 other workgroups quantise x (Q8K, activation layout).
 //   k_mp_group    one workgroup: per-expert token bitmasks give counts,
 //                 groups (experts ascending), each (token, route)'s position
@@ -36,10 +37,11 @@ namespace iq {
 namespace {
 
 constexpr int kMpThreads = 1024;  // routing and grouping workgroups
-// Tokens per routing workgroup: wave 2i routes token i, wave 2i + 1 forms
-// its shared-expert gate.  Four tokens keep the serial chains (top-k rounds,
-// the index-order softmax sum) on separate SIMDs: 11.9 us for 256 tokens at
-// sixteen tokens per workgroup, one wave each, against 8.9 at four.
+// Tokens per routing workgroup: wave 3i routes token i, wave 3i + 1 forms
+// its shared-expert gate, wave 3i + 2 its softmax denominator.  Few tokens
+// per workgroup keep the serial chains (top-k rounds, the index-order
+// softmax sum) on separate SIMDs: 11.9 us for 256 tokens at sixteen tokens
+// per workgroup, one wave each, against 8.9 at four.
 constexpr int kMpRouteTok = 4;
 // Chunks of one 16-row MFMA tile: at prefill widths most groups are small
 // (Dirichlet(0.3) routing at 256 tokens: two thirds of the hit experts get
@@ -65,25 +67,44 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_route(MoeParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nr = (p.M + kMpRouteTok - 1) / kMpRouteTok;
     if ((int)blockIdx.x < nr) {
+        // token i of the workgroup: wave 3i its top-k and then its weights,
+        // wave 3i + 1 its shared-expert gate, wave 3i + 2 the softmax
+        // denominator meanwhile (it does not depend on the selection)
         __shared__ __align__(16) float s_ev[kMpRouteTok][kMoeMaxExperts];
-        const int t = (int)blockIdx.x * kMpRouteTok + (wave >> 1);
-        if (wave >= 2 * kMpRouteTok || t >= p.M) return;
-        if (wave & 1) {
-            if (p.selector) {
+        __shared__ int s_sel[kMpRouteTok][kMoeMaxTopK];
+        __shared__ float s_w[kMpRouteTok][kMoeMaxTopK];
+        __shared__ float s_den[kMpRouteTok];
+        const int ti = wave / 3, role = wave - 3 * ti;
+        const int t = (int)blockIdx.x * kMpRouteTok + ti;
+        if (ti >= kMpRouteTok) return;  // (a wave that has ended is not waited for at a barrier)
+        const int E = (int)p.E, K = (int)p.K;
+        if (role == 1) {
+            if (p.selector && t < p.M) {
                 const float gate = selector_gate(p.x + (int64_t)t * p.H, p.selector, p.H);
                 if (lane == 0) p.sgate[t] = gate;
             }
             return;
         }
-        const int E = (int)p.E, K = (int)p.K;
-        int sel[kMoeMaxTopK];
-        float lv[kRoutePer], w[kMoeMaxTopK];
-        route_topk<kMoeMaxTopK>(p.logits + (int64_t)t * E, E, K, sel, lv);
-        if (lane == 0)
-            for (int s = 0; s < K; s++) p.experts[t * K + s] = sel[s];
-        route_weights<kMoeMaxTopK>(lv, E, K, sel, p.normalize, s_ev[wave >> 1], w);
-        if (lane == 0)
-            for (int s = 0; s < K; s++) p.weights[t * K + s] = w[s];
+        float lv[kRoutePer];
+        if (t < p.M) route_load(p.logits + (int64_t)t * E, E, lv);
+        if (t < p.M && role == 2) {
+            const float den = route_softmax_den(lv, E, s_ev[ti]);
+            if (lane == 0) s_den[ti] = den;
+        } else if (t < p.M) {
+            route_topk_each_any(lv, E, K, [&](int s, int e) {
+                if (lane == 0) {
+                    p.experts[t * K + s] = e;
+                    s_sel[ti][s] = e;
+                }
+            });
+        }
+        lds_barrier();  // the top-k and denominator waves of every token
+        if (role != 0 || t >= p.M) return;
+        route_pick_weights(s_den[ti], K, s_sel[ti], p.normalize, s_ev[ti], s_w[ti]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < K) p.weights[t * K + lane] = s_w[ti][lane];
         return;
     }
     // x quantisation: one wave per (row, 256-value block)
