@@ -344,9 +344,9 @@ __device__ void moe1_route(const MoeParams& p, int wave, int t) {
 }
 
 // The one-token form.  Grid (I/8, slots + 1, M): row 0 of each token
-// holds its routing workgroup (x == 0); workgroup (x, s + 1, t) forms the 8
+// holds its routing workgroup (x == 0); workgroup (x, K - s, t) forms the 8
 // intermediate rows from 8 x of gate and up of token t's expert at route
-// rank s (or the shared expert), split by K over eight waves: gate on
+// rank s (row K + 1: the shared expert), split by K over eight waves: gate on
 // waves 0-3 and up on waves 4-7, each wave a quarter of the blocks of one
 // matrix.  Each wave forms its blocks' exact lane integers and f32 scales;
 // wave 0 then advances the accumulators through all NG blocks in order (the
@@ -375,7 +375,10 @@ __global__ __launch_bounds__(512) void k_moe1_gate_up8(MoeParams p) {
         if (blockIdx.x == 0) moe1_route(p, wave, t);
         return;
     }
-    const int sidx = (int)blockIdx.y - 1;
+    // grid rows 1..K hold route ranks K-1..0, row K+1 the shared expert: the
+    // ranks whose top-k takes the most rounds are dispatched first (M=1 layer
+    // 12.84 -> 12.70 us)
+    const int sidx = (int)blockIdx.y <= K ? K - (int)blockIdx.y : K;
     constexpr int LPB = 256 / VPL;
     const int g0 = quarter * NB;
     const int gx = g0 + lane / LPB;  // x block this lane quantises (waves 0-3)
