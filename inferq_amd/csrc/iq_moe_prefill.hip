@@ -152,13 +152,21 @@ __device__ __forceinline__ void block_scan(int (&v)[N], int* s_tmp /* [N][16] */
     }
 }
 
+// The 16-row chunk list is ordered by the work of a chunk: the shared
+// expert's full chunks, the routed groups' full chunks, then the partial
+// chunks by descending row count.  A chunk's workgroups run 13-17 us (one
+// per column tile) and the launch runs about four rounds of them per CU, so
+// the long ones go first and the short ones fill the last round (the order
+// changes which rows share a launch round, never a result).
 __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     extern __shared__ uint32_t s_mask[];  // [E][mw] token bitmask of each expert
     __shared__ int s_start[kMoeMaxExperts];
     __shared__ int s_tmp[64];
+    __shared__ int s_pcnt[kMpRows], s_pbase[kMpRows], s_pnext[kMpRows];  // partial chunks by rows
     const int tid = threadIdx.x;
     const int E = (int)p.E, K = (int)p.K, M = p.M, NA = M * K, mw = (M + 31) / 32;
     for (int i = tid; i < E * mw; i += kMpThreads) s_mask[i] = 0;
+    if (tid < kMpRows) s_pcnt[tid] = s_pnext[tid] = 0;
     __syncthreads();
     for (int a = tid; a < NA; a += kMpThreads) {
         const int t = a / K, e = p.experts[a];
@@ -168,22 +176,41 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     int cnt = 0;
     if (tid < E)
         for (int w = 0; w < mw; w++) cnt += __popc(s_mask[tid * mw + w]);
-    const int nch = (cnt + kMpRows - 1) / kMpRows;
+    const int nfull = cnt / kMpRows, rpart = cnt % kMpRows;  // full chunks, rows of the partial one (0: none)
     const int ntc = (cnt + kMpTileRows - 1) / kMpTileRows;
-    // group id, first grouped row, first chunk, first tile-order chunk
-    int sv[4] = {cnt > 0, cnt, nch, ntc}, tot[4];
+    // group id, first grouped row, first full chunk, first tile-order chunk
+    int sv[4] = {cnt > 0, cnt, nfull, ntc}, tot[4];
     block_scan<4>(sv, s_tmp, tot);
-    const int gid = sv[0], start = sv[1], cst = sv[2], tst = sv[3];
-    const int n_routed = tot[0], routed_chunks = tot[2], routed_tchunks = tot[3];
+    const int gid = sv[0], start = sv[1], cfs = sv[2], tst = sv[3];
+    const int n_routed = tot[0], routed_full = tot[2], routed_tchunks = tot[3];
+    const bool has_shared = p.sgate_w != nullptr;
+    const int sfull = has_shared ? M / kMpRows : 0, spart = has_shared ? M % kMpRows : 0;
+    if (tid < E && rpart > 0) atomicAdd(&s_pcnt[rpart], 1);
+    if (tid == 0 && spart > 0) atomicAdd(&s_pcnt[spart], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int b = sfull + routed_full;
+        for (int r = kMpRows - 1; r >= 1; r--) {
+            s_pbase[r] = b;
+            b += s_pcnt[r];
+        }
+        s_pbase[0] = b;  // the number of chunks
+    }
+    __syncthreads();
     if (tid < E) {
         s_start[tid] = start;
         if (cnt > 0) {
             p.group_expert[gid] = tid;
             p.group_start[gid] = start;
             p.group_count[gid] = cnt;
-            for (int j = 0; j < nch; j++) {
-                p.chunk_group[cst + j] = gid;
-                p.chunk_r0[cst + j] = kMpRows * j;
+            for (int j = 0; j < nfull; j++) {
+                p.chunk_group[sfull + cfs + j] = gid;
+                p.chunk_r0[sfull + cfs + j] = kMpRows * j;
+            }
+            if (rpart > 0) {
+                const int c = s_pbase[rpart] + atomicAdd(&s_pnext[rpart], 1);
+                p.chunk_group[c] = gid;
+                p.chunk_r0[c] = kMpRows * nfull;
             }
             for (int j = 0; j < ntc; j++) {
                 p.tchunk_group[tst + j] = gid;
@@ -203,8 +230,6 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
         p.assign_row[pos] = t;
         p.slot_pos[a] = pos;
     }
-    const bool has_shared = p.sgate_w != nullptr;
-    const int sch = has_shared ? (M + kMpRows - 1) / kMpRows : 0;
     const int stch = has_shared ? (M + kMpTileRows - 1) / kMpTileRows : 0;
     if (has_shared) {
         for (int t = tid; t < M; t += kMpThreads) p.assign_row[NA + t] = t;
@@ -212,10 +237,15 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
             p.group_expert[n_routed] = E;
             p.group_start[n_routed] = NA;
             p.group_count[n_routed] = M;
+            if (spart > 0) {
+                const int c = s_pbase[spart] + atomicAdd(&s_pnext[spart], 1);
+                p.chunk_group[c] = n_routed;
+                p.chunk_r0[c] = kMpRows * sfull;
+            }
         }
-        for (int j = tid; j < sch; j += kMpThreads) {
-            p.chunk_group[routed_chunks + j] = n_routed;
-            p.chunk_r0[routed_chunks + j] = kMpRows * j;
+        for (int j = tid; j < sfull; j += kMpThreads) {
+            p.chunk_group[j] = n_routed;
+            p.chunk_r0[j] = kMpRows * j;
         }
         for (int j = tid; j < stch; j += kMpThreads) {
             p.tchunk_group[routed_tchunks + j] = n_routed;
@@ -224,7 +254,7 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     }
     if (tid == 0) {
         p.meta[0] = n_routed + (has_shared ? 1 : 0);
-        p.meta[1] = routed_chunks + sch;
+        p.meta[1] = s_pbase[0];
         p.meta[2] = routed_tchunks + stch;
     }
 }
