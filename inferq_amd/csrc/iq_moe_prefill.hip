@@ -163,10 +163,12 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     __shared__ int s_start[kMoeMaxExperts];
     __shared__ int s_tmp[64];
     __shared__ int s_pcnt[kMpRows], s_pbase[kMpRows], s_pnext[kMpRows];  // partial chunks by rows
+    __shared__ int s_t1;  // tile-order chunks of one 16-row tile placed so far
     const int tid = threadIdx.x;
     const int E = (int)p.E, K = (int)p.K, M = p.M, NA = M * K, mw = (M + 31) / 32;
     for (int i = tid; i < E * mw; i += kMpThreads) s_mask[i] = 0;
     if (tid < kMpRows) s_pcnt[tid] = s_pnext[tid] = 0;
+    if (tid == 0) s_t1 = 0;
     __syncthreads();
     for (int a = tid; a < NA; a += kMpThreads) {
         const int t = a / K, e = p.experts[a];
@@ -177,14 +179,21 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
     if (tid < E)
         for (int w = 0; w < mw; w++) cnt += __popc(s_mask[tid * mw + w]);
     const int nfull = cnt / kMpRows, rpart = cnt % kMpRows;  // full chunks, rows of the partial one (0: none)
-    const int ntc = (cnt + kMpTileRows - 1) / kMpTileRows;
-    // group id, first grouped row, first full chunk, first tile-order chunk
-    int sv[4] = {cnt > 0, cnt, nfull, ntc}, tot[4];
+    // tile-order chunks: those of two 16-row tiles (full, or more than 16
+    // rows) first, then those of one
+    const int tpart = cnt % kMpTileRows;
+    const int nt2 = cnt / kMpTileRows + (tpart > 16 ? 1 : 0), nt1 = tpart > 0 && tpart <= 16 ? 1 : 0;
+    // group id, first grouped row, first full chunk, first two-tile tile-order chunk
+    int sv[4] = {cnt > 0, cnt, nfull, nt2}, tot[4];
     block_scan<4>(sv, s_tmp, tot);
     const int gid = sv[0], start = sv[1], cfs = sv[2], tst = sv[3];
-    const int n_routed = tot[0], routed_full = tot[2], routed_tchunks = tot[3];
+    const int n_routed = tot[0], routed_full = tot[2], routed_t2 = tot[3];
     const bool has_shared = p.sgate_w != nullptr;
     const int sfull = has_shared ? M / kMpRows : 0, spart = has_shared ? M % kMpRows : 0;
+    const int stpart = has_shared ? M % kMpTileRows : 0;
+    const int snt2 = has_shared ? M / kMpTileRows + (stpart > 16 ? 1 : 0) : 0;
+    const int snt1 = stpart > 0 && stpart <= 16 ? 1 : 0;
+    const int t1base = routed_t2 + snt2;  // the one-tile chunks follow every two-tile chunk
     if (tid < E && rpart > 0) atomicAdd(&s_pcnt[rpart], 1);
     if (tid == 0 && spart > 0) atomicAdd(&s_pcnt[spart], 1);
     __syncthreads();
@@ -212,9 +221,14 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
                 p.chunk_group[c] = gid;
                 p.chunk_r0[c] = kMpRows * nfull;
             }
-            for (int j = 0; j < ntc; j++) {
+            for (int j = 0; j < nt2; j++) {
                 p.tchunk_group[tst + j] = gid;
                 p.tchunk_r0[tst + j] = kMpTileRows * j;
+            }
+            if (nt1) {
+                const int c = t1base + atomicAdd(&s_t1, 1);
+                p.tchunk_group[c] = gid;
+                p.tchunk_r0[c] = kMpTileRows * nt2;
             }
         }
     }
@@ -230,7 +244,6 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
         p.assign_row[pos] = t;
         p.slot_pos[a] = pos;
     }
-    const int stch = has_shared ? (M + kMpTileRows - 1) / kMpTileRows : 0;
     if (has_shared) {
         for (int t = tid; t < M; t += kMpThreads) p.assign_row[NA + t] = t;
         if (tid == 0) {
@@ -247,15 +260,20 @@ __global__ __launch_bounds__(kMpThreads) void k_mp_group(MoeParams p) {
             p.chunk_group[j] = n_routed;
             p.chunk_r0[j] = kMpRows * j;
         }
-        for (int j = tid; j < stch; j += kMpThreads) {
-            p.tchunk_group[routed_tchunks + j] = n_routed;
-            p.tchunk_r0[routed_tchunks + j] = kMpTileRows * j;
+        for (int j = tid; j < snt2; j += kMpThreads) {
+            p.tchunk_group[routed_t2 + j] = n_routed;
+            p.tchunk_r0[routed_t2 + j] = kMpTileRows * j;
+        }
+        if (tid == 0 && snt1) {
+            const int c = t1base + atomicAdd(&s_t1, 1);
+            p.tchunk_group[c] = n_routed;
+            p.tchunk_r0[c] = kMpTileRows * snt2;
         }
     }
     if (tid == 0) {
         p.meta[0] = n_routed + (has_shared ? 1 : 0);
         p.meta[1] = s_pbase[0];
-        p.meta[2] = routed_tchunks + stch;
+        p.meta[2] = t1base + s_t1;
     }
 }
 
