@@ -557,6 +557,27 @@ def lm_head_lines(args, hip, device, cpu=None):
         res["lm_head_q6k_248320x2048_m1" if m == 1 else "lm_head_q6k_m8"] = measurement(
             "lm_head [248320x2048]", "Q6_K", 248320, 2048, st, m, t, "gpu:auto",
             moved=st + m * (2048 + 248320) * 4, **kw)
+        # greedy selection on the LM head (iq_matmul_argmax: the selection
+        # fused into the product), checked against the rule over the oracle's
+        # logits
+        idx = torch.empty(m, dtype=torch.int32, device=device)
+        val = torch.empty(m, dtype=torch.float32, device=device)
+
+        def select(i):
+            qgemm.check(qgemm.lib().iq_matmul_argmax(lm.handle, x.data_ptr(), m, idx.data_ptr(), val.data_ptr(),
+                                                     qgemm._stream()))
+
+        ta = time_graph(select, max(10, args.steps // 10), hip, warmup=2)
+        ka = {}
+        if cpu is not None:
+            select(0)
+            gi = idx.cpu().numpy()
+            want = [int(np.flatnonzero(r == r.max())[-1]) for r in np.asarray(ref, np.float32)]
+            ka = dict(diff=float(np.abs(val.cpu().numpy().astype(np.float64) - ref[np.arange(m), gi]).max()),
+                      bitexact=float(gi.tolist() == want))
+        res["lm_head_argmax_m1" if m == 1 else "lm_head_argmax_m8"] = measurement(
+            "lm_head [248320x2048] + greedy selection", "Q6_K", 248320, 2048, st, m, ta, "gpu:matmul_argmax",
+            moved=st + m * 2048 * 4, **ka)
     del lm, raw
     return res
 

@@ -221,7 +221,10 @@ int iq_argmax_rows(const float *y, int64_t m, int64_t n, int32_t *idx, float *va
 /* The LM head with greedy selection: idx/val as iq_argmax_rows over
  * x . W^T, whose logits (bitwise iq_matmul's) stay in the library workspace
  * and are never handed back -- a greedy decode step reads m indices
- * instead of m x rows floats.  With a leading_rows matrix it is the
+ * instead of m x rows floats.  Where the product runs on the one-row GEMV
+ * or the 2..8-row MFMA tile (the LM head), its kernel reduces the logits as
+ * it writes them and one small launch joins the partial maxima; the result
+ * is the same either way.  With a leading_rows matrix it is the
  * vocab-prefix draft head's selection.
  * Replaces: lm_head.forward followed by sampling::argmax
  * (src/qwen/quantized_model.rs:737-743, src/sampling.rs:104-110;

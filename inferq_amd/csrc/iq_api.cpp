@@ -255,12 +255,33 @@ size_t matmul_ws_bytes(const iq_weight* w, int64_t m) {
     return ap > d ? ap : d;
 }
 
-// Workspace of iq_matmul_argmax: the logits, the argmax partials and the
-// product's own workspace.
+// Greedy selection fused into the product (iq_matmul_argmax): 1 = one row
+// on the four-row-item GEMV, 2 = 2..8 rows on the pair-lane MFMA tile, 0 =
+// none (the product, then launch_argmax over its logits).
+int argmax_fusion(const iq_weight* w, int64_t m) {
+    const WeightView v = view_of(w);
+    if (m == 1 && gemv_argmax_supported(v)) return 1;
+    if (dense_argmax_supported(v, m)) return 2;
+    return 0;
+}
+
+// (key, logit) pairs per input row of a fused selection.
+int64_t argmax_fused_parts(const iq_weight* w, int64_t m) {
+    const int f = argmax_fusion(w, m);
+    return f == 1 ? gemv_argmax_parts(view_of(w)) : f == 2 ? dense_argmax_parts(view_of(w)) : 0;
+}
+
+// Workspace of iq_matmul_argmax: the logits, then either the argmax
+// partials and the product's own workspace or, fused, the pairs (keys,
+// then logits) and the product's workspace.
 size_t argmax_call_bytes(const iq_weight* w, int64_t m) {
     const size_t yb = ((size_t)(m * w->rows) * 4 + 255) & ~(size_t)255;
     const size_t ab = (argmax_workspace_size(m, w->rows) + 255) & ~(size_t)255;
-    return yb + ab + matmul_ws_bytes(w, m);
+    const size_t rest = ab + matmul_ws_bytes(w, m);
+    const size_t P = (size_t)(m * argmax_fused_parts(w, m));
+    const size_t fused = P ? ((P * 8 + 255) & ~(size_t)255) + ((P * 4 + 255) & ~(size_t)255) + matmul_ws_bytes(w, m)
+                           : 0;
+    return yb + (rest > fused ? rest : fused);
 }
 
 // Kernel choice of a product (iq_matmul_via's path argument).  Every path
@@ -582,6 +603,22 @@ IQ_API int iq_matmul_argmax(iq_weight_t w, const float* x, int64_t m, int32_t* i
     if (int rc = lease.acquire(argmax_call_bytes(w, m), s)) return rc;
     uint8_t* base = (uint8_t*)lease.ptr();
     float* y = (float*)base;
+    if (const int f = argmax_fusion(w, m)) {
+        // the product reduces its outputs as it writes them (per wave, or
+        // per workgroup and row), and one small launch joins the pairs
+        const int64_t parts = argmax_fused_parts(w, m);
+        const size_t P = (size_t)(m * parts);
+        const size_t kb = (P * 8 + 255) & ~(size_t)255, vb = (P * 4 + 255) & ~(size_t)255;
+        uint64_t* keys = (uint64_t*)(base + yb);
+        float* vals = (float*)(base + yb + kb);
+        int nparts = (int)parts;
+        hipError_t e = f == 1 ? launch_gemv_argmax(view_of(w), x, y, keys, vals, &nparts, s)
+                              : launch_dense_argmax(view_of(w), x, m, y, base + yb + kb + vb, keys, vals, s);
+        if (e != hipSuccess) return hip_fail(e, "matmul launch");
+        e = launch_argmax_kv(keys, vals, m, nparts, idx, val, s);
+        if (e != hipSuccess) return hip_fail(e, "argmax launch");
+        return IQ_OK;
+    }
     hipError_t e = launch_path(w, x, m, y, base + yb + ab, IQ_PATH_AUTO, nullptr, nullptr, s);
     if (e != hipSuccess) return hip_fail(e, "matmul launch");
     e = launch_argmax(y, m, w->rows, w->rows, idx, val, base + yb, s);

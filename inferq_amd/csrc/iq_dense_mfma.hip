@@ -28,6 +28,10 @@ struct DmArgs {
     int m;
     float* y;  // [m][ldy]
     int64_t ldy;
+    // fused greedy selection (k_dm_mm_pk): per input row r, workgroup b
+    // leaves its 64 columns' largest (argmax key, logit) at r * gridDim.x + b
+    uint64_t* amx_key = nullptr;
+    float* amx_val = nullptr;
 };
 
 // One wave per (row, 256-value block): Q8K (bit-exact from_float).
@@ -80,8 +84,9 @@ __global__ __launch_bounds__(256) void k_dm_mm(DmArgs a) {
 }
 
 // At most 8 input rows: 64 weight rows x the 8 rows per workgroup, two
-// reference lanes per MFMA (ml_product_pk).
-template <int FMT>
+// reference lanes per MFMA (ml_product_pk).  AMX: greedy selection fused
+// (DmArgs::amx_key).
+template <int FMT, bool AMX = false>
 __global__ __launch_bounds__(256) void k_dm_mm_pk(DmArgs a) {
     using L = MlStagePk<FMT>;
     __shared__ __align__(16) uint8_t st[2][L::END];
@@ -113,6 +118,42 @@ __global__ __launch_bounds__(256) void k_dm_mm_pk(DmArgs a) {
         for (int r = 0; r < 4; r++) {
             const int rr = 4 * q + r;
             if (rr < rows && n < a.n) a.y[(int64_t)rr * a.ldy + n] = v[r];
+        }
+    }
+    if constexpr (AMX) {
+        // lanes q and q + 2 hold the same outputs; the keys of lanes q < 2
+        // (input rows 4 q + r, column n) meet over the 16 columns of a lane
+        // group, then over the workgroup's four waves
+        __shared__ uint64_t s_k[4][8];
+        __shared__ float s_v[4][8];
+        uint64_t key[4];
+        float kv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = 4 * (q & 1) + r;
+            key[r] = q < 2 && rr < rows && n < a.n ? argmax_key(v[r], n) : 0;
+            kv[r] = v[r];
+            row16_max_kv(key[r], kv[r]);
+        }
+        if (q < 2 && jj == 0)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                s_k[wave][4 * q + r] = key[r];
+                s_v[wave][4 * q + r] = kv[r];
+            }
+        __syncthreads();
+        if (threadIdx.x < 8 && (int)threadIdx.x < rows) {
+            const int rr = threadIdx.x;
+            uint64_t bk = s_k[0][rr];
+            float bv = s_v[0][rr];
+            for (int w = 1; w < 4; w++)
+                if (s_k[w][rr] > bk) {
+                    bk = s_k[w][rr];
+                    bv = s_v[w][rr];
+                }
+            const int64_t o = (int64_t)rr * gridDim.x + blockIdx.x;
+            a.amx_key[o] = bk;
+            a.amx_val[o] = bv;
         }
     }
 }
@@ -185,7 +226,8 @@ hipError_t launch_sk(const DmArgs& a, hipStream_t s) {
 template <int FMT>
 hipError_t launch_pk(const DmArgs& a, hipStream_t s) {
     const dim3 grid((unsigned)((a.n + kMlCols - 1) / kMlCols));
-    hipLaunchKernelGGL((k_dm_mm_pk<FMT>), grid, dim3(256), 0, s, a);
+    if (a.amx_key) hipLaunchKernelGGL((k_dm_mm_pk<FMT, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_dm_mm_pk<FMT, false>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -256,8 +298,35 @@ hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, i
     return launch_dense_mfma_any(w, x, ldx, m, y, ldy, ws, s);
 }
 
+// The split-K tile's choice: up to 8 rows on mid-size matrices of width
+// 2048 or 4096.
+static bool dm_takes_sk(const WeightView& w, int64_t m) {
+    const int nb = (int)(w.cols / 256);
+    return m <= 8 && (nb == 8 || nb == 16) && w.rows * w.row_bytes <= kDmSkMaxBytes;
+}
+
+static hipError_t dense_run(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                            void* ws, uint64_t* amx_key, float* amx_val, hipStream_t s);
+
 hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                                  void* ws, hipStream_t s) {
+    return dense_run(w, x, ldx, m, y, ldy, ws, nullptr, nullptr, s);
+}
+
+bool dense_argmax_supported(const WeightView& w, int64_t m) {
+    return m >= 2 && m <= 8 && dense_mfma_supported(w, m) && !dm_takes_sk(w, m);
+}
+
+int64_t dense_argmax_parts(const WeightView& w) { return (w.rows + kMlCols - 1) / kMlCols; }
+
+hipError_t launch_dense_argmax(const WeightView& w, const float* x, int64_t m, float* y, void* ws, uint64_t* keys,
+                               float* vals, hipStream_t s) {
+    if (!dense_argmax_supported(w, m) || !keys || !vals) return hipErrorNotSupported;
+    return dense_run(w, x, w.cols, m, y, w.rows, ws, keys, vals, s);
+}
+
+static hipError_t dense_run(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                            void* ws, uint64_t* amx_key, float* amx_val, hipStream_t s) {
     if (!dm_layout_ok(w) || !dm_rows_ok(w, m)) return hipErrorNotSupported;
     const DmPlan P = dm_plan(w, m);
     uint8_t* base = (uint8_t*)ws;
@@ -272,12 +341,15 @@ hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ld
     a.m = (int)m;
     a.y = y;
     a.ldy = ldy;
+    a.amx_key = amx_key;
+    a.amx_val = amx_val;
     const int64_t qwaves = m * a.nb;
     hipLaunchKernelGGL(k_dm_quant, dim3((unsigned)((qwaves + 3) / 4)), dim3(256), 0, s, x, ldx, (int)m, a.nb,
                        (int8_t*)a.q, (float*)a.d, (_Float16*)a.hs);
     if (hipError_t e = hipGetLastError()) return e;
     // up to 8 rows: the split-K tile on mid-size matrices of width 2048 or 4096
-    const bool sk = m <= 8 && (a.nb == 8 || a.nb == 16) && w.rows * w.row_bytes <= kDmSkMaxBytes;
+    const bool sk = dm_takes_sk(w, m);
+    if (amx_key && (sk || m > 8)) return hipErrorNotSupported;  // fused selection: pair-lane tile only
     // 16-row tiles up to 16 rows, and wider where 32-row tiles would leave
     // the GPU short of workgroups (at most 256 of them for Q4_K, 128 for
     // Q6_K, whose 16-row tiles cost more): [2048 x 4096] Q4_K at 64 / 256

@@ -122,6 +122,61 @@ __device__ __forceinline__ float hsum4(float v) {
     return v;
 }
 
+// Greedy-selection key of logit v at index i (sampling::argmax,
+// src/sampling.rs:104-110): the order-preserving image of v in the high 32
+// bits and the index in the low 32, so the largest key is the largest value
+// and, among equal values, the largest index (the last of equal maxima);
+// non-finite values map to 0, below every finite value's key; -0 ranks
+// equal to +0.
+__device__ __forceinline__ uint64_t argmax_key(float v, int64_t i) {
+    if (!__builtin_isfinite(v)) return 0;
+    if (v == 0.f) v = 0.f;
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(uint32_t)i;
+}
+
+// One step of a (key, value) maximum across lanes `off` apart (keys are
+// unique but for 0, whose value is never used).
+__device__ __forceinline__ void max_kv_xor(uint64_t& key, float& val, int off) {
+    const uint32_t lo = __shfl_xor((uint32_t)key, off), hi = __shfl_xor((uint32_t)(key >> 32), off);
+    const float ov = __shfl_xor(val, off);
+    const uint64_t ok = ((uint64_t)hi << 32) | lo;
+    if (ok > key) {
+        key = ok;
+        val = ov;
+    }
+}
+
+// One step of the same maximum with the partner lane given by a DPP
+// permutation within each row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ void max_kv_dpp(uint64_t& key, float& val) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)key, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(key >> 32), CTRL, 0xF, 0xF, false);
+    const float ov = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, val), CTRL, 0xF, 0xF, false));
+    const uint64_t ok = ((uint64_t)hi << 32) | lo;
+    if (ok > key) {
+        key = ok;
+        val = ov;
+    }
+}
+
+// The largest (key, value) pair of each row of 16 lanes, in every lane of
+// the row: quad swaps, then the half-row and row mirrors.
+__device__ __forceinline__ void row16_max_kv(uint64_t& key, float& val) {
+    max_kv_dpp<0xB1>(key, val);   // quad_perm [1,0,3,2]
+    max_kv_dpp<0x4E>(key, val);   // quad_perm [2,3,0,1]
+    max_kv_dpp<0x141>(key, val);  // row_half_mirror
+    max_kv_dpp<0x140>(key, val);  // row_mirror
+}
+
+// The largest (key, value) pair of the wave, in every lane.
+__device__ __forceinline__ void wave_max_kv(uint64_t& key, float& val) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) max_kv_xor(key, val, off);
+}
+
 // Correctly rounded exp for f32 arguments: exp is evaluated in double and
 // rounded once.  glibc's expf (what the reference's f32::exp calls) agrees
 // with it except where glibc itself misrounds a near-midpoint case.

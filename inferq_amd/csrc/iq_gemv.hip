@@ -82,6 +82,10 @@ struct GemvArgs {
     float* y;
     int64_t ldy;
     int act_lds;  // bytes of the activation tile in LDS
+    // fused greedy selection (one input row): wave w of workgroup b leaves
+    // its rows' largest (argmax key, logit) at index 4 b + w
+    uint64_t* amx_key = nullptr;
+    float* amx_val = nullptr;
 };
 
 // Activation tile in LDS: q [MT][nu][256] (lane-transposed groups),
@@ -255,10 +259,11 @@ __device__ __forceinline__ Q8Dec q8_decode_lds(const uint8_t* b, int k) {
 
 // ---- the kernel ----------------------------------------------------------------
 
-template <int FMT, int MT, int RPW, int NBUF>
+template <int FMT, int MT, int RPW, int NBUF, bool AMX = false>
 __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
     using G = GvGeom<FMT, RPW>;
     static_assert(RPW == 8 || (RPW == 4 && MT == 1), "four-row items: one input row");
+    static_assert(!AMX || MT == 1, "fused greedy selection: one input row");
     constexpr int UPL = RPW == 8 ? G::SU : G::SU / 2;  // units of a slice per lane
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -296,6 +301,20 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
     // no items reads group 0, which always exists.
     const int gbase = nitems > 0 ? grp0 : 0;
     const int ilast = nitems > 0 ? nitems - 1 : 0;
+    // fused greedy selection: the largest key among this lane's rows, and
+    // its logit; every wave leaves its pair (key 0 when it had no rows)
+    uint64_t bk = 0;
+    float bv = 0.f;
+    auto amx_finish = [&]() {
+        if constexpr (AMX) {
+            wave_max_kv(bk, bv);
+            if (lane == 0) {
+                const int64_t wi = (int64_t)blockIdx.x * 4 + wave;
+                p.amx_key[wi] = bk;
+                p.amx_val[wi] = bv;
+            }
+        }
+    };
     auto issue = [&](u32x4a16 (&st)[G::NL], int it_) {
         const int it = min(it_, ilast);
         const int g8 = gbase + (it / nsl) * gstride, sl = it - (it / nsl) * nsl;
@@ -372,7 +391,10 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
         if constexpr (NBUF == 2) issue(stB, 1);
     }
     lds_barrier();
-    if (nitems == 0) return;  // uniform per wave; no barrier follows
+    if (nitems == 0) {  // uniform per wave; no barrier follows
+        amx_finish();
+        return;
+    }
 
     const ActLds<FMT, MT> act(smem, p.nu);
     uint8_t* wl = smem + p.act_lds + wave * G::WAVE_LDS;
@@ -509,7 +531,16 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
             for (int mi = 0; mi < MT; mi++) {
                 float v = hsum8(acc[mi]);
                 if constexpr (FMT == kQ4_K) v = v + hsum4(accm[mi]);
-                if (k == 0 && half == 0 && row < p.n && (MT == 1 || mi < mc)) p.y[(int64_t)(m0 + mi) * p.ldy + row] = v;
+                if (k == 0 && half == 0 && row < p.n && (MT == 1 || mi < mc)) {
+                    p.y[(int64_t)(m0 + mi) * p.ldy + row] = v;
+                    if constexpr (AMX) {
+                        const uint64_t key = argmax_key(v, row);
+                        if (key > bk) {
+                            bk = key;
+                            bv = v;
+                        }
+                    }
+                }
                 acc[mi] = accm[mi] = 0.f;
             }
         }
@@ -525,6 +556,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
             if (it + 1 < nitems) issue(stA, it + 1);
             compute(it);
         }
+        amx_finish();
         return;
     }
     // Two items per trip with one exit at the bottom: every path through
@@ -538,6 +570,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs& p) {
         issue(stB, it + 3);
         if (it + 1 < nitems) compute(it + 1);
     }
+    amx_finish();
 }
 
 template <int FMT, int MT>
@@ -550,9 +583,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs p) {
 // workgroups per CU, whose waves have nothing to overlap with but their own
 // next slice (Q8_0 [4096 x 2048] 6.9 -> 6.3 us, [4096 x 4096] 9.8 -> 8.2 us;
 // [16384 x 2048] 11.3 against 13.0 us the other way round).
-template <int FMT, int NBUF>
+// AMX: greedy selection fused (GemvArgs::amx_key).
+template <int FMT, int NBUF, bool AMX = false>
 __global__ __launch_bounds__(256, NBUF == 1 ? 4 : 3) void k_gemv4(GemvArgs p) {
-    gemv_run<FMT, 1, 4, NBUF>(p);
+    gemv_run<FMT, 1, 4, NBUF, AMX>(p);
 }
 
 struct DevLimits {
@@ -576,14 +610,14 @@ const DevLimits& limits() {
     return L;
 }
 
-template <int FMT, int MT, int RPW, int NBUF>
+template <int FMT, int MT, int RPW, int NBUF, bool AMX = false>
 const void* kfn() {
-    if constexpr (RPW == 4) return (const void*)k_gemv4<FMT, NBUF>;
+    if constexpr (RPW == 4) return (const void*)k_gemv4<FMT, NBUF, AMX>;
     else return (const void*)k_gemv<FMT, MT>;
 }
 // Workgroups per CU the kernel's registers allow at `lds` bytes of LDS,
 // queried once per LDS size (0: unknown).
-template <int FMT, int MT, int RPW, int NBUF>
+template <int FMT, int MT, int RPW, int NBUF, bool AMX = false>
 int occupancy(size_t lds) {
     static std::atomic<long long> cache[8];  // (lds << 8) | blocks; 0 = empty
     for (auto& c : cache) {
@@ -592,7 +626,7 @@ int occupancy(size_t lds) {
         if ((size_t)(v >> 8) == lds) return (int)(v & 0xff);
     }
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn<FMT, MT, RPW, NBUF>(), 256, lds) != hipSuccess) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn<FMT, MT, RPW, NBUF, AMX>(), 256, lds) != hipSuccess) {
         (void)hipGetLastError();  // clear this query's own error
         return 0;
     }
@@ -604,8 +638,8 @@ int occupancy(size_t lds) {
     return occ;
 }
 
-template <int FMT, int MT, int RPW = 8, int NBUF = 2>
-hipError_t launch_t(GemvArgs args, hipStream_t s) {
+template <int FMT, int MT, int RPW = 8, int NBUF = 2, bool AMX = false>
+hipError_t launch_t(GemvArgs args, hipStream_t s, int* nparts = nullptr) {
     using G = GvGeom<FMT, RPW>;
     args.act_lds = act_lds_bytes<FMT, MT>(args.nu);
     args.groups = (int)((args.n + RPW - 1) / RPW);
@@ -613,7 +647,7 @@ hipError_t launch_t(GemvArgs args, hipStream_t s) {
     const DevLimits& L = limits();
     if (lds > (size_t)L.lds_block) return hipErrorNotSupported;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(kfn<FMT, MT, RPW, NBUF>(), hipFuncAttributeMaxDynamicSharedMemorySize,
+        hipError_t e = hipFuncSetAttribute(kfn<FMT, MT, RPW, NBUF, AMX>(), hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds);
         if (e != hipSuccess) {
             (void)hipGetLastError();
@@ -621,14 +655,24 @@ hipError_t launch_t(GemvArgs args, hipStream_t s) {
         }
     }
     int per_cu = (int)(L.lds_cu / lds);
-    const int occ = occupancy<FMT, MT, RPW, NBUF>(lds);
+    const int occ = occupancy<FMT, MT, RPW, NBUF, AMX>(lds);
     if (occ > 0 && occ < per_cu) per_cu = occ;
     const int64_t wgs = ((int64_t)args.groups + 3) / 4;
     const int64_t cap = (int64_t)L.cus * (per_cu < 1 ? 1 : per_cu);
     dim3 grid((unsigned)(wgs < cap ? wgs : cap), (unsigned)((args.m + MT - 1) / MT));
-    if constexpr (RPW == 4) hipLaunchKernelGGL((k_gemv4<FMT, NBUF>), grid, dim3(256), lds, s, args);
+    if (nparts) *nparts = (int)grid.x * 4;
+    if constexpr (RPW == 4) hipLaunchKernelGGL((k_gemv4<FMT, NBUF, AMX>), grid, dim3(256), lds, s, args);
     else hipLaunchKernelGGL((k_gemv<FMT, MT>), grid, dim3(256), lds, s, args);
     return hipGetLastError();
+}
+
+// One input row on four-row items: one slice in flight where the grid fills
+// the GPU twice over, two otherwise.
+template <int FMT, bool AMX>
+hipError_t launch_one_row(const GemvArgs& args, hipStream_t s, int* nparts) {
+    const int64_t wgs = ((args.n + 3) / 4 + 3) / 4 * args.m;  // four-row items, one-row tiles
+    if (wgs < 2 * (int64_t)limits().cus) return launch_t<FMT, 1, 4, 2, AMX>(args, s, nparts);
+    return launch_t<FMT, 1, 4, 1, AMX>(args, s, nparts);
 }
 
 // Input rows per tile: the fewest tiles that still give every SIMD a few
@@ -642,11 +686,7 @@ hipError_t launch_fmt(const GemvArgs& args, hipStream_t s) {
     const int mt_min = args.nu <= 16 ? 1 : 2;  // one-row tiles quantise at most 16 groups
     while (mt > mt_min && (int64_t)args.groups * ((m + mt - 1) / mt) < 2048) mt /= 2;
     switch (mt) {
-    case 1: {
-        const int64_t wgs = ((args.n + 3) / 4 + 3) / 4 * m;  // four-row items, one-row tiles
-        if (wgs < 2 * (int64_t)limits().cus) return launch_t<FMT, 1, 4, 2>(args, s);
-        return launch_t<FMT, 1, 4, 1>(args, s);
-    }
+    case 1: return launch_one_row<FMT, false>(args, s, nullptr);
     case 2: return launch_t<FMT, 2>(args, s);
     case 4: return launch_t<FMT, 4>(args, s);
     default: return launch_t<FMT, 8>(args, s);
@@ -938,6 +978,39 @@ hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t
     case kQ4_K: return launch_fmt<kQ4_K>(args, s);
     case kQ6_K: return launch_fmt<kQ6_K>(args, s);
     case kQ8_0: return launch_fmt<kQ8_0>(args, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// The dispatch runs one-row products on the four-row-item kernel wherever
+// the split kernel does not take them (launch_gemv above): the LM head
+// (417 MB, past kSkMaxBytes), Q8_0 matrices, other widths.
+bool gemv_argmax_supported(const WeightView& w) { return gemv_supported(w, 1) && !sk_supported(w); }
+
+// Waves of the four-row-item grid at most: four per workgroup, one
+// workgroup per four items of four rows.
+int64_t gemv_argmax_parts(const WeightView& w) { return ((w.rows + 3) / 4 + 3) / 4 * 4; }
+
+hipError_t launch_gemv_argmax(const WeightView& w, const float* x, float* y, uint64_t* keys, float* vals, int* nparts,
+                              hipStream_t s) {
+    if (!gemv_argmax_supported(w) || !keys || !vals || !nparts) return hipErrorNotSupported;
+    GemvArgs args;
+    args.w = w.w;
+    args.n = w.rows;
+    args.row_bytes = w.row_bytes;
+    args.nu = (int)(w.cols / 256);
+    args.x = x;
+    args.ldx = w.cols;
+    args.m = 1;
+    args.y = y;
+    args.ldy = w.rows;
+    args.act_lds = 0;
+    args.amx_key = keys;
+    args.amx_val = vals;
+    switch (w.dtype) {
+    case kQ4_K: return launch_one_row<kQ4_K, true>(args, s, nparts);
+    case kQ6_K: return launch_one_row<kQ6_K, true>(args, s, nparts);
+    case kQ8_0: return launch_one_row<kQ8_0, true>(args, s, nparts);
     default: return hipErrorInvalidValue;
     }
 }

@@ -89,4 +89,25 @@ size_t argmax_workspace_size(int64_t m, int64_t n);
 hipError_t launch_argmax(const float* y, int64_t m, int64_t n, int64_t ldy, int32_t* idx, float* val, void* ws,
                          hipStream_t s);
 
+// Greedy selection fused into the product.  Where gemv_argmax_supported
+// (one input row, iq_gemv.hip), launch_gemv_argmax computes y = x . W^T as
+// launch_gemv does (the same bits) and also leaves each wave's largest
+// (argmax key, logit) pair of its rows in keys / vals, *nparts of them (at
+// most gemv_argmax_parts).  Where dense_argmax_supported (2..8 input rows on
+// the pair-lane MFMA tile, iq_dense_mfma.hip), launch_dense_argmax does the
+// same per workgroup and input row: pair (r, b) at r * dense_argmax_parts +
+// b, with `ws` as launch_dense_mfma's.  launch_argmax_kv (iq_argmax.hip)
+// then reduces m rows of nparts pairs to each row's index and value, as
+// launch_argmax would from y.
+bool gemv_argmax_supported(const WeightView& w);
+int64_t gemv_argmax_parts(const WeightView& w);
+hipError_t launch_gemv_argmax(const WeightView& w, const float* x, float* y, uint64_t* keys, float* vals, int* nparts,
+                              hipStream_t s);
+bool dense_argmax_supported(const WeightView& w, int64_t m);
+int64_t dense_argmax_parts(const WeightView& w);
+hipError_t launch_dense_argmax(const WeightView& w, const float* x, int64_t m, float* y, void* ws, uint64_t* keys,
+                               float* vals, hipStream_t s);
+hipError_t launch_argmax_kv(const uint64_t* keys, const float* vals, int64_t m, int nparts, int32_t* idx, float* val,
+                            hipStream_t s);
+
 }  // namespace iq

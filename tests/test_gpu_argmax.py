@@ -99,3 +99,95 @@ def test_vocab_prefix_draft_head(gpu, lm_head):
     full = lm_head.forward(x).cpu().numpy()
     idx, _ = draft.forward_argmax(x)
     assert idx.cpu().numpy().tolist() == [ref_argmax(r[:32768]) for r in full]
+
+
+def _check_selection(mat, x, what):
+    """forward_argmax against the rule over forward()'s logits: indices
+    equal, values bit-identical to the logits they index."""
+    logits = mat.forward(x).cpu().numpy()
+    idx, val = mat.forward_argmax(x)
+    idx, val = idx.cpu().numpy(), val.cpu().numpy()
+    assert idx.tolist() == [ref_argmax(r) for r in logits], what
+    assert_bitexact(val, logits[np.arange(len(idx)), idx], what)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 2048), (3, 2048), (5, 1024), (4099, 2048), (40961, 4096), (65537, 3072)])
+def test_one_row_fused_selection_ragged_shapes(gpu, rows, cols):
+    """At one input row the selection is fused into the four-row-item
+    product (every Q8_0 matrix takes it): each wave reduces its own rows,
+    one launch joins the waves.  Row counts that leave partial items,
+    partial workgroups and waves without rows."""
+    t = S.random_matrix_device(S.Q8_0, rows, cols, gpu, 7000 + rows)
+    mat = Q.QuantizedMatrix.view(t, S.Q8_0, rows, cols)
+    x = torch.randn(1, cols, device=gpu, generator=torch.Generator(device=gpu).manual_seed(rows))
+    _check_selection(mat, x, f"fused selection [{rows} x {cols}] Q8_0")
+
+
+@pytest.mark.parametrize("dtype,period,reps", [(S.Q8_0, 7, 10001), (S.Q6_K, 61, 700), (S.Q4_K, 13, 5000)])
+def test_one_row_fused_selection_ties_across_waves(gpu, dtype, period, reps):
+    """Rows repeating with a short period give bit-equal logits at indices
+    spread over every wave and workgroup: the LAST of the equal maxima must
+    win (Rust's max_by).  The Q6_K and Q4_K matrices are past the split
+    kernel's 64 MiB, as the LM head is, so they take the fused product
+    too."""
+    base = S.random_matrix_device(dtype, period, 2048, gpu, 7100 + period)
+    t = base.repeat(reps)
+    rows = period * reps
+    mat = Q.QuantizedMatrix.view(t, dtype, rows, 2048)
+    x = torch.randn(1, 2048, device=gpu, generator=torch.Generator(device=gpu).manual_seed(period))
+    logits = mat.forward(x).cpu().numpy()[0]
+    assert np.array_equal(logits[:period].view(np.uint32), logits[-period:].view(np.uint32))
+    want = ref_argmax(logits)
+    assert want >= rows - period  # the last period holds the last maximum
+    _check_selection(mat, x, f"ties, period {period}")
+
+
+def test_one_row_fused_selection_in_graph_replays(gpu, lm_head):
+    """The fused selection captured after a reserve, replayed with eager
+    work between the replays: every replay equals the eager call."""
+    g = torch.Generator(device=gpu).manual_seed(99)
+    xs = [torch.randn(1, 2048, device=gpu, generator=g) for _ in range(3)]
+    x = torch.empty(1, 2048, device=gpu)
+    idx = torch.empty(1, dtype=torch.int32, device=gpu)
+    val = torch.empty(1, dtype=torch.float32, device=gpu)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        lm_head.reserve(1)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            Q.check(Q.lib().iq_matmul_argmax(lm_head.handle, x.data_ptr(), 1, idx.data_ptr(), val.data_ptr(),
+                                             Q._stream()))
+    for xi in xs:
+        x.copy_(xi)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want_i, want_v = lm_head.forward_argmax(xi)
+        torch.cuda.synchronize()
+        assert idx.cpu().tolist() == want_i.cpu().tolist()
+        assert_bitexact(val.cpu().numpy(), want_v.cpu().numpy(), "graph replay of the fused selection")
+
+
+@pytest.mark.parametrize("m", [2, 3, 5, 8])
+def test_verify_width_fused_selection(gpu, lm_head, m):
+    """At 2..8 rows on a large matrix the selection is fused into the
+    pair-lane MFMA tile (each workgroup reduces its 64 columns per input
+    row): the same indices and values as the rule over the logits."""
+    x = torch.randn(m, 2048, device=gpu, generator=torch.Generator(device=gpu).manual_seed(300 + m))
+    _check_selection(lm_head, x, f"LM head fused selection m={m}")
+
+
+@pytest.mark.parametrize("dtype,period,reps,m", [(S.Q6_K, 61, 700, 4), (S.Q4_K, 13, 5000, 8), (S.Q6_K, 64, 667, 3)])
+def test_verify_width_fused_selection_ties(gpu, dtype, period, reps, m):
+    """Periodic rows (bit-equal logits in every workgroup) on the pair-lane
+    tile, and a row count that leaves a partial last workgroup (61 x 700 =
+    42700 = 667 x 64 + 12): the last of the equal maxima wins in every
+    input row."""
+    base = S.random_matrix_device(dtype, period, 2048, gpu, 7200 + period)
+    t = base.repeat(reps)
+    rows = period * reps
+    mat = Q.QuantizedMatrix.view(t, dtype, rows, 2048)
+    x = torch.randn(m, 2048, device=gpu, generator=torch.Generator(device=gpu).manual_seed(period + m))
+    logits = mat.forward(x).cpu().numpy()
+    assert all(ref_argmax(r) >= rows - period for r in logits)
+    _check_selection(mat, x, f"fused selection ties, period {period}, m={m}")
