@@ -41,16 +41,23 @@
 extern "C" {
 #endif
 
-/* GGML type ids as carried by GGUF (the reference's GgmlDType). */
-/* Q5_K runs on the lane kernel in ggml's published vec_dot_q5_K_q8_K order
- * (the reference hands it to candle's per-row vec_dot, src/gguf.rs:593). */
-enum iq_dtype { IQ_Q8_0 = 8, IQ_Q4_K = 12, IQ_Q5_K = 13, IQ_Q6_K = 14 };
+/* GGML type ids as carried by GGUF (the reference's GgmlDType).  The
+ * executable matrix dtypes are the reference's (QuantizedMatrix::new,
+ * src/gguf.rs:305-317).  Q5_K runs on the lane kernel in ggml's published
+ * vec_dot_q5_K_q8_K order (the reference hands it to candle's per-row
+ * vec_dot, src/gguf.rs:593).  F32 and BF16 matrices, which the reference
+ * multiplies through candle's f32 matmul (no multi-row kernel,
+ * src/gguf.rs:533-535, :599), take an f32 product in a fixed order of this
+ * library's (the MoE router's: per lane over k = lane + 64 j, then a
+ * butterfly), within 1e-4 of the reference and bitwise the same at every
+ * row count; they have no fixed kernel paths and no per-block sums. */
+enum iq_dtype { IQ_F32 = 0, IQ_Q8_0 = 8, IQ_Q4_K = 12, IQ_Q5_K = 13, IQ_Q6_K = 14, IQ_BF16 = 30 };
 
 enum iq_status {
     IQ_OK = 0,
     IQ_ERR_INVALID = -1, /* null handle / pointer, bad argument */
     IQ_ERR_SHAPE = -2,   /* width not a whole number of blocks, wrong input width, size mismatch */
-    IQ_ERR_DTYPE = -3,   /* dtype outside {Q8_0, Q4_K, Q5_K, Q6_K}, mismatched dtypes, or no kernel */
+    IQ_ERR_DTYPE = -3,   /* dtype outside {F32, BF16, Q8_0, Q4_K, Q5_K, Q6_K}, mismatched dtypes, or no kernel */
     IQ_ERR_OOM = -4,     /* device allocation failed */
     IQ_ERR_HIP = -5,     /* HIP runtime error (launch, copy, no device) */
     IQ_ERR_RANGE = -6    /* index out of range (expert, rows) */

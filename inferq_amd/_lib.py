@@ -12,6 +12,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libiq_qgemm.so")
 
 IQ_Q8_0, IQ_Q4_K, IQ_Q5_K, IQ_Q6_K = 8, 12, 13, 14
+IQ_F32, IQ_BF16 = 0, 30  # unquantised matrices (the reference's F32 / BF16 QuantizedMatrix)
 # enum iq_path (the reference's MultiRowPath, src/gguf.rs:43-62)
 PATH_AUTO, PATH_LANES, PATH_GEMV, PATH_LANE_MFMA, PATH_PREFILL_TILES = 0, 1, 2, 3, 4
 IQ_OK = 0

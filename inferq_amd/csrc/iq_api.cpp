@@ -39,6 +39,8 @@ int hip_fail(hipError_t e, const char* what) {
 
 const char* dtype_name(int dtype) {
     switch (dtype) {
+    case kF32: return "F32";
+    case kBF16: return "BF16";
     case kQ4_K: return "Q4K";
     case kQ5_K: return "Q5K";
     case kQ6_K: return "Q6K";
@@ -47,9 +49,14 @@ const char* dtype_name(int dtype) {
     }
 }
 
-int64_t block_elems(int dtype) { return dtype == kQ8_0 ? 32 : 256; }
-int64_t block_bytes(int dtype) { return dtype == kQ4_K ? 144 : dtype == kQ5_K ? 176 : dtype == kQ6_K ? 210 : 34; }
-bool dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0; }
+bool float_dtype(int dtype) { return dtype == kF32 || dtype == kBF16; }
+int64_t block_elems(int dtype) { return float_dtype(dtype) ? 1 : dtype == kQ8_0 ? 32 : 256; }
+int64_t block_bytes(int dtype) {
+    return dtype == kF32 ? 4 : dtype == kBF16 ? 2 : dtype == kQ4_K ? 144 : dtype == kQ5_K ? 176 : dtype == kQ6_K ? 210 : 34;
+}
+bool dtype_ok(int dtype) {
+    return dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0 || float_dtype(dtype);
+}
 bool moe_dtype_ok(int dtype) { return dtype == kQ4_K || dtype == kQ5_K || dtype == kQ6_K || dtype == kQ8_0; }
 
 namespace {
@@ -194,8 +201,8 @@ WeightView view_of(const iq_weight* w) {
 // src/gguf.rs:627-646).
 int check_matrix(int dtype, int64_t rows, int64_t cols, size_t nbytes, int64_t* row_bytes) {
     if (!dtype_ok(dtype))
-        return fail(IQ_ERR_DTYPE, "unsupported executable GGUF matrix dtype %d; expected Q4_K, Q5_K, Q6_K or Q8_0",
-                    dtype);
+        return fail(IQ_ERR_DTYPE,
+                    "unsupported executable GGUF matrix dtype %d; expected Q4_K, Q5_K, Q6_K, Q8_0, F32, or BF16", dtype);
     if (rows <= 0 || cols <= 0) return fail(IQ_ERR_SHAPE, "invalid matrix shape [%lld, %lld]", (long long)rows,
                                              (long long)cols);
     if (cols % block_elems(dtype))
@@ -249,6 +256,7 @@ int quantize_for(const iq_weight* w, const float* x, int64_t m, const ActView& a
 // Device workspace a product of m rows needs (activation quantisation, and
 // for the int8-MFMA path its layouts and split-K partial tiles).
 size_t matmul_ws_bytes(const iq_weight* w, int64_t m) {
+    if (float_dtype(w->dtype)) return 0;  // the f32 product reads x as it is
     const size_t a = act_bytes(m, w->cols), p = prefill_workspace_size(view_of(w), m);
     const size_t d = dense_mfma_workspace_any(view_of(w), m);
     const size_t ap = a > p ? a : p;
@@ -290,6 +298,10 @@ hipError_t launch_path(const iq_weight* w, const float* x, int64_t m, float* y, 
                        int32_t* msum, hipStream_t s) {
     const WeightView v = view_of(w);
     hipError_t e = hipErrorNotSupported;
+    // F32 / BF16: one f32 product, no fixed kernel paths (the reference has
+    // no multi-row kernel for them either) and no per-block integers
+    if (float_dtype(w->dtype))
+        return path == IQ_PATH_AUTO && !isum ? launch_float_mm(v, x, w->cols, m, y, w->rows, s) : hipErrorNotSupported;
     if (path == IQ_PATH_AUTO) {
         if (!isum && dense_mfma_supported(v, m)) e = launch_dense_mfma(v, x, w->cols, m, y, w->rows, ws, s);
         if (e == hipErrorNotSupported && !isum && gemv_supported(v, m)) e = launch_gemv(v, x, w->cols, m, y, w->rows, s);

@@ -8,10 +8,12 @@
 namespace iq {
 
 // GGML type ids (GGUF dtype codes).
+constexpr int kF32 = 0;
 constexpr int kQ8_0 = 8;
 constexpr int kQ4_K = 12;
 constexpr int kQ5_K = 13;
 constexpr int kQ6_K = 14;
+constexpr int kBF16 = 30;
 
 // Quantised activations in the internal (lane-transposed) layout.
 struct ActView {
@@ -81,6 +83,11 @@ hipError_t launch_dense_mfma(const WeightView& w, const float* x, int64_t ldx, i
                              void* ws, hipStream_t s);
 hipError_t launch_dense_mfma_any(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                                  void* ws, hipStream_t s);
+
+// y[m][ldy] = x . W^T for F32 and BF16 matrices (iq_dense_f32.hip), in the
+// MoE router's f32 order; hipErrorNotSupported for other dtypes.
+hipError_t launch_float_mm(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
+                           hipStream_t s);
 
 // Greedy selection over logit rows y [m][ldy] (iq_argmax.hip): idx[r] the
 // last index of the largest finite value of row r (-1 when none is finite),

@@ -13,11 +13,11 @@ import ctypes
 import numpy as np
 
 from . import _lib
-from ._lib import IQ_Q4_K, IQ_Q5_K, IQ_Q6_K, IQ_Q8_0, QgemmError, check, lib
+from ._lib import IQ_BF16, IQ_F32, IQ_Q4_K, IQ_Q5_K, IQ_Q6_K, IQ_Q8_0, QgemmError, check, lib
 
-DTYPE_NAMES = {IQ_Q4_K: "Q4K", IQ_Q5_K: "Q5K", IQ_Q6_K: "Q6K", IQ_Q8_0: "Q8_0"}
-BLOCK_ELEMS = {IQ_Q4_K: 256, IQ_Q5_K: 256, IQ_Q6_K: 256, IQ_Q8_0: 32}
-BLOCK_BYTES = {IQ_Q4_K: 144, IQ_Q5_K: 176, IQ_Q6_K: 210, IQ_Q8_0: 34}
+DTYPE_NAMES = {IQ_Q4_K: "Q4K", IQ_Q5_K: "Q5K", IQ_Q6_K: "Q6K", IQ_Q8_0: "Q8_0", IQ_F32: "F32", IQ_BF16: "BF16"}
+BLOCK_ELEMS = {IQ_Q4_K: 256, IQ_Q5_K: 256, IQ_Q6_K: 256, IQ_Q8_0: 32, IQ_F32: 1, IQ_BF16: 1}
+BLOCK_BYTES = {IQ_Q4_K: 144, IQ_Q5_K: 176, IQ_Q6_K: 210, IQ_Q8_0: 34, IQ_F32: 4, IQ_BF16: 2}
 
 _initialised = set()
 

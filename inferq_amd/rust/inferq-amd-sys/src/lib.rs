@@ -11,6 +11,9 @@ pub const IQ_Q8_0: c_int = 8;
 pub const IQ_Q4_K: c_int = 12;
 pub const IQ_Q5_K: c_int = 13;
 pub const IQ_Q6_K: c_int = 14;
+/// Unquantised matrices (the reference's F32 / BF16 QuantizedMatrix).
+pub const IQ_F32: c_int = 0;
+pub const IQ_BF16: c_int = 30;
 
 pub const IQ_OK: c_int = 0;
 pub const IQ_ERR_INVALID: c_int = -1;

@@ -62,6 +62,13 @@ def test_upload_rejects_malformed_matrices(L):
     _err(L, L.iq_weights_upload(None, 144, _lib.IQ_Q4_K, 1, 256, ctypes.byref(h)), _lib.IQ_ERR_INVALID)
     _err(L, L.iq_weights_view(p + 4, 144, _lib.IQ_Q4_K, 1, 256, ctypes.byref(h)), _lib.IQ_ERR_INVALID,
          "16-byte aligned")
+    # F32 and BF16 are executable matrix dtypes (src/gguf.rs:305-317) with
+    # one element per "block"; F16 is not
+    _err(L, L.iq_weights_upload(p, 10, _lib.IQ_F32, 2, 3, ctypes.byref(h)), _lib.IQ_ERR_SHAPE,
+         "quantized matrix has 10 bytes, expected 24")
+    _err(L, L.iq_weights_upload(p, 10, _lib.IQ_BF16, 2, 3, ctypes.byref(h)), _lib.IQ_ERR_SHAPE, "expected 12")
+    _err(L, L.iq_weights_upload(p, 12, 1, 2, 3, ctypes.byref(h)), _lib.IQ_ERR_DTYPE,
+         "expected Q4_K, Q5_K, Q6_K, Q8_0, F32, or BF16")
 
 
 def test_null_handles_are_rejected(L):
