@@ -742,14 +742,22 @@ __global__ __launch_bounds__(256) void k_gemv1_sk(const uint8_t* __restrict__ w,
         uint32_t av[8];
         load_act(a, 0, g, k, av);
         const float yd = a.d[g];
-        if constexpr (FMT == kQ4_K) {
-            const Q4Dec dec = q4_decode(wb[0][b], k);
+        if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+            Q4Dec dec;
+            if constexpr (FMT == kQ4_K) dec = q4_decode(wb[0][b], k);
+            else dec = q5_decode(wb[0][b], k);
             const uint32_t q8s = *(const uint32_t*)(a.s8 + g * 8 + 2 * (k & 3));
             int32_t isum, msum;
             float d, dmin;
             q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
             s_isum[slot][k][g] = isum;
-            if (k < 4) s_msum[slot][k][g] = msum;
+            if constexpr (FMT == kQ5_K) {
+                // the Q5_K mins: one integer per (row, block), one f32 scalar per row
+                const int32_t mtot = isum_quad(msum);
+                if (k == 0) s_msum[slot][0][g] = mtot;
+            } else if (k < 4) {
+                s_msum[slot][k][g] = msum;
+            }
             if (k == 0) {
                 s_dd[slot][g] = d;
                 s_dm[slot][g] = dmin;
@@ -770,9 +778,11 @@ __global__ __launch_bounds__(256) void k_gemv1_sk(const uint8_t* __restrict__ w,
     for (int g = 0; g < NG; g++) {
         acc = __builtin_fmaf(s_dd[slot][g], (float)s_isum[slot][k][g], acc);
         if constexpr (FMT == kQ4_K) accm = __builtin_fmaf(s_dm[slot][g], (float)s_msum[slot][k & 3][g], accm);
+        if constexpr (FMT == kQ5_K) accm = accm + s_dm[slot][g] * (float)s_msum[slot][0][g];
     }
     float v = hsum8(acc);
     if constexpr (FMT == kQ4_K) v = v + hsum4(accm);
+    if constexpr (FMT == kQ5_K) v = v + accm;
     if (k == 0 && i < n) y[i] = v;
 }
 
@@ -827,8 +837,10 @@ __global__ __launch_bounds__(256) void k_gemv_sk(const uint8_t* __restrict__ w, 
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         const int g = g0 + b;
-        if constexpr (FMT == kQ4_K) {
-            const Q4Dec dec = q4_decode(wb[0][b], k);
+        if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+            Q4Dec dec;
+            if constexpr (FMT == kQ4_K) dec = q4_decode(wb[0][b], k);
+            else dec = q5_decode(wb[0][b], k);
 #pragma unroll
             for (int r = 0; r < MT; r++) {
                 if (r < mc) {  // uniform
@@ -840,7 +852,12 @@ __global__ __launch_bounds__(256) void k_gemv_sk(const uint8_t* __restrict__ w, 
                     float d, dmin;
                     q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
                     s_isum[r][slot][k][g] = isum;
-                    if (k < 4) s_msum[r][slot][k][g] = msum;
+                    if constexpr (FMT == kQ5_K) {
+                        const int32_t mtot = isum_quad(msum);  // one f32 mins scalar per row
+                        if (k == 0) s_msum[r][slot][0][g] = mtot;
+                    } else if (k < 4) {
+                        s_msum[r][slot][k][g] = msum;
+                    }
                     if (k == 0) {
                         s_dd[r][slot][g] = d;
                         s_dm[r][slot][g] = dmin;
@@ -871,9 +888,11 @@ __global__ __launch_bounds__(256) void k_gemv_sk(const uint8_t* __restrict__ w, 
         for (int g = 0; g < NG; g++) {
             acc = __builtin_fmaf(s_dd[r][slot][g], (float)s_isum[r][slot][k][g], acc);
             if constexpr (FMT == kQ4_K) accm = __builtin_fmaf(s_dm[r][slot][g], (float)s_msum[r][slot][k & 3][g], accm);
+            if constexpr (FMT == kQ5_K) accm = accm + s_dm[r][slot][g] * (float)s_msum[r][slot][0][g];
         }
         float v = hsum8(acc);
         if constexpr (FMT == kQ4_K) v = v + hsum4(accm);
+        if constexpr (FMT == kQ5_K) v = v + accm;
         if (k == 0 && i < n) y[(int64_t)(m0 + r) * ldy + i] = v;
     }
 }
@@ -916,6 +935,8 @@ hipError_t launch_sk(const WeightView& w, const float* x, float* y, hipStream_t 
 constexpr int64_t kSkMaxBytes = (int64_t)64 << 20;
 bool sk_supported(const WeightView& w) {
     if (w.cols != 2048 && w.cols != 4096) return false;
+    // Q5_K has no LDS-staged kernel to stream better, so any size
+    if (w.dtype == kQ5_K) return ((uintptr_t)w.w & 15) == 0;
     if (w.rows * w.row_bytes > kSkMaxBytes) return false;
     if (w.dtype == kQ4_K) return ((uintptr_t)w.w & 15) == 0;
     if (w.dtype == kQ6_K) return ((uintptr_t)w.w & 3) == 0;
@@ -931,6 +952,10 @@ bool sk_supported(const WeightView& w) {
 // matrices go to the lane kernel (iq_lanes.hip).
 bool gemv_supported(const WeightView& w, int64_t m) {
     if (m < 1 || m >= kPrefillMinRows || w.rows < 1) return false;
+    // Q5_K: the split kernels only, one to eight rows (the reference keeps
+    // Q5_K on its per-row path, src/gguf.rs:588-593; the lane order is the
+    // same)
+    if (w.dtype == kQ5_K) return m <= 8 && w.rows <= (int64_t)1 << 31 && sk_supported(w);
     const int64_t bytes = w.rows * w.row_bytes;
     if (m > 8 && bytes > (m <= 16 ? (int64_t)64 << 20 : (int64_t)8 << 20)) return false;
     const int64_t nu = w.cols / 256;
@@ -947,9 +972,14 @@ bool gemv_supported(const WeightView& w, int64_t m) {
 hipError_t launch_gemv(const WeightView& w, const float* x, int64_t ldx, int64_t m, float* y, int64_t ldy,
                        hipStream_t s) {
     if (!gemv_supported(w, m)) return hipErrorNotSupported;
-    if (m == 1 && sk_supported(w)) return w.dtype == kQ4_K ? launch_sk<kQ4_K>(w, x, y, s) : launch_sk<kQ6_K>(w, x, y, s);
+    if (m == 1 && sk_supported(w))
+        return w.dtype == kQ4_K ? launch_sk<kQ4_K>(w, x, y, s)
+                                : w.dtype == kQ5_K ? launch_sk<kQ5_K>(w, x, y, s) : launch_sk<kQ6_K>(w, x, y, s);
     if (m == 2 && sk_supported(w))
-        return w.dtype == kQ4_K ? launch_sk2<kQ4_K>(w, x, ldx, y, ldy, s) : launch_sk2<kQ6_K>(w, x, ldx, y, ldy, s);
+        return w.dtype == kQ4_K ? launch_sk2<kQ4_K>(w, x, ldx, y, ldy, s)
+                                : w.dtype == kQ5_K ? launch_sk2<kQ5_K>(w, x, ldx, y, ldy, s)
+                                                   : launch_sk2<kQ6_K>(w, x, ldx, y, ldy, s);
+    if (w.dtype == kQ5_K) return launch_sk_rows<kQ5_K>(w, x, ldx, m, y, ldy, s);  // 3..8 rows
     // Three to eight rows as single-row tiles of the split kernel while the
     // tiles total at most 4096 workgroups at width 2048 (768 at width 4096,
     // whose tiles quantise and chain twice the blocks); past that the

@@ -299,6 +299,8 @@ __device__ __forceinline__ void lanes_load_exact(const uint8_t* const (&wrow)[R]
         for (int g = 0; g < NG; g++) {
             if constexpr (FMT == kQ4_K) {
                 load_q4(wrow[r] + (int64_t)g * 144, k, w[r][g]);
+            } else if constexpr (FMT == kQ5_K) {
+                load_q5(wrow[r] + (int64_t)g * 176, k, w[r][g]);
             } else if constexpr (NG % 2 == 0) {
                 // rows of an even number of 210-byte blocks are 4-byte
                 // aligned, so block g starts at 2g (mod 4)

@@ -77,3 +77,22 @@ def test_moe_refuses_unknown_expert_dtypes(gpu):
     t = torch.zeros(4 * 256 * 176, dtype=torch.uint8, device=gpu)
     with pytest.raises(Q.QgemmError, match="unsupported expert dtypes"):
         MOE.QuantizedMoeLayer(256, 256, 4, 2, 2, S.Q6_K, t, t, t)  # 2 = Q4_0, not executable
+
+
+@pytest.mark.parametrize("cols", [2048, 4096])
+def test_q5k_split_kernels_equal_the_lane_kernel(gpu, cols):
+    """At one to eight rows of width 2048 or 4096 the dispatch runs Q5_K on
+    the split-K kernels (each wave forms a quarter of the blocks' exact
+    lane integers, one chain per row in block order, the mins as one f32
+    scalar per row); every row count gives the lane kernel's bits."""
+    from inferq_amd import _lib
+
+    rng = np.random.default_rng(cols)
+    rows = 1000
+    mat = Q.QuantizedMatrix.upload(S.random_matrix(Q5, rows, cols, rng), Q5, rows, cols)
+    for m in (1, 2, 3, 4, 6, 7, 8):
+        x = torch.from_numpy(S.normal((m, cols), np.random.default_rng(m))).to(gpu)
+        assert_bitexact(mat.forward(x).cpu().numpy(), mat.forward_via(x, _lib.PATH_LANES).cpu().numpy(),
+                        f"Q5_K [{rows} x {cols}] m={m} split vs lanes")
+        assert_bitexact(mat.forward_via(x, _lib.PATH_GEMV).cpu().numpy(), mat.forward(x).cpu().numpy(),
+                        f"Q5_K m={m} gemv path")
