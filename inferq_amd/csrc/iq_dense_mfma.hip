@@ -249,7 +249,7 @@ constexpr int64_t kDmSkMaxBytes = (int64_t)64 << 20;
 // alignment (Q6_K: an even block count per row).
 bool dm_layout_ok(const WeightView& w) {
     if (w.cols % 256 != 0 || w.rows < 1) return false;
-    if (w.dtype == kQ4_K) return ((uintptr_t)w.w & 15) == 0;
+    if (w.dtype == kQ4_K || w.dtype == kQ5_K) return ((uintptr_t)w.w & 15) == 0;
     if (w.dtype == kQ6_K) return ((uintptr_t)w.w & 3) == 0 && w.row_bytes % 4 == 0;
     return false;
 }
@@ -278,6 +278,9 @@ static bool dm_rows_ok(const WeightView& w, int64_t m) {
 
 bool dense_mfma_supported(const WeightView& w, int64_t m) {
     if (m < 2 || !dm_layout_ok(w) || !dm_rows_ok(w, m)) return false;
+    // Q5_K: the 16- and 32-row tiles from 9 rows (up to 8 rows the split-K
+    // GEMV or the lane kernel take it)
+    if (w.dtype == kQ5_K) return m >= 9;
     if (m >= kPrefillMinRows) return true;
     const int64_t bytes = w.rows * w.row_bytes, MiB = (int64_t)1 << 20;
     if (bytes >= 64 * MiB) return true;
@@ -350,6 +353,7 @@ static hipError_t dense_run(const WeightView& w, const float* x, int64_t ldx, in
     // up to 8 rows: the split-K tile on mid-size matrices of width 2048 or 4096
     const bool sk = dm_takes_sk(w, m);
     if (amx_key && (sk || m > 8)) return hipErrorNotSupported;  // fused selection: pair-lane tile only
+    if (w.dtype == kQ5_K && m <= 8) return hipErrorNotSupported;  // Q5_K: row tiles only
     // 16-row tiles up to 16 rows, and wider where 32-row tiles would leave
     // the GPU short of workgroups (at most 256 of them for Q4_K, 128 for
     // Q6_K, whose 16-row tiles cost more): [2048 x 4096] Q4_K at 64 / 256
@@ -357,7 +361,8 @@ static hipError_t dense_run(const WeightView& w, const float* x, int64_t ldx, in
     // 21.7 -> 18.2 us; from 512 workgroups the 32-row tiles win (Q6_K
     // [8192 x 2048] at 256 rows 45.4 against 59.5 us)
     const int64_t g32 = (w.rows + kMlCols - 1) / kMlCols * ((m + 31) / 32);
-    const bool rt1 = m <= 16 || g32 <= (w.dtype == kQ4_K ? 256 : 128);
+    const bool rt1 = m <= 16 || g32 <= (w.dtype == kQ6_K ? 128 : 256);
+    if (w.dtype == kQ5_K) return rt1 ? launch_t<kQ5_K, 1>(a, s) : launch_t<kQ5_K, 2>(a, s);
     if (w.dtype == kQ4_K)
         return sk ? launch_sk<kQ4_K>(a, s) : m <= 8 ? launch_pk<kQ4_K>(a, s)
                                        : rt1 ? launch_t<kQ4_K, 1>(a, s) : launch_t<kQ4_K, 2>(a, s);

@@ -18,7 +18,10 @@
 // folded in.  Scaled weights exceed int8, so each is split into two int8
 // streams whose integer sums recombine exactly: Q4_K sc*q = 8 (sc >> 3) q +
 // (sc & 7) q; Q6_K sc*(q - 32) = 256 hi + lo with hi in -16..16 and lo in
-// -128..127.  The Q4_K mins msum_k = m_2k s_2k + m_2k+1 s_2k+1 (s = 32-value
+// -128..127; Q5_K (q = nibble + 16 bit) into three, 8 (sc >> 3) nibble +
+// (sc & 7) nibble + 16 sc bit.  Q5_K's mins join one f32 scalar per row
+// and block, summs = summs + dmin * (m . s) (ggml's vec_dot_q5_K_q8_K), the
+// integer m . s from one f16 MFMA (exact: integers below 2^24).  The Q4_K mins msum_k = m_2k s_2k + m_2k+1 s_2k+1 (s = 32-value
 // activation sums) come from an f16 MFMA over the 16-value sums (integers
 // below 2^24: exact).  A lane keeps the f32 chains of all eight reference
 // lanes for its outputs and joins them at the end in the hsum trees' order,
@@ -46,6 +49,15 @@ struct MlFmt<kQ4_K> {
     static constexpr int BB = 144;  // block bytes
     static constexpr int BS = 144;  // LDS bytes per staged row-block
     static constexpr int NL = 9;    // staging loads per row-block (16 bytes each)
+    static constexpr bool kMins = true;
+};
+// Q5_K (ml_product only): the Q4_K header, qh at 16..47, qs at 48..175;
+// 176-byte columns (11 groups of 16 bytes, coprime with the 16 bank groups)
+template <>
+struct MlFmt<kQ5_K> {
+    static constexpr int BB = 176;
+    static constexpr int BS = 176;
+    static constexpr int NL = 11;
     static constexpr bool kMins = true;
 };
 template <>
@@ -273,9 +285,11 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
         // distinct bank groups, where eight 4-byte reads per block would
         // put four lanes on each bank
         u32x4a16 qs4[2] = {};
+        u32x4a16 qh4[2] = {};  // Q5_K: qh bytes 0..31 (dword k: the fifth bits of lane k)
         // Q6_K: the lane's ql and qh windows for reference lanes k = 0..7
         uint32_t l0s[8] = {}, l1s[8] = {}, qhs[8] = {};
-        if constexpr (FMT == kQ4_K) {
+        if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+            constexpr int QO = FMT == kQ5_K ? 48 : 16;  // offset of qs
             const u32x4a16 hdr = *(const u32x4a16*)bcol;
             xd = f16_to_f32(hdr.x);
             xdm = f16_to_f32(hdr.x >> 16);
@@ -283,8 +297,12 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
             const uint32_t sw = q < 2 ? sc.sc_lo : sc.sc_hi;
             s6a = byte_of(sw, 2 * (q & 1));
             s6b = byte_of(sw, 2 * (q & 1) + 1);
-            qs4[0] = *(const u32x4a16*)(bcol + 16 + 32 * q);
-            qs4[1] = *(const u32x4a16*)(bcol + 32 + 32 * q);
+            qs4[0] = *(const u32x4a16*)(bcol + QO + 32 * q);
+            qs4[1] = *(const u32x4a16*)(bcol + QO + 16 + 32 * q);
+            if constexpr (FMT == kQ5_K) {
+                qh4[0] = *(const u32x4a16*)(bcol + 16);
+                qh4[1] = *(const u32x4a16*)(bcol + 32);
+            }
         } else {
             xd = f16_to_f32(ml_lds_win(bcol, sh, 208) & 0xffffu);
             q6s = ml_lds_win(bcol, sh, 192 + 4 * q);
@@ -300,15 +318,22 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            uint32_t w1[2], w2[2];
-            int mul;  // isum = mul * (stream 1) + (stream 2)
-            if constexpr (FMT == kQ4_K) {
+            uint32_t w1[2], w2[2], w3[2] = {0u, 0u};
+            int mul;  // isum = mul * (stream 1) + (stream 2) (+ 16 * (stream 3), Q5_K)
+            if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
                 const uint32_t qd = qs4[k >> 2][k & 3];
                 const uint32_t lo = qd & 0x0f0f0f0fu, hi = (qd >> 4) & 0x0f0f0f0fu;
                 w1[0] = bytes_mul_small(lo, s6a >> 3);
                 w1[1] = bytes_mul_small(hi, s6b >> 3);
                 w2[0] = bytes_mul_small(lo, s6a & 7u);
                 w2[1] = bytes_mul_small(hi, s6b & 7u);
+                if constexpr (FMT == kQ5_K) {
+                    // fifth bits of chunks 2q, 2q + 1 (bits 2q, 2q + 1 of
+                    // qh bytes 4k .. 4k + 3), each byte 0 or the scale
+                    const uint32_t qhd = qh4[k >> 2][k & 3];
+                    w3[0] = bytes_mul_small((qhd >> (2 * q)) & 0x01010101u, s6a);
+                    w3[1] = bytes_mul_small((qhd >> (2 * q + 1)) & 0x01010101u, s6b);
+                }
                 mul = 8;
             } else {
                 const int hk = k >= 4;
@@ -325,15 +350,21 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
             }
             const long b1 = (long)(((uint64_t)w1[1] << 32) | w1[0]);
             const long b2 = (long)(((uint64_t)w2[1] << 32) | w2[0]);
+            const long b3 = (long)(((uint64_t)w3[1] << 32) | w3[0]);
 #pragma unroll
             for (int t = 0; t < RT; t++) {
                 const long a = *(const long*)(S + L::A + (16 * t + jj) * kMlAS + 32 * k + 8 * q);
                 const v4i_ml z = {};
                 const v4i_ml i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, z, 0, 0, 0);
                 const v4i_ml i2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b2, z, 0, 0, 0);
+                v4i_ml i3 = z;
+                if constexpr (FMT == kQ5_K) i3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b3, z, 0, 0, 0);
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc[k][4 * t + r] = __builtin_fmaf(dd[4 * t + r], (float)(i1[r] * mul + i2[r]), acc[k][4 * t + r]);
+                for (int r = 0; r < 4; r++) {
+                    int32_t isum = i1[r] * mul + i2[r];
+                    if constexpr (FMT == kQ5_K) isum += 16 * i3[r];
+                    acc[k][4 * t + r] = __builtin_fmaf(dd[4 * t + r], (float)isum, acc[k][4 * t + r]);
+                }
             }
             // one lane's products at a time: the chains are advanced here
             // (not sunk to the end of the block), which bounds the live
@@ -342,7 +373,26 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
             for (int r = 0; r < 4 * RT; r++) asm volatile("" : "+v"(acc[k][r]));
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (F::kMins) {
+        if constexpr (FMT == kQ5_K) {
+            // m . s over the whole block in one f16 MFMA (lane group q
+            // supplies mins 2q, 2q + 1 against 16-value sums 4q .. 4q + 3),
+            // then summs = summs + dmin * (m . s) per row, held in accm[0]
+            const uint32_t mwd = q < 2 ? sc.mn_lo : sc.mn_hi;
+            const _Float16 mA = (_Float16)(float)byte_of(mwd, 2 * (q & 1));
+            const _Float16 mB = (_Float16)(float)byte_of(mwd, 2 * (q & 1) + 1);
+            const v4h_ml bm = {mA, mA, mB, mB};
+#pragma unroll
+            for (int t = 0; t < RT; t++) {
+                const v4h_ml am = *(const v4h_ml*)(S + L::H + (16 * t + jj) * 32 + 8 * q);
+                const v4f_ml z = {};
+                const v4f_ml ms = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, z, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) accm[0][4 * t + r] = accm[0][4 * t + r] + dm[4 * t + r] * ms[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 4 * RT; r++) asm volatile("" : "+v"(accm[0][r]));
+            __builtin_amdgcn_sched_barrier(0);
+        } else if constexpr (F::kMins) {
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const uint32_t mwd = k < 2 ? sc.mn_lo : sc.mn_hi;
@@ -372,7 +422,8 @@ __device__ __forceinline__ void ml_product(const MlOperands& op, ARow arow, BRow
 #pragma unroll
     for (int r = 0; r < 4 * RT; r++) {
         v[r] = ((acc[0][r] + acc[4][r]) + (acc[2][r] + acc[6][r])) + ((acc[1][r] + acc[5][r]) + (acc[3][r] + acc[7][r]));
-        if constexpr (F::kMins) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
+        if constexpr (FMT == kQ5_K) v[r] = v[r] + accm[0][r];  // the mins scalar
+        else if constexpr (F::kMins) v[r] = v[r] + ((accm[0][r] + accm[2][r]) + (accm[1][r] + accm[3][r]));
     }
 }
 

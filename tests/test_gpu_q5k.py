@@ -96,3 +96,20 @@ def test_q5k_split_kernels_equal_the_lane_kernel(gpu, cols):
                         f"Q5_K [{rows} x {cols}] m={m} split vs lanes")
         assert_bitexact(mat.forward_via(x, _lib.PATH_GEMV).cpu().numpy(), mat.forward(x).cpu().numpy(),
                         f"Q5_K m={m} gemv path")
+
+
+@pytest.mark.parametrize("rows,cols", [(1000, 2048), (200, 4096), (64, 1024), (5, 256)])
+def test_q5k_mfma_tiles_equal_the_lane_kernel(gpu, rows, cols):
+    """From 9 rows the dispatch runs Q5_K on the exact lane-order int8 MFMA
+    tiles (three scaled-weight streams, the mins as one f32 scalar per row
+    and block from one f16 MFMA): the lane kernel's bits at every row count,
+    16- and 32-row tiles, ragged row and column tiles."""
+    from inferq_amd import _lib
+
+    rng = np.random.default_rng(rows + 7 * cols)
+    mat = Q.QuantizedMatrix.upload(S.random_matrix(Q5, rows, cols, rng), Q5, rows, cols)
+    for m in (9, 17, 33, 64, 100, 256):
+        x = torch.from_numpy(S.normal((m, cols), np.random.default_rng(m))).to(gpu)
+        lanes = mat.forward_via(x, _lib.PATH_LANES).cpu().numpy()
+        assert_bitexact(mat.forward(x).cpu().numpy(), lanes, f"Q5_K [{rows} x {cols}] m={m} MFMA vs lanes")
+        assert_bitexact(mat.forward_via(x, _lib.PATH_LANE_MFMA).cpu().numpy(), lanes, f"Q5_K m={m} explicit path")
