@@ -639,7 +639,8 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
 // kMoeTokenMajorMax tokens; other calls take the grouped paths.
 bool moe1_supported(const MoeParams& p, int gfmt, int dfmt) {
     const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
-    const bool fmts = (gfmt == kQ4_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ6_K);
+    // down experts also in Q5_K (the lane kernel's products, its mins scalar)
+    const bool fmts = (gfmt == kQ4_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ5_K || dfmt == kQ6_K);
     return p.M >= 1 && p.M <= kMoeTokenMajorMax && fmts && p.H == 2048 && p.I == 512 && nslots <= kMoe1MaxSlots &&
            p.E <= kMoeMaxExperts;
 }
@@ -692,6 +693,7 @@ template <int GFMT>
 hipError_t launch_moe1_g(const MoeParams& p, int dfmt, hipStream_t s, hipEvent_t const* ev) {
     switch (dfmt) {
     case kQ4_K: return launch_moe1<GFMT, kQ4_K>(p, s, ev);
+    case kQ5_K: return launch_moe1<GFMT, kQ5_K>(p, s, ev);
     case kQ6_K: return launch_moe1<GFMT, kQ6_K>(p, s, ev);
     default: return hipErrorInvalidValue;
     }
@@ -874,6 +876,8 @@ hipError_t launch_moe_stage(const MoeParams& p, int gfmt, int dfmt, int stage, h
     if (gfmt == kQ4_K && dfmt == kQ4_K) return launch_moe1_stage<kQ4_K, kQ4_K>(p, stage, s);
     if (gfmt == kQ6_K && dfmt == kQ6_K) return launch_moe1_stage<kQ6_K, kQ6_K>(p, stage, s);
     if (gfmt == kQ6_K && dfmt == kQ4_K) return launch_moe1_stage<kQ6_K, kQ4_K>(p, stage, s);
+    if (gfmt == kQ4_K && dfmt == kQ5_K) return launch_moe1_stage<kQ4_K, kQ5_K>(p, stage, s);
+    if (gfmt == kQ6_K && dfmt == kQ5_K) return launch_moe1_stage<kQ6_K, kQ5_K>(p, stage, s);
     return hipErrorNotSupported;
 }
 

@@ -334,13 +334,17 @@ __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
     // of a lane is then row 4 (q & 1) + r (every lane group), else row
     // 16 (r / 4) + 4 q + r % 4
     float v[4 * kMpRT];
-    const bool pk = rows <= 8;  // uniform per workgroup
+    // uniform per workgroup; Q5_K (down products only) has no pair-lane form
+    // and takes the 16-row tile for every chunk
+    const bool pk = FMT != kQ5_K && rows <= 8;
     if (pk) {
-        ((uint32_t*)zero)[threadIdx.x & 63] = 0u;  // read only after the product's first barrier
-        float vp[4];
-        ml_product_pk<FMT>(op, arow, brow, (uint8_t (*)[LP::END])lds, zero, vp);
+        if constexpr (FMT != kQ5_K) {
+            ((uint32_t*)zero)[threadIdx.x & 63] = 0u;  // read only after the product's first barrier
+            float vp[4];
+            ml_product_pk<FMT>(op, arow, brow, (uint8_t (*)[LP::END])lds, zero, vp);
 #pragma unroll
-        for (int r = 0; r < 4 * kMpRT; r++) v[r] = r < 4 ? vp[r] : 0.f;
+            for (int r = 0; r < 4 * kMpRT; r++) v[r] = r < 4 ? vp[r] : 0.f;
+        }
     } else {
         ml_product<FMT, kMpRT>(op, arow, brow, st, v);
     }
@@ -617,7 +621,7 @@ __global__ __launch_bounds__(256) void k_mp_actq(MoeParams p, int P) {
     const Q8KLane r = quant_q8k_core(load4(p.act + row * p.I + (int64_t)b * 256 + 4 * lane));
     ((uint32_t*)(p.aq.q + row * p.aq.ldq + (int64_t)b * 256))[perm_dword(lane >> 3, lane & 7)] = r.packed;
     if (lane == 0) p.aq.d[row * p.aq.ldd + b] = r.d;
-    if constexpr (DFMT == kQ4_K)
+    if constexpr (DFMT == kQ4_K || DFMT == kQ5_K)  // the down products' mins
         if ((lane & 3) == 0) p.ahs[(row * nb + b) * 16 + (lane >> 2)] = (_Float16)(float)r.bsum16;
 }
 
@@ -688,7 +692,10 @@ hipError_t launch_p(const MoeParams& p, hipStream_t s, hipEvent_t const* ev) {
     hipLaunchKernelGGL((k_mp_actq<DFMT>), dim3((unsigned)((aw + 3) / 4)), dim3(256), 0, s, p, P);
     if (hipError_t e = hipGetLastError()) return e;
     if (ev) (void)hipEventRecord(ev[2], s);
-    if (p.down_tiles && p.d_nbw == 2 && p.H % (kMlCols * kMpResCT) == 0)
+    if constexpr (DFMT == kQ5_K) {  // no tile-order form: the exact products on either path
+        hipLaunchKernelGGL((k_mp_mm<DFMT, 1>), dim3((unsigned)((p.H + kMlCols - 1) / kMlCols), (unsigned)p.max_chunks),
+                           dim3(256), 0, s, p);
+    } else if (p.down_tiles && p.d_nbw == 2 && p.H % (kMlCols * kMpResCT) == 0)
         hipLaunchKernelGGL((k_mp_down_res<DFMT, 2, kMpResCT>), dim3((unsigned)(p.H / (kMlCols * kMpResCT)),
                            (unsigned)p.max_tchunks), dim3(256), 0, s, p);
     else if (p.down_tiles)
@@ -713,16 +720,16 @@ int moep_max_chunks(int64_t M, int64_t K, int64_t E, int rows) {
 }
 
 bool moep_supported(const MoeParams& p, int gfmt, int dfmt) {
-    const bool kq = (gfmt == kQ4_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ6_K);
+    const bool kq = (gfmt == kQ4_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ5_K || dfmt == kQ6_K);
     auto al = [](const void* q, uintptr_t a) { return q == nullptr || ((uintptr_t)q & (a - 1)) == 0; };
-    const uintptr_t ga = gfmt == kQ4_K ? 16 : 4, da = dfmt == kQ4_K ? 16 : 4;
+    const uintptr_t ga = gfmt == kQ4_K ? 16 : 4, da = dfmt == kQ6_K ? 4 : 16;
     const bool aligned = al(p.gate, ga) && al(p.up, ga) && al(p.sgate_w, ga) && al(p.sup_w, ga) && al(p.down, da) &&
                          al(p.sdown_w, da) && al(p.out, 16) &&
                          al(p.residual, 16);  // k_mp_combine moves four floats at a time
     return kq && aligned && p.M >= kMoePrefillMinTokens && p.H % 256 == 0 && p.I % 256 == 0 && p.E <= kMoeMaxExperts &&
            p.K <= kMoeMaxTopK && p.g_row_bytes % 4 == 0 && p.d_row_bytes % 4 == 0 &&
            (int64_t)p.E * ((p.M + 31) / 32) * 4 <= 32768 && p.xhs != nullptr && p.chunk_group != nullptr &&
-           (dfmt != kQ4_K || p.ahs != nullptr);
+           ((dfmt != kQ4_K && dfmt != kQ5_K) || p.ahs != nullptr);
 }
 
 hipError_t launch_moe_prefill(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hipEvent_t const* ev) {
@@ -731,6 +738,8 @@ hipError_t launch_moe_prefill(const MoeParams& p, int gfmt, int dfmt, hipStream_
     if (gfmt == kQ4_K && dfmt == kQ4_K) return launch_p<kQ4_K, kQ4_K>(p, s, ev);
     if (gfmt == kQ6_K && dfmt == kQ6_K) return launch_p<kQ6_K, kQ6_K>(p, s, ev);
     if (gfmt == kQ6_K && dfmt == kQ4_K) return launch_p<kQ6_K, kQ4_K>(p, s, ev);
+    if (gfmt == kQ4_K && dfmt == kQ5_K) return launch_p<kQ4_K, kQ5_K>(p, s, ev);
+    if (gfmt == kQ6_K && dfmt == kQ5_K) return launch_p<kQ6_K, kQ5_K>(p, s, ev);
     return hipErrorNotSupported;
 }
 
