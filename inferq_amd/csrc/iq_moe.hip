@@ -419,14 +419,21 @@ __global__ __launch_bounds__(512) void k_moe1_gate_up8(MoeParams p) {
         uint32_t av[8];
         load_act(a, 0, g, k, av);
         const float yd = a.d[g];
-        if constexpr (GFMT == kQ4_K) {
-            const Q4Dec dec = q4_decode(w[0][b], k);
+        if constexpr (GFMT == kQ4_K || GFMT == kQ5_K) {
+            Q4Dec dec;
+            if constexpr (GFMT == kQ4_K) dec = q4_decode(w[0][b], k);
+            else dec = q5_decode(w[0][b], k);
             const uint32_t q8s = *(const uint32_t*)(a.s8 + g * 8 + 2 * (k & 3));
             int32_t isum, msum;
             float d, dmin;
             q4_dot(dec, av, yd, q8s, isum, msum, d, dmin);
             s_isum[r][slot][k][g] = isum;
-            if (k < 4) s_msum[r][slot][k][g] = msum;
+            if constexpr (GFMT == kQ5_K) {  // the Q5_K mins: one f32 scalar per row
+                const int32_t mtot = isum_quad(msum);
+                if (k == 0) s_msum[r][slot][0][g] = mtot;
+            } else if (k < 4) {
+                s_msum[r][slot][k][g] = msum;
+            }
             if (k == 0) {
                 s_dd[r][slot][g] = d;
                 s_dm[r][slot][g] = dmin;
@@ -451,9 +458,11 @@ __global__ __launch_bounds__(512) void k_moe1_gate_up8(MoeParams p) {
             acc = __builtin_fmaf(s_dd[rr][slot][g], (float)s_isum[rr][slot][k][g], acc);
             if constexpr (GFMT == kQ4_K)
                 accm = __builtin_fmaf(s_dm[rr][slot][g], (float)s_msum[rr][slot][k & 3][g], accm);
+            if constexpr (GFMT == kQ5_K) accm = accm + s_dm[rr][slot][g] * (float)s_msum[rr][slot][0][g];
         }
         float v = hsum8(acc);
         if constexpr (GFMT == kQ4_K) v = v + hsum4(accm);
+        if constexpr (GFMT == kQ5_K) v = v + accm;
         o[rr] = v;
     }
     // SwiGLU as the reference writes it: (g / (1 + exp(-g))) * u
@@ -639,8 +648,9 @@ __global__ __launch_bounds__(1024) void k_moe1_down(MoeParams p) {
 // kMoeTokenMajorMax tokens; other calls take the grouped paths.
 bool moe1_supported(const MoeParams& p, int gfmt, int dfmt) {
     const int nslots = (int)p.K + (p.sdown_w ? 1 : 0);
-    // down experts also in Q5_K (the lane kernel's products, its mins scalar)
-    const bool fmts = (gfmt == kQ4_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ5_K || dfmt == kQ6_K);
+    // Q5_K experts: the lane kernel's products, its mins scalar
+    const bool fmts = (gfmt == kQ4_K || gfmt == kQ5_K || gfmt == kQ6_K) &&
+                      (dfmt == kQ4_K || dfmt == kQ5_K || dfmt == kQ6_K);
     return p.M >= 1 && p.M <= kMoeTokenMajorMax && fmts && p.H == 2048 && p.I == 512 && nslots <= kMoe1MaxSlots &&
            p.E <= kMoeMaxExperts;
 }
@@ -788,6 +798,7 @@ hipError_t launch_moe(const MoeParams& p, int gfmt, int dfmt, hipStream_t s, hip
         if (ev) (void)hipEventRecord(ev[0], s);
         switch (gfmt) {
         case kQ4_K: return launch_moe1_g<kQ4_K>(p, dfmt, s, ev);
+        case kQ5_K: return launch_moe1_g<kQ5_K>(p, dfmt, s, ev);
         case kQ6_K: return launch_moe1_g<kQ6_K>(p, dfmt, s, ev);
         default: return hipErrorInvalidValue;
         }
@@ -878,6 +889,9 @@ hipError_t launch_moe_stage(const MoeParams& p, int gfmt, int dfmt, int stage, h
     if (gfmt == kQ6_K && dfmt == kQ4_K) return launch_moe1_stage<kQ6_K, kQ4_K>(p, stage, s);
     if (gfmt == kQ4_K && dfmt == kQ5_K) return launch_moe1_stage<kQ4_K, kQ5_K>(p, stage, s);
     if (gfmt == kQ6_K && dfmt == kQ5_K) return launch_moe1_stage<kQ6_K, kQ5_K>(p, stage, s);
+    if (gfmt == kQ5_K && dfmt == kQ4_K) return launch_moe1_stage<kQ5_K, kQ4_K>(p, stage, s);
+    if (gfmt == kQ5_K && dfmt == kQ5_K) return launch_moe1_stage<kQ5_K, kQ5_K>(p, stage, s);
+    if (gfmt == kQ5_K && dfmt == kQ6_K) return launch_moe1_stage<kQ5_K, kQ6_K>(p, stage, s);
     return hipErrorNotSupported;
 }
 

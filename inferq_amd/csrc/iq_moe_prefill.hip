@@ -334,8 +334,8 @@ __global__ __launch_bounds__(256) void k_mp_mm(MoeParams p) {
     // of a lane is then row 4 (q & 1) + r (every lane group), else row
     // 16 (r / 4) + 4 q + r % 4
     float v[4 * kMpRT];
-    // uniform per workgroup; Q5_K (down products only) has no pair-lane form
-    // and takes the 16-row tile for every chunk
+    // uniform per workgroup; Q5_K has no pair-lane form and takes the
+    // 16-row tile for every chunk
     const bool pk = FMT != kQ5_K && rows <= 8;
     if (pk) {
         if constexpr (FMT != kQ5_K) {
@@ -720,9 +720,9 @@ int moep_max_chunks(int64_t M, int64_t K, int64_t E, int rows) {
 }
 
 bool moep_supported(const MoeParams& p, int gfmt, int dfmt) {
-    const bool kq = (gfmt == kQ4_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ5_K || dfmt == kQ6_K);
+    const bool kq = (gfmt == kQ4_K || gfmt == kQ5_K || gfmt == kQ6_K) && (dfmt == kQ4_K || dfmt == kQ5_K || dfmt == kQ6_K);
     auto al = [](const void* q, uintptr_t a) { return q == nullptr || ((uintptr_t)q & (a - 1)) == 0; };
-    const uintptr_t ga = gfmt == kQ4_K ? 16 : 4, da = dfmt == kQ6_K ? 4 : 16;
+    const uintptr_t ga = gfmt == kQ6_K ? 4 : 16, da = dfmt == kQ6_K ? 4 : 16;
     const bool aligned = al(p.gate, ga) && al(p.up, ga) && al(p.sgate_w, ga) && al(p.sup_w, ga) && al(p.down, da) &&
                          al(p.sdown_w, da) && al(p.out, 16) &&
                          al(p.residual, 16);  // k_mp_combine moves four floats at a time
@@ -740,6 +740,9 @@ hipError_t launch_moe_prefill(const MoeParams& p, int gfmt, int dfmt, hipStream_
     if (gfmt == kQ6_K && dfmt == kQ4_K) return launch_p<kQ6_K, kQ4_K>(p, s, ev);
     if (gfmt == kQ4_K && dfmt == kQ5_K) return launch_p<kQ4_K, kQ5_K>(p, s, ev);
     if (gfmt == kQ6_K && dfmt == kQ5_K) return launch_p<kQ6_K, kQ5_K>(p, s, ev);
+    if (gfmt == kQ5_K && dfmt == kQ4_K) return launch_p<kQ5_K, kQ4_K>(p, s, ev);
+    if (gfmt == kQ5_K && dfmt == kQ5_K) return launch_p<kQ5_K, kQ5_K>(p, s, ev);
+    if (gfmt == kQ5_K && dfmt == kQ6_K) return launch_p<kQ5_K, kQ6_K>(p, s, ev);
     return hipErrorNotSupported;
 }
 

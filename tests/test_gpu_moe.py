@@ -508,22 +508,28 @@ def test_reference_prefill_pass_512_tokens_top10(gpu, oracle, wide_router_layer)
     assert_bitexact(got, halves, "512-token call vs two 256-token calls")
 
 
-@pytest.fixture(scope="module")
-def q5_down_layer():
-    """Config-2 shaped layer with Q5_K down experts (hidden 2048, 256
-    experts, top-8, a shared expert in the same formats)."""
-    return S.random_moe_layer(2048, 512, 256, Q4, S.Q5_K, np.random.default_rng(5150), shared=True)
+Q5_LAYERS = {}
 
 
+def _q5_layer(formats):
+    """Config-2 shaped layers with Q5_K experts (hidden 2048, 256 experts,
+    top-8, a shared expert in the same formats), built once per formats."""
+    if formats not in Q5_LAYERS:
+        Q5_LAYERS[formats] = S.random_moe_layer(2048, 512, 256, formats[0], formats[1],
+                                                np.random.default_rng(5150 + sum(formats)), shared=True)
+    return Q5_LAYERS[formats]
+
+
+@pytest.mark.parametrize("formats", [(Q4, S.Q5_K), (S.Q5_K, S.Q5_K), (S.Q5_K, Q6)], ids=["q4q5", "q5q5", "q5q6"])
 @pytest.mark.parametrize("m", [1, 12, 16, 33, 256])
-def test_q5k_down_experts_on_the_fast_paths(gpu, oracle, q5_down_layer, m):
-    """Q5_K down experts run on the token-major kernels (up to 32 tokens:
-    the lane kernel's products and mins scalar; from 12 tokens with the
-    routing launch, from 16 with the SwiGLU rows quantised once) and on the
-    grouped MFMA path (16-row tiles with three weight streams): routes
+def test_q5k_experts_on_the_fast_paths(gpu, oracle, formats, m):
+    """Q5_K gate/up or down experts run on the token-major kernels (up to 32
+    tokens: the lane kernel's products and mins scalar; from 12 tokens with
+    the routing launch, from 16 with the SwiGLU rows quantised once) and on
+    the grouped MFMA path (16-row tiles with three weight streams): routes
     equal the oracle's, outputs within 1e-4 of it, every token bitwise the
     one-token call."""
-    layer = q5_down_layer
+    layer = _q5_layer(formats)
     moe, _ = _device_layer(layer, 8, gpu)
     rng = np.random.default_rng(700 + m)
     x = S.normal((m, 2048), rng)
@@ -534,8 +540,8 @@ def test_q5k_down_experts_on_the_fast_paths(gpu, oracle, q5_down_layer, m):
     assert [r.experts for r in out.routes] == ref_e.tolist(), f"routes m={m}"
     got = out.hidden.cpu().numpy()
     for r in range(m):
-        assert_close_normwise(got[r], ref[r], 1e-4, f"Q5_K down m={m} row {r}")
+        assert_close_normwise(got[r], ref[r], 1e-4, f"Q5_K experts {formats} m={m} row {r}")
     if m > 1:
         idx = sorted({0, m // 2, m - 1})
         singles = np.concatenate([moe.forward(xt[i:i + 1], lt[i:i + 1]).hidden.cpu().numpy() for i in idx])
-        assert_bitexact(got[idx], singles, f"Q5_K down m={m} vs one-token calls")
+        assert_bitexact(got[idx], singles, f"Q5_K experts {formats} m={m} vs one-token calls")
