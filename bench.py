@@ -528,7 +528,43 @@ def secondary(args, hip, stream, device, layers, cpu=None, chk=None):
             "attention q/gate [8192x2048] + k, v [512x2048] + o [2048x4096]", "Q4_K", 11264, 2048, pbytes, m, t,
             "gpu:auto", moved=pbytes + m * 4 * sum(n + k for _, n, k in shapes), **kw)
     del proj, raw
+    # Q5_K: the attention output [2048 x 4096] of the reference's Q4_K_M
+    # files (src/gguf.rs:588-593) at decode, verify and prefill widths
+    extra.update(q5k_lines(hip, device, cpu))
     return extra
+
+
+def q5k_lines(hip, device, cpu=None):
+    """Q5_K o [2048 x 4096] at 1, 8 and 256 rows, rotated over copies beyond
+    the MALL, checked bitwise against the oracle."""
+    import torch
+
+    from inferq_amd import qgemm, synth
+
+    n, k = 2048, 4096
+    bpm = n * k // 256 * 176
+    copies = -(-MIN_STREAM_BYTES // bpm)
+    raw = [synth.random_matrix_device(synth.Q5_K, n, k, device, 900 + c) for c in range(copies)]
+    mats = [qgemm.QuantizedMatrix.view(r, synth.Q5_K, n, k) for r in raw]
+    wh = raw[0].cpu().numpy() if cpu is not None else None
+    res = {}
+    for m in (1, 8, 256):
+        x = torch.randn(m, k, device=device)
+        y = torch.empty(m, n, device=device)
+        t = time_graph(lambda i: mats[i % copies].forward_into(x, y), 50, hip)
+        kw = {}
+        if cpu is not None:
+            got = mats[0].forward(x).cpu().numpy()
+            xh = x.cpu().numpy()
+            ref = cpu.matmul(synth.Q5_K, wh, n, k, xh)
+            kw = dict(diff=max_abs_diff(got, ref), rel=normwise(got, ref), bitexact=bit_fraction(got, ref),
+                      cpu=cpu.time_matmul(synth.Q5_K, wh, n, k, xh))
+        line = measurement("q5k [2048x4096]", "Q5_K", n, k, bpm, m, t, "gpu:auto", moved=bpm + m * 4 * (n + k), **kw)
+        if m == 256:
+            line["TOPS"] = round(2 * m * n * k / (t["median_ms"] * 1e-3) / 1e12, 1)
+        res[f"q5k_2048x4096_m{m}"] = line
+    del mats, raw
+    return res
 
 
 def lm_head_lines(args, hip, device, cpu=None):
