@@ -713,7 +713,9 @@ hipError_t launch_moe1_g(const MoeParams& p, int dfmt, hipStream_t s, hipEvent_t
 // Grid (E, ceil(M / TT)), one wave per workgroup: expert e = blockIdx.x
 // against tokens blockIdx.y * TT ..; each lane keeps one partial sum per
 // token over h = lane + 64 j (the router row is read once per TT tokens).
-template <int TT>
+// U values per lane are loaded before any is summed (one token: U = 32, the
+// whole 2048-wide row in one round trip instead of four), in the same order.
+template <int TT, int U>
 __global__ __launch_bounds__(64) void k_moe_router(MoeParams p) {
     const int lane = threadIdx.x;
     const int e = blockIdx.x, t0 = blockIdx.y * TT;
@@ -724,19 +726,19 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeParams p) {
 #pragma unroll
     for (int i = 0; i < TT; i++) part[i] = 0.f;
     int64_t h = lane;
-    for (; h + 64 * 7 < H; h += 64 * 8) {
-        float rv[8];
+    for (; h + 64 * (U - 1) < H; h += 64 * U) {
+        float rv[U];
 #pragma unroll
-        for (int j = 0; j < 8; j++) rv[j] = r[h + 64 * j];
+        for (int j = 0; j < U; j++) rv[j] = r[h + 64 * j];
 #pragma unroll
         for (int i = 0; i < TT; i++) {
             if (i < nt) {
                 const float* xr = p.x + (int64_t)(t0 + i) * H + h;
-                float xv[8];
+                float xv[U];
 #pragma unroll
-                for (int j = 0; j < 8; j++) xv[j] = xr[64 * j];
+                for (int j = 0; j < U; j++) xv[j] = xr[64 * j];
 #pragma unroll
-                for (int j = 0; j < 8; j++) part[i] = part[i] + xv[j] * rv[j];
+                for (int j = 0; j < U; j++) part[i] = part[i] + xv[j] * rv[j];
             }
         }
     }
@@ -876,8 +878,8 @@ hipError_t launch_moe_shared_combine(const float* x, const float* selector, cons
 
 hipError_t launch_moe_router(const MoeParams& p, hipStream_t s) {
     if (!p.router || !p.logits_ws || p.M < 1) return hipErrorInvalidValue;
-    if (p.M <= 2) hipLaunchKernelGGL((k_moe_router<1>), dim3((unsigned)p.E, (unsigned)p.M), dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((k_moe_router<8>), dim3((unsigned)p.E, (unsigned)((p.M + 7) / 8)), dim3(64), 0, s, p);
+    if (p.M <= 2) hipLaunchKernelGGL((k_moe_router<1, 32>), dim3((unsigned)p.E, (unsigned)p.M), dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((k_moe_router<8, 8>), dim3((unsigned)p.E, (unsigned)((p.M + 7) / 8)), dim3(64), 0, s, p);
     return hipGetLastError();
 }
 
