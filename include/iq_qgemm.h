@@ -19,12 +19,13 @@
  *     reference's CPU kernels for the same inputs, on every entry except
  *     iq_matmul_via(..., IQ_PATH_PREFILL_TILES, ...) and MoE handles set to
  *     IQ_PATH_PREFILL_TILES (iq_moe_set_path), which a caller must request
- *     explicitly (their f32 order differs; within 1e-4).  Three f32
+ *     explicitly (their f32 order differs; within 1e-4).  Four f32
  *     orders follow a published or fixed order that the reference's own
  *     code (candle's, absent here) could not be checked against, so they
  *     are bit-identical to this library's CPU restatement and within 1e-4
- *     of the reference: Q5_K products (ggml's vec_dot_q5_K_q8_K order), the
- *     router logits of iq_moe_forward_x, and the shared-expert selector dot.
+ *     of the reference: Q5_K products (ggml's vec_dot_q5_K_q8_K order),
+ *     F32 / BF16 matrix products, the router logits of iq_moe_forward_x,
+ *     and the shared-expert selector dot.
  *   - Workspaces: library-owned device memory grows on the first call that
  *     needs more and is never freed under a graph that may still use it.
  *     Growth is refused during graph capture; the *_reserve entries size a
@@ -43,9 +44,10 @@ extern "C" {
 
 /* GGML type ids as carried by GGUF (the reference's GgmlDType).  The
  * executable matrix dtypes are the reference's (QuantizedMatrix::new,
- * src/gguf.rs:305-317).  Q5_K runs on the lane kernel in ggml's published
- * vec_dot_q5_K_q8_K order (the reference hands it to candle's per-row
- * vec_dot, src/gguf.rs:593).  F32 and BF16 matrices, which the reference
+ * src/gguf.rs:305-317).  Q5_K products follow ggml's published
+ * vec_dot_q5_K_q8_K order on every kernel that takes them (the split-K
+ * GEMV, the exact MFMA tiles, the lane kernel; the reference hands Q5_K to
+ * candle's per-row vec_dot, src/gguf.rs:593).  F32 and BF16 matrices, which the reference
  * multiplies through candle's f32 matmul (no multi-row kernel,
  * src/gguf.rs:533-535, :599), take an f32 product in a fixed order of this
  * library's (the MoE router's: per lane over k = lane + 64 j, then a
