@@ -161,3 +161,44 @@ def test_corner_experts(gpu, oracle, formats, m):
     for r in range(min(m, 6) if m > 1 else 0):
         one = moe.forward(torch.from_numpy(x[r:r + 1]).to(gpu), torch.from_numpy(logits[r:r + 1]).to(gpu))
         assert_bitexact(got[r], one.hidden.cpu().numpy()[0], f"corner experts {formats} m={m} token {r} vs one-token call")
+
+
+@pytest.mark.parametrize("mode", ["ff", "80", "mix"])
+@pytest.mark.parametrize("dtype", [S.Q4_K, S.Q6_K, S.Q8_0], ids=["q4k", "q6k", "q80"])
+def test_corner_row_entries(gpu, oracle, dtype, mode):
+    """The per-row entries (q4k_q8k_row / q6k_q8k_row / q80_q80_row,
+    src/qgemm.rs:447-468) on a corner-byte row and corner activation rows,
+    bitwise to the oracle's restatement."""
+    cols = 2048
+    wrow = corner_matrix(dtype, 1, cols, mode, 41 + dtype)
+    for rows in (1, 6, 12):
+        x = corner_activations(rows, cols, rows)
+        q = np.stack([oracle.quantize_q80(r) if dtype == S.Q8_0 else oracle.quantize_q8k(r) for r in x])
+        block_major = np.ascontiguousarray(q.T)
+        got = Q.row_kernel(dtype, wrow, block_major, rows)
+        expected = oracle.row_kernel(dtype, wrow.view(oracle.BLOCK[dtype]), block_major, rows, impl="lanes")
+        assert_bitexact(got, expected, f"{S.NAMES[dtype]} row entry bytes {mode} rows={rows}")
+
+
+@pytest.mark.parametrize("dtype", FORMATS, ids=FMT_IDS)
+def test_corner_block_integers(gpu, oracle, dtype):
+    """The per-block lane integers (isum, and msum for Q4_K / Q5_K) of
+    corner-byte blocks against corner activations, exact."""
+    rows, cols = 16, 512
+    w = corner_matrix(dtype, rows, cols, "mix", 77 + dtype)
+    x = corner_activations(6, cols, 6)
+    mat = Q.QuantizedMatrix.upload(w, dtype, rows, cols)
+    y, isum, msum = mat.block_sums(torch.from_numpy(x).to(gpu))
+    isum = isum.cpu().numpy()
+    msum = msum.cpu().numpy() if msum is not None else None
+    nb = cols // S.BLOCK_ELEMS[dtype]
+    wb = w.view(oracle.BLOCK[dtype]).reshape(rows, nb)
+    for r in range(x.shape[0]):
+        q = oracle.quantize_q80(x[r]) if dtype == S.Q8_0 else oracle.quantize_q8k(x[r])
+        for n in range(rows):
+            for b in range(nb):
+                ei, em = oracle.block_lanes(dtype, wb[n, b], q[b])
+                assert np.array_equal(isum[r, n, b], ei), (r, n, b)
+                if em is not None:
+                    assert np.array_equal(msum[r, n, b], em), (r, n, b)
+    assert_bitexact(y.cpu().numpy(), oracle.matmul(dtype, w, rows, cols, x), "corner block_sums output")
