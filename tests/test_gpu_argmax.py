@@ -191,3 +191,27 @@ def test_verify_width_fused_selection_ties(gpu, dtype, period, reps, m):
     logits = mat.forward(x).cpu().numpy()
     assert all(ref_argmax(r) >= rows - period for r in logits)
     _check_selection(mat, x, f"fused selection ties, period {period}, m={m}")
+
+
+@pytest.mark.parametrize("dtype,reps", [(S.Q8_0, 4099), (S.Q6_K, 40960), (S.Q4_K, 65536)])
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_fused_selection_over_a_matrix_of_equal_logits(gpu, dtype, reps, m):
+    """Every quant and scale byte zero (d finite): every logit of a row is
+    zero (+0 or -0, which rank equal), so the last index of the matrix must
+    win in every input row, across every wave and workgroup of the fused
+    product and of the joining launch.  The K-quant matrices are past
+    64 MiB, as the LM head is."""
+    bb = S.BLOCK_BYTES[dtype]
+    nb = 2048 // S.BLOCK_ELEMS[dtype]
+    base = S.random_matrix_device(dtype, 1, 2048, gpu, 7300 + dtype).reshape(nb, bb)
+    lo, hi = {S.Q4_K: (0, 4), S.Q6_K: (208, 210), S.Q8_0: (0, 2)}[dtype]
+    zero = torch.zeros_like(base)
+    zero[:, lo:hi] = base[:, lo:hi]
+    rows = reps
+    t = zero.reshape(-1).repeat(rows)
+    mat = Q.QuantizedMatrix.view(t, dtype, rows, 2048)
+    x = torch.randn(m, 2048, device=gpu, generator=torch.Generator(device=gpu).manual_seed(m))
+    logits = mat.forward(x).cpu().numpy()
+    assert not np.any(logits)
+    assert [ref_argmax(r) for r in logits] == [rows - 1] * m
+    _check_selection(mat, x, f"equal logits {S.NAMES[dtype]} [{rows} x 2048] m={m}")
